@@ -1,0 +1,114 @@
+/*
+ * morphocore_amd — C ABI of the MI355X (gfx950) morphology kernels.
+ *
+ * This is the drop-in boundary for morphocore's csrc hot path. Each entry point replaces one
+ * device-level launcher of the reference extension (cited per function below; paths relative to the
+ * reference repository root) and keeps its argument meaning:
+ *   - tensors are dense row-major device pointers (NCHW), already contiguous;
+ *   - x is [B, Cin, H, W]; the structuring element is [Cout, Cw, KH, KW] with Cw == Cin, or Cw == 1
+ *     for the IDENTITY merge; with weight noise it is [B, Cout, Cw, KH, KW] and
+ *     weight_batch_stride = Cout * Cw * KH * KW (0 for a shared structuring element);
+ *   - outputs are [B, Cout, H, W]; packed indices are int32 (channel << 16) | (kh * KW + kw);
+ *   - op: 0 dilation, 1 erosion; merge: 0 MAX, 1 MIN, 2 ADD ("sum"), 3 AVERAGE ("mean"),
+ *     5 IDENTITY (4, SMOOTH, is not provided by this library); padding is resolved by the caller into
+ *     `replicate` (clamped edge pixel) or a `fill` value (ZERO: 0, CONSTANT: the value, GEODESIC:
+ *     -inf for dilation, +inf for erosion), as morpho_fill_value does
+ *     (morphocore/functional/csrc/cpp/morpho_padding_policy.hpp:22-33);
+ *   - `stream` is a hipStream_t (NULL: the null stream). Every call only enqueues work on it.
+ *
+ * Return value: 0 on success, MCA_ERR_INVALID for a rejected argument (the message mirrors the
+ * reference's TORCH_CHECK text), MCA_ERR_HIP for a HIP runtime error. mca_last_error() returns the
+ * calling thread's last message.
+ *
+ * Backward entry points take a caller-owned device workspace of at least the size the matching
+ * *_workspace_size function returns; its contents on entry are irrelevant.
+ */
+#ifndef MORPHOCORE_AMD_H
+#define MORPHOCORE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MCA_OK 0
+#define MCA_ERR_INVALID 1
+#define MCA_ERR_HIP 2
+
+/* Library version string ("0.13.1-mi355x"). No reference counterpart (morphocore/__init__.py:1
+ * holds the reference package's version). */
+const char* mca_version(void);
+
+/* Message of the calling thread's last failed call, "" if none. Stands in for the text of the
+ * c10::Error the reference's TORCH_CHECKs raise. */
+const char* mca_last_error(void);
+
+/* Dilation / erosion forward, every merge.
+ * Replaces morpho_forward_cuda<op, T> (morphocore/functional/csrc/cuda/morpho_op.cuh:16-17,
+ * morpho_op.cu:30-74). `indices` may be NULL; when given, merge must be MAX or MIN and
+ * KH * KW < 65536, Cin < 32768 (morpho_op.cu:40-41). */
+int mca_morpho_forward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                           int64_t weight_batch_stride, float* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+int mca_morpho_forward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
+                           int64_t weight_batch_stride, double* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+
+/* Workspace bytes mca_morpho_backward_* needs for this merge and geometry; has_indices says
+ * whether saved indices will be passed. No reference counterpart: the reference allocates its
+ * temporaries inside morpho_backward_cuda (morpho_op.cu:102-177) from torch's allocator. */
+size_t mca_morpho_backward_workspace_size_f32(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW);
+size_t mca_morpho_backward_workspace_size_f64(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW);
+
+/* Dilation / erosion backward: overwrites grad_input [B, Cin, H, W] and grad_weight [Cout, Cw, KH, KW]
+ * (summed over the batch when the structuring element is per batch element).
+ * Replaces morpho_backward_cuda<op, T> (morphocore/functional/csrc/cuda/morpho_op.cuh:21-24,
+ * morpho_op.cu:102-177). `indices` (MAX / MIN only) may be NULL, in which case the winners are
+ * recomputed. */
+int mca_morpho_backward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                            int64_t weight_batch_stride, const int32_t* indices, const float* grad_output, float* grad_input,
+                            float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
+                            int64_t weight_batch_stride, const int32_t* indices, const double* grad_output, double* grad_input,
+                            double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Smorph forward. `weight` is the blended structuring element w~ the Python layer builds
+ * (morphocore/functional/smorph.py:56-70); `alpha` holds one value per channel pair, index
+ * o * Cin + i ([Cout] for IDENTITY), as smorph_pair_alphas expands it
+ * (morphocore/functional/csrc/cpp/smorph_cpu_kernels.hxx:642-649).
+ * Replaces smorph_forward_cuda<T> (morphocore/functional/csrc/cuda/smorph.cuh:15-16, smorph.cu:32-61). */
+int mca_smorph_forward_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, int64_t B, int64_t Cin,
+                           int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+int mca_smorph_forward_f64(int merge, const double* input, const double* weight, const double* alpha, double* output, int64_t B,
+                           int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+
+/* Workspace bytes mca_smorph_backward_* needs. No reference counterpart (the reference allocates
+ * inside smorph_backward_cuda, smorph.cu:63-103). */
+size_t mca_smorph_backward_workspace_size_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                              int64_t KH, int64_t KW);
+size_t mca_smorph_backward_workspace_size_f64(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                              int64_t KH, int64_t KW);
+
+/* Smorph backward: overwrites grad_input, grad_weight (gradient of w~) and grad_alpha (one value per
+ * channel pair, like `alpha`). `output` is the forward's output (the MAX / MIN merge target).
+ * Replaces smorph_backward_cuda<T> (morphocore/functional/csrc/cuda/smorph.cuh:21-25, smorph.cu:63-103). */
+int mca_smorph_backward_f32(int merge, const float* input, const float* weight, const float* alpha, const float* output,
+                            const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha, int64_t B, int64_t Cin,
+                            int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
+                            size_t workspace_bytes, void* stream);
+int mca_smorph_backward_f64(int merge, const double* input, const double* weight, const double* alpha, const double* output,
+                            const double* grad_output, double* grad_input, double* grad_weight, double* grad_alpha, int64_t B,
+                            int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MORPHOCORE_AMD_H */

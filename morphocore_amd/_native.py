@@ -1,0 +1,137 @@
+"""ctypes binding of the C ABI in ``include/morphocore_amd.h`` (``libmorphocore_amd.so``).
+
+The library holds the gfx950 kernels; nothing here computes. Every call enqueues work on the
+current HIP stream of the tensors' device, which is what the reference's CUDA launchers do with
+``getCurrentCUDAStream()`` (reference: morphocore/functional/csrc/cuda/morpho_cuda_launch.cuh).
+A missing library is an error, never a fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmorphocore_amd.so")
+
+# Every symbol include/morphocore_amd.h declares.
+EXPORTS = (
+    "mca_version",
+    "mca_last_error",
+    "mca_morpho_forward_f32",
+    "mca_morpho_forward_f64",
+    "mca_morpho_backward_workspace_size_f32",
+    "mca_morpho_backward_workspace_size_f64",
+    "mca_morpho_backward_f32",
+    "mca_morpho_backward_f64",
+    "mca_smorph_forward_f32",
+    "mca_smorph_forward_f64",
+    "mca_smorph_backward_workspace_size_f32",
+    "mca_smorph_backward_workspace_size_f64",
+    "mca_smorph_backward_f32",
+    "mca_smorph_backward_f64",
+)
+
+_lib = None
+
+_I, _I64, _P, _SZ = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+_GEOM = [_I64] * 8
+
+
+def lib() -> ctypes.CDLL:
+    """Load the native library (once). Raises RuntimeError when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"morphocore_amd: native library {LIB_PATH} is not built; build it with "
+            "`make -C morphocore_amd/csrc` or `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    so = ctypes.CDLL(LIB_PATH)
+    so.mca_version.restype = ctypes.c_char_p
+    so.mca_version.argtypes = []
+    so.mca_last_error.restype = ctypes.c_char_p
+    so.mca_last_error.argtypes = []
+    for sfx, real in (("f32", ctypes.c_float), ("f64", ctypes.c_double)):
+        f = getattr(so, f"mca_morpho_forward_{sfx}")
+        f.argtypes = [_I, _I, _I, real, _P, _P, _I64, _P, _P] + _GEOM + [_P]
+        f.restype = _I
+        f = getattr(so, f"mca_morpho_backward_workspace_size_{sfx}")
+        f.argtypes = [_I, _I] + _GEOM
+        f.restype = _SZ
+        f = getattr(so, f"mca_morpho_backward_{sfx}")
+        f.argtypes = [_I, _I, _I, real, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+        f = getattr(so, f"mca_smorph_forward_{sfx}")
+        f.argtypes = [_I, _P, _P, _P, _P] + _GEOM + [_P]
+        f.restype = _I
+        f = getattr(so, f"mca_smorph_backward_workspace_size_{sfx}")
+        f.argtypes = [_I] + _GEOM
+        f.restype = _SZ
+        f = getattr(so, f"mca_smorph_backward_{sfx}")
+        f.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+    _lib = so
+    return so
+
+
+def version() -> str:
+    return lib().mca_version().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(lib().mca_last_error().decode())
+
+
+def _sfx(t: torch.Tensor) -> str:
+    if t.dtype == torch.float32:
+        return "f32"
+    if t.dtype == torch.float64:
+        return "f64"
+    raise RuntimeError(f"morphocore_amd supports float32 and float64 tensors, got {t.dtype}")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def morpho_forward(op, merge, replicate, fill, x, weight, weight_batch_stride, out, indices, geom):
+    """Enqueue the dilation / erosion forward (C ABI mca_morpho_forward_*)."""
+    f = getattr(lib(), f"mca_morpho_forward_{_sfx(x)}")
+    _check(f(op, merge, int(replicate), fill, _ptr(x), _ptr(weight), weight_batch_stride, _ptr(out), _ptr(indices), *geom, _stream(x)))
+
+
+def morpho_backward(op, merge, replicate, fill, x, weight, weight_batch_stride, indices, grad_out, grad_in, grad_w, geom):
+    """Enqueue the dilation / erosion backward (C ABI mca_morpho_backward_*), workspace from torch."""
+    so, sfx = lib(), _sfx(x)
+    nbytes = getattr(so, f"mca_morpho_backward_workspace_size_{sfx}")(merge, int(indices is not None), *geom)
+    ws = _workspace(nbytes, x.device)
+    f = getattr(so, f"mca_morpho_backward_{sfx}")
+    _check(f(op, merge, int(replicate), fill, _ptr(x), _ptr(weight), weight_batch_stride, _ptr(indices), _ptr(grad_out), _ptr(grad_in),
+             _ptr(grad_w), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def smorph_forward(merge, x, weight, alpha_pairs, out, geom):
+    """Enqueue the smorph forward (C ABI mca_smorph_forward_*)."""
+    f = getattr(lib(), f"mca_smorph_forward_{_sfx(x)}")
+    _check(f(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), *geom, _stream(x)))
+
+
+def smorph_backward(merge, x, weight, alpha_pairs, out, grad_out, grad_in, grad_w, grad_alpha, geom):
+    """Enqueue the smorph backward (C ABI mca_smorph_backward_*), workspace from torch."""
+    so, sfx = lib(), _sfx(x)
+    nbytes = getattr(so, f"mca_smorph_backward_workspace_size_{sfx}")(merge, *geom)
+    ws = _workspace(nbytes, x.device)
+    f = getattr(so, f"mca_smorph_backward_{sfx}")
+    _check(f(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w), _ptr(grad_alpha),
+             *geom, _ptr(ws), ws.numel(), _stream(x)))

@@ -1,0 +1,249 @@
+// C ABI of the morphocore_amd kernels: argument validation with the reference's messages, then the
+// asynchronous launchers of morpho.hip / smorph.hip. Declarations: include/morphocore_amd.h.
+#include "../../include/morphocore_amd.h"
+
+#include <string>
+
+#include "launch.hpp"
+
+namespace
+{
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg)
+{
+    g_last_error = msg;
+    return MCA_ERR_INVALID;
+}
+
+int hip_status(hipError_t err)
+{
+    if (err == hipSuccess) return MCA_OK;
+    g_last_error = std::string("HIP error: ") + hipGetErrorString(err);
+    return MCA_ERR_HIP;
+}
+
+bool fits_int(int64_t v) { return v >= 0 && v <= 0x7fffffff; }
+
+// Geometry checks shared by every entry point; fills `g`. Returns MCA_OK or an error.
+int make_geom(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t wbs,
+              mca::Geom& g)
+{
+    if (merge < 0 || merge > mca::MERGE_IDENTITY) return fail("Unknown merge mode " + std::to_string(merge));
+    if (merge == mca::MERGE_SMOOTH) return fail("Unsupported merge operation");
+    if (!fits_int(B) || !fits_int(Cin) || !fits_int(Cout) || !fits_int(Cw) || !fits_int(H) || !fits_int(W) || !fits_int(KH) || !fits_int(KW))
+        return fail("Tensor dimensions must be non negative and below 2^31");
+    if (KH < 1 || KW < 1) return fail("The structuring element must have at least one tap");
+    if (merge == mca::MERGE_IDENTITY)
+    {
+        if (Cout != Cin) return fail("Identity mode requires weight.shape[0] == input.shape[1]");
+        if (Cw != 1) return fail("Identity mode requires weight.shape[1] == 1");
+    }
+    else if (Cw != Cin)
+    {
+        return fail("Input channels must match weight input channels");
+    }
+    if (wbs < 0) return fail("weight_batch_stride must be non negative");
+    // Workgroup counts of the launches: tiles x channels x batch must fit a 1-D grid.
+    const int64_t tiles = ((W + mca::TILE_W - 1) / mca::TILE_W) * ((H + 15) / 16);
+    if (B * tiles * (Cout > Cin ? Cout : Cin) > 0x7fffffff) return fail("Problem too large for one launch");
+    g.B = (int)B;
+    g.Cin = (int)Cin;
+    g.Cout = (int)Cout;
+    g.Cw = (int)Cw;
+    g.H = (int)H;
+    g.W = (int)W;
+    g.KH = (int)KH;
+    g.KW = (int)KW;
+    g.wbs = wbs;
+    return MCA_OK;
+}
+
+int check_lds(size_t bytes)
+{
+    if (bytes > mca::LDS_LIMIT) return fail("Structuring element too large for the kernels' shared memory");
+    return MCA_OK;
+}
+
+template <typename T>
+int morpho_forward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, T* output,
+                        int32_t* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                        void* stream)
+{
+    mca::Geom g{};
+    if (op != mca::DILATION && op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(op));
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if (indices)
+    {
+        if (merge != mca::MERGE_MAX && merge != mca::MERGE_MIN) return fail("Indices are only saved for the max and min merges");
+        if (!(KH * KW < (1 << 16) && Cin < (1 << 15))) return fail("Structuring element or channel count too large to save indices");
+    }
+    if ((rc = check_lds(mca::morpho_forward_lds<T>(g))) != MCA_OK) return rc;
+    return hip_status(mca::morpho_forward<T>(op, merge, replicate != 0, fill, input, weight, output, indices, g, (hipStream_t)stream));
+}
+
+template <typename T>
+size_t morpho_workspace_impl(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                             int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return mca::morpho_backward_workspace<T>(merge, has_indices != 0, g);
+}
+
+template <typename T>
+int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, const int32_t* indices,
+                         const T* grad_output, T* grad_input, T* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                         int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    mca::Geom g{};
+    if (op != mca::DILATION && op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(op));
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if (indices && merge != mca::MERGE_MAX && merge != mca::MERGE_MIN) return fail("Indices are only saved for the max and min merges");
+    if ((merge == mca::MERGE_MAX || merge == mca::MERGE_MIN) && !(KH * KW < (1 << 16) && Cin < (1 << 15)))
+        return fail("Structuring element or channel count too large to save indices");
+    if ((rc = check_lds(mca::morpho_backward_lds<T>(merge, g))) != MCA_OK) return rc;
+    if (!indices && (merge == mca::MERGE_MAX || merge == mca::MERGE_MIN) && (rc = check_lds(mca::morpho_forward_lds<T>(g))) != MCA_OK)
+        return rc;
+    const size_t need = mca::morpho_backward_workspace<T>(merge, indices != nullptr, g);
+    if (workspace_bytes < need || (need > 0 && !workspace))
+        return fail("Workspace too small: " + std::to_string(workspace_bytes) + " bytes given, " + std::to_string(need) + " needed");
+    return hip_status(mca::morpho_backward<T>(op, merge, replicate != 0, fill, input, weight, indices, grad_output, grad_input, grad_weight,
+                                              g, workspace, workspace_bytes, (hipStream_t)stream));
+}
+
+template <typename T>
+int smorph_forward_impl(int merge, const T* input, const T* weight, const T* alpha, T* output, int64_t B, int64_t Cin, int64_t Cout,
+                        int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_lds(mca::smorph_lds<T>(merge, g, false))) != MCA_OK) return rc;
+    return hip_status(mca::smorph_forward<T>(merge, input, weight, alpha, output, g, (hipStream_t)stream));
+}
+
+template <typename T>
+size_t smorph_workspace_impl(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return mca::smorph_backward_workspace<T>(merge, g);
+}
+
+template <typename T>
+int smorph_backward_impl(int merge, const T* input, const T* weight, const T* alpha, const T* output, const T* grad_output, T* grad_input,
+                         T* grad_weight, T* grad_alpha, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                         int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_lds(mca::smorph_lds<T>(merge, g, true))) != MCA_OK) return rc;
+    const size_t need = mca::smorph_backward_workspace<T>(merge, g);
+    if (workspace_bytes < need || (need > 0 && !workspace))
+        return fail("Workspace too small: " + std::to_string(workspace_bytes) + " bytes given, " + std::to_string(need) + " needed");
+    return hip_status(mca::smorph_backward<T>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, g,
+                                              workspace, workspace_bytes, (hipStream_t)stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mca_version(void) { return "0.13.1-mi355x"; }
+
+const char* mca_last_error(void) { return g_last_error.c_str(); }
+
+int mca_morpho_forward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                           int64_t weight_batch_stride, float* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return morpho_forward_impl<float>(op, merge, replicate, fill, input, weight, weight_batch_stride, output, indices, B, Cin, Cout, Cw,
+                                      H, W, KH, KW, stream);
+}
+
+int mca_morpho_forward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
+                           int64_t weight_batch_stride, double* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return morpho_forward_impl<double>(op, merge, replicate, fill, input, weight, weight_batch_stride, output, indices, B, Cin, Cout,
+                                       Cw, H, W, KH, KW, stream);
+}
+
+size_t mca_morpho_backward_workspace_size_f32(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW)
+{
+    return morpho_workspace_impl<float>(merge, has_indices, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+size_t mca_morpho_backward_workspace_size_f64(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW)
+{
+    return morpho_workspace_impl<double>(merge, has_indices, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+int mca_morpho_backward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                            int64_t weight_batch_stride, const int32_t* indices, const float* grad_output, float* grad_input,
+                            float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return morpho_backward_impl<float>(op, merge, replicate, fill, input, weight, weight_batch_stride, indices, grad_output, grad_input,
+                                       grad_weight, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
+                            int64_t weight_batch_stride, const int32_t* indices, const double* grad_output, double* grad_input,
+                            double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return morpho_backward_impl<double>(op, merge, replicate, fill, input, weight, weight_batch_stride, indices, grad_output, grad_input,
+                                        grad_weight, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_smorph_forward_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, int64_t B, int64_t Cin,
+                           int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return smorph_forward_impl<float>(merge, input, weight, alpha, output, B, Cin, Cout, Cw, H, W, KH, KW, stream);
+}
+
+int mca_smorph_forward_f64(int merge, const double* input, const double* weight, const double* alpha, double* output, int64_t B,
+                           int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return smorph_forward_impl<double>(merge, input, weight, alpha, output, B, Cin, Cout, Cw, H, W, KH, KW, stream);
+}
+
+size_t mca_smorph_backward_workspace_size_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                              int64_t KH, int64_t KW)
+{
+    return smorph_workspace_impl<float>(merge, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+size_t mca_smorph_backward_workspace_size_f64(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                              int64_t KH, int64_t KW)
+{
+    return smorph_workspace_impl<double>(merge, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+int mca_smorph_backward_f32(int merge, const float* input, const float* weight, const float* alpha, const float* output,
+                            const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha, int64_t B, int64_t Cin,
+                            int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
+                            size_t workspace_bytes, void* stream)
+{
+    return smorph_backward_impl<float>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, B, Cin, Cout,
+                                       Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_smorph_backward_f64(int merge, const double* input, const double* weight, const double* alpha, const double* output,
+                            const double* grad_output, double* grad_input, double* grad_weight, double* grad_alpha, int64_t B,
+                            int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
+                            size_t workspace_bytes, void* stream)
+{
+    return smorph_backward_impl<double>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, B, Cin,
+                                        Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+// Host-side launchers of the HIP kernels (morpho.hip, smorph.hip), called by the C ABI (capi.cpp).
+// Arguments are assumed validated by the caller; every launch is asynchronous on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace mca
+{
+
+// Workspace bytes are rounded to this alignment for every sub-buffer.
+constexpr size_t WS_ALIGN = 256;
+
+inline size_t align_up(size_t v) { return (v + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
+
+// Rows of outputs each wave computes, per element size.
+template <typename T>
+constexpr int rows_per_wave()
+{
+    return sizeof(T) == 8 ? 4 : 8;
+}
+
+// Largest LDS allocation a launch may request (bytes).
+constexpr size_t LDS_LIMIT = 64 * 1024;
+
+template <typename T>
+hipError_t morpho_forward(int op, int merge, bool replicate, T fill, const T* x, const T* w, T* out, int32_t* indices, const Geom& g,
+                          hipStream_t stream);
+
+// Bytes of LDS the forward kernel needs; > LDS_LIMIT means the structuring element is too large.
+template <typename T>
+size_t morpho_forward_lds(const Geom& g);
+
+template <typename T>
+size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g);
+
+template <typename T>
+size_t morpho_backward_lds(int merge, const Geom& g);
+
+template <typename T>
+hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const int32_t* indices, const T* grad_out,
+                           T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+template <typename T>
+hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream);
+
+template <typename T>
+size_t smorph_lds(int merge, const Geom& g, bool backward);
+
+template <typename T>
+size_t smorph_backward_workspace(int merge, const Geom& g);
+
+template <typename T>
+hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, const T* out, const T* grad_out, T* grad_in, T* grad_w,
+                           T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// Shared helpers (morpho.hip).
+template <typename T>
+hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);
+
+template <typename T>
+hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, hipStream_t stream);
+
+}  // namespace mca

@@ -1,0 +1,395 @@
+"""Parity of the HIP kernels with the CPU oracle (oracle/), on the GPU.
+
+Forward values of every merge and the packed indices are compared bit for bit; gradients and smorph
+within the contract's tolerance (relative 1e-6 float32, 1e-12 float64, norm-wise: max |diff| over
+max |expected| per tensor). Inputs are seeded and sized so the oracle finishes in seconds; the
+reference's own test cases (odd shapes, even kernels, kernel larger than the image, every padding,
+ties) are re-expressed here.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import TOL, normwise_error, seeded
+
+pytestmark = pytest.mark.gpu
+
+MERGES = ["max", "min", "sum", "mean", "identity"]
+PADDINGS = ["zero", "geodesic", "constant", "replicate"]
+DTYPES = [torch.float32, torch.float64]
+
+
+def _mca():
+    import morphocore_amd
+    from morphocore_amd import _native
+    from morphocore_amd.functional import _autograd
+    return morphocore_amd, _native, _autograd
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _weight_shape(merge, cin, cout, kh, kw):
+    return (cin, 1, kh, kw) if merge == "identity" else (cout, cin, kh, kw)
+
+
+def kernel_forward(op, merge, padding, pv, x, w, save=False, sample_weight=None):
+    """One call of the C ABI forward on the GPU (kernel-facing weight)."""
+    _, native, A = _mca()
+    dev = torch.device("cuda")
+    xd = x.to(dev).contiguous()
+    wd = (w if sample_weight is None else sample_weight).to(dev).contiguous()
+    B, Cin, H, W = x.shape
+    Cout, Cw, KH, KW = w.shape
+    out = torch.empty((B, Cout, H, W), dtype=x.dtype, device=dev)
+    idx = torch.empty((B, Cout, H, W), dtype=torch.int32, device=dev) if save else None
+    wbs = Cout * Cw * KH * KW if sample_weight is not None else 0
+    native.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding] == O.REPLICATE, A.fill_value(op, O.PADDINGS[padding], pv), xd, wd, wbs,
+                          out, idx, (B, Cin, Cout, Cw, H, W, KH, KW))
+    torch.cuda.synchronize()
+    return _np(out), (None if idx is None else _np(idx))
+
+
+SHAPES = [
+    # B, Cin, Cout, H, W, KH, KW
+    (2, 3, 5, 19, 70, 3, 5),   # two column tiles, ragged rows
+    (1, 2, 2, 7, 9, 4, 2),     # even kernel sizes
+    (1, 1, 3, 3, 4, 5, 5),     # kernel larger than the image
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("padding", PADDINGS)
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+def test_forward_bit_exact(op, merge, padding, dtype):
+    for si, (B, Cin, Cout, H, W, KH, KW) in enumerate(SHAPES):
+        if merge == "identity":
+            Cout = Cin
+        x = seeded(10 + si, B, Cin, H, W, dtype=dtype, kind="randn")
+        w = seeded(20 + si, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="randn", scale=0.3)
+        save = merge in ("max", "min")
+        out, idx = kernel_forward(op, merge, padding, 0.25, x, w, save=save)
+        ref, ref_idx = O.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding], 0.25, x.numpy(), w.numpy(), save_indices=save)
+        assert np.array_equal(out, ref), f"shape {si}: forward differs"
+        assert np.array_equal(np.signbit(out), np.signbit(ref))
+        if save:
+            assert np.array_equal(idx, ref_idx), f"shape {si}: indices differ"
+
+
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+@pytest.mark.parametrize("merge", ["max", "min", "sum", "identity"])
+def test_forward_ties_and_signed_zeros(op, merge):
+    """Quantised inputs with a zero structuring element: every window ties; the first tap and the
+    first channel must win, and a zero result keeps the sign of the first zero tap."""
+    B, Cin, Cout, H, W, K = 2, 4, 3, 21, 66, 5
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(1, B, Cin, H, W, kind="quant")
+    x[:, :, ::3, ::2] = -0.0
+    x[:, 1:, 5:9, 10:30] = 0.0
+    w = torch.zeros(_weight_shape(merge, Cin, Cout, K, K))
+    w[..., 0, 0] = -0.0
+    for padding in PADDINGS:
+        save = merge in ("max", "min")
+        out, idx = kernel_forward(op, merge, padding, 0.0, x, w, save=save)
+        ref, ref_idx = O.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding], 0.0, x.numpy(), w.numpy(), save_indices=save)
+        assert np.array_equal(out, ref)
+        assert np.array_equal(np.signbit(out), np.signbit(ref)), padding
+        if save:
+            assert np.array_equal(idx, ref_idx), padding
+
+
+def _backward_case(op, merge, padding, dtype, x, w, g, save_indices=True, pv=0.5):
+    """Forward + backward through torch.ops.morphocore on the GPU vs the oracle."""
+    _mca()
+    dev = torch.device("cuda")
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    fn = torch.ops.morphocore.dilation if op == O.DILATION else torch.ops.morphocore.erosion
+    out = fn(xd, wd, O.MERGES[merge], O.PADDINGS[padding], pv, save_indices, 0.0)
+    out.backward(g.to(dev))
+    ref, ref_idx = O.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding], pv, x.numpy(), w.numpy(), save_indices=merge in ("max", "min"))
+    gx, gw = O.morpho_backward(op, O.MERGES[merge], O.PADDINGS[padding], pv, x.numpy(), w.numpy(), g.numpy(), indices=ref_idx)
+    return _np(out), ref, _np(xd.grad), gx, _np(wd.grad), gw
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("padding", ["geodesic", "replicate", "constant"])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+def test_backward_parity(op, merge, padding, dtype):
+    B, Cin, Cout, H, W, KH, KW = 2, 3, 4, 23, 69, 5, 3
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(3, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(4, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="randn", scale=0.2)
+    g = seeded(5, B, Cout, H, W, dtype=dtype, kind="randn")
+    out, ref, gx, rgx, gw, rgw = _backward_case(op, merge, padding, dtype, x, w, g)
+    assert np.array_equal(out, ref)
+    assert normwise_error(gx, rgx) <= TOL[dtype]
+    assert normwise_error(gw, rgw) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("save_indices", [True, False])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+def test_backward_exact_on_dyadic_inputs(op, merge, save_indices):
+    """Quantised inputs, zero structuring element, integer gradients: every sum is exact, so the
+    gradients must match bit for bit whatever the accumulation order."""
+    B, Cin, Cout, H, W, K = 2, 3, 4, 20, 70, 5
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(6, B, Cin, H, W, kind="quant")
+    w = torch.zeros(_weight_shape(merge, Cin, Cout, K, K))
+    g = seeded(7, B, Cout, H, W, kind="quant") * 16 - 8
+    # 'mean' scales by the rounded 1 / Cin, which makes its sums inexact: checked norm-wise.
+    out, ref, gx, rgx, gw, rgw = _backward_case(op, merge, "replicate", torch.float32, x, w, g, save_indices=save_indices)
+    assert np.array_equal(out, ref)
+    if merge == "mean":
+        assert normwise_error(gx, rgx) <= 1e-6 and normwise_error(gw, rgw) <= 1e-6
+    else:
+        assert np.array_equal(gx, rgx)
+        assert np.array_equal(gw, rgw)
+
+
+def test_backward_geodesic_minus_inf_weights():
+    """Dropped taps (-inf) with geodesic padding: windows that see only -inf route to tap 0, as the
+    strict-improvement scan leaves it (reference test_weight_dropout.py:107-139)."""
+    x = seeded(8, 1, 2, 9, 11, kind="randn")
+    w = seeded(9, 3, 2, 3, 3, kind="randn")
+    w[:, :, 0, :] = -float("inf")
+    w[0, 1] = -float("inf")
+    g = seeded(10, 1, 3, 9, 11, kind="randn")
+    for merge in ("max", "sum", "min"):
+        out, ref, gx, rgx, gw, rgw = _backward_case(O.DILATION, merge, "geodesic", torch.float32, x, w, g)
+        assert np.array_equal(out, ref)
+        assert normwise_error(gx, rgx) <= 1e-6
+        assert normwise_error(gw, rgw) <= 1e-6
+
+
+def test_noise_matches_per_sample_weights():
+    """Weight noise (morpho_op_wrap.hxx:55-64): the same draw, reproduced from the seed, fed to the
+    oracle as per-sample weights, gives the same output and gradients."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    B, Cin, Cout, H, W, K = 3, 2, 4, 17, 20, 3
+    x = seeded(11, B, Cin, H, W)
+    w = seeded(12, Cout, Cin, K, K, kind="randn", scale=0.1)
+    g = seeded(13, B, Cout, H, W, kind="randn")
+    for merge in ("max", "sum"):
+        xd = x.to(dev).requires_grad_(True)
+        wd = w.to(dev).requires_grad_(True)
+        torch.manual_seed(1234)
+        out = mca.functional.dilation(xd, wd, merge, "geodesic", training=True, noise_scale=0.05)
+        out.backward(g.to(dev))
+        torch.manual_seed(1234)
+        noise = (torch.rand((B, Cout, Cin, K, K), dtype=torch.float32, device=dev) * 2.0 - 1.0) * 0.05
+        sample = (wd.detach().unsqueeze(0) + noise).cpu().numpy()
+        ref, idx = O.morpho_forward(O.DILATION, O.MERGES[merge], O.GEODESIC, 0.0, x.numpy(), w.numpy(), save_indices=merge == "max",
+                                    sample_weight=sample)
+        gx, gw = O.morpho_backward(O.DILATION, O.MERGES[merge], O.GEODESIC, 0.0, x.numpy(), w.numpy(), g.numpy(), indices=idx,
+                                   sample_weight=sample)
+        assert np.array_equal(_np(out), ref)
+        assert normwise_error(_np(xd.grad), gx) <= 1e-6
+        assert normwise_error(_np(wd.grad), gw) <= 1e-6
+
+
+def test_ranks_2d_3d():
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    x = seeded(14, 13, 4).to(dev)
+    w = seeded(15, 5, 5, kind="randn").to(dev)
+    out = mca.functional.dilation(x, w, "max", "geodesic")
+    assert out.shape == (13, 4)
+    ref, _ = O.morpho_forward(O.DILATION, O.MAX, O.GEODESIC, 0.0, _np(x)[None, None], _np(w)[None, None])
+    assert np.array_equal(_np(out), ref[0, 0])
+    x3 = seeded(16, 2, 10, 12).to(dev)
+    w4 = seeded(17, 3, 2, 3, 3, kind="randn").to(dev)
+    out3 = mca.functional.erosion(x3, w4, "sum")
+    assert out3.shape == (3, 10, 12)
+
+
+def test_functional_erosion_flips_weight():
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    x = seeded(18, 2, 3, 15, 16)
+    w = seeded(19, 4, 3, 3, 5, kind="randn", scale=0.1)
+    out = mca.functional.erosion(x.to(dev), w.to(dev), "min", "zero")
+    ref, _ = O.morpho_forward(O.EROSION, O.MIN, O.ZERO, 0.0, x.numpy(), np.ascontiguousarray(w.flip((-2, -1)).numpy()))
+    assert np.array_equal(_np(out), ref)
+
+
+# ------------------------------------------------------------------------------------------------
+# Smorph
+# ------------------------------------------------------------------------------------------------
+
+def _smorph_case(merge, x, w_tilde, alpha, g):
+    _mca()
+    dev = torch.device("cuda")
+    xd = x.to(dev).requires_grad_(True)
+    wd = w_tilde.to(dev).requires_grad_(True)
+    ad = alpha.to(dev).requires_grad_(True)
+    out = torch.ops.morphocore.smorph(xd, wd, ad, O.MERGES[merge])
+    out.backward(g.to(dev))
+    ref = O.smorph_forward(O.MERGES[merge], x.numpy(), w_tilde.numpy(), alpha.numpy())
+    gx, gw, ga = O.smorph_backward(O.MERGES[merge], x.numpy(), w_tilde.numpy(), alpha.numpy(), g.numpy())
+    return (_np(out), ref), (_np(xd.grad), gx), (_np(wd.grad), gw), (_np(ad.grad), ga)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("a", [-20.0, -1.0, 0.0, 1.0, 20.0])
+@pytest.mark.parametrize("merge", MERGES)
+def test_smorph_parity(merge, a, dtype):
+    B, Cin, Cout, H, W, K = 2, 3, 4, 18, 67, 5
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(21, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(22, *_weight_shape(merge, Cin, Cout, K, K), dtype=dtype, kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    alpha = (torch.full((pairs,), a, dtype=dtype) + seeded(23, pairs, dtype=dtype, kind="randn", scale=0.1 if a != 0 else 0.0))
+    alpha = alpha.reshape((Cout,) if merge == "identity" else (Cout, Cin))
+    g = seeded(24, B, Cout, H, W, dtype=dtype, kind="randn")
+    for actual, expected in _smorph_case(merge, x, w, alpha, g):
+        assert normwise_error(actual, expected) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("merge", ["sum", "max"])
+def test_smorph_shared_alpha(merge):
+    x = seeded(25, 1, 2, 11, 13, kind="randn")
+    w = seeded(26, 3, 2, 3, 3, kind="randn", scale=0.1)
+    alpha = torch.tensor(2.5)
+    g = seeded(27, 1, 3, 11, 13, kind="randn")
+    for actual, expected in _smorph_case(merge, x, w, alpha, g):
+        assert normwise_error(actual, expected) <= 1e-6
+
+
+def test_smorph_functional_matches_blend():
+    """functional.smorph blends w with its flip by tanh(alpha) before the operator (smorph.py:56-70)."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    x = seeded(28, 2, 3, 16, 16, kind="randn")
+    w = seeded(29, 4, 3, 5, 5, kind="randn", scale=0.1)
+    alpha = seeded(30, 4, 3, kind="randn")
+    out = mca.functional.smorph(x.to(dev), w.to(dev), alpha.to(dev), channel_merge_mode="mean")
+    wt = O.smorph_w_tilde(w.numpy(), alpha.numpy(), "mean")
+    ref = O.smorph_forward(O.AVERAGE, x.numpy(), wt, alpha.numpy())
+    assert normwise_error(_np(out), ref) <= 1e-6
+
+
+# ------------------------------------------------------------------------------------------------
+# The BASELINE configurations, at sizes the oracle finishes in seconds
+# ------------------------------------------------------------------------------------------------
+
+def test_config1_dilation_max_full_size():
+    """dilation fwd+bwd fp32, merge 'max', x (4,3,64,64) ~U[0,1), w (16,3,3,3) ~N(0,0.1), seed 0."""
+    torch.manual_seed(0)
+    x = torch.rand(4, 3, 64, 64)
+    w = torch.randn(16, 3, 3, 3) * 0.1
+    g = seeded(1, 4, 16, 64, 64, kind="randn")
+    out, ref, gx, rgx, gw, rgw = _backward_case(O.DILATION, "max", "replicate", torch.float32, x, w, g)
+    assert np.array_equal(out, ref)
+    assert normwise_error(gx, rgx) <= 1e-6 and normwise_error(gw, rgw) <= 1e-6
+    o2, idx = kernel_forward(O.DILATION, "max", "replicate", 0.0, x, w, save=True)
+    _, ridx = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x.numpy(), w.numpy(), save_indices=True)
+    assert np.array_equal(idx, ridx)
+
+
+@pytest.mark.parametrize("variant", ["random", "quantised"])
+def test_config2_erosion_sum(variant):
+    """configs[1] at B=2: erosion fp32, merge 'sum', (2,32,128,128), w (32,32,5,5) ~N(0,0.05); the
+    quantised variant has x in {0..15}/16 and w = 0."""
+    x = seeded(0, 2, 32, 128, 128, kind="quant" if variant == "quantised" else "rand")
+    w = torch.zeros(32, 32, 5, 5) if variant == "quantised" else seeded(1, 32, 32, 5, 5, kind="randn", scale=0.05)
+    g = seeded(2, 2, 32, 128, 128, kind="quant") * 16 - 8 if variant == "quantised" else seeded(2, 2, 32, 128, 128, kind="randn")
+    out, ref, gx, rgx, gw, rgw = _backward_case(O.EROSION, "sum", "replicate", torch.float32, x, w, g)
+    assert np.array_equal(out, ref)
+    if variant == "quantised":
+        assert np.array_equal(gx, rgx) and np.array_equal(gw, rgw)
+    else:
+        assert normwise_error(gx, rgx) <= 1e-6 and normwise_error(gw, rgw) <= 1e-6
+
+
+@pytest.mark.parametrize("a", [-20.0, -1.0, 0.0, 1.0, 20.0])
+def test_config3_smorph_mean(a):
+    """configs[2] at (1,16,64,64), w (16,16,7,7) ~N(0,0.1), alpha = full(a)."""
+    x = seeded(0, 1, 16, 64, 64, kind="randn")
+    w = seeded(1, 16, 16, 7, 7, kind="randn", scale=0.1)
+    alpha = torch.full((16, 16), a)
+    wt = torch.from_numpy(O.smorph_w_tilde(w.numpy(), alpha.numpy(), "mean"))
+    g = seeded(2, 1, 16, 64, 64, kind="randn")
+    for actual, expected in _smorph_case("mean", x, wt, alpha, g):
+        assert normwise_error(actual, expected) <= 1e-6
+
+
+def test_config4_dilation_identity_f64():
+    """configs[3] at (2,16,56,56) float64, identity, w (16,1,3,3) ~N(0,0.1); the literal
+    (C,C,3,3) weight is rejected as by the reference."""
+    x = seeded(0, 2, 16, 56, 56, dtype=torch.float64, low=-1.0, scale=2.0)
+    w = seeded(1, 16, 1, 3, 3, dtype=torch.float64, kind="randn", scale=0.1)
+    g = seeded(2, 2, 16, 56, 56, dtype=torch.float64, kind="randn")
+    out, ref, gx, rgx, gw, rgw = _backward_case(O.DILATION, "identity", "replicate", torch.float64, x, w, g)
+    assert np.array_equal(out, ref)
+    assert normwise_error(gx, rgx) <= 1e-12 and normwise_error(gw, rgw) <= 1e-12
+    with pytest.raises(RuntimeError, match="Identity mode requires weight.shape\\[1\\] == 1"):
+        torch.ops.morphocore.dilation(x.cuda(), torch.zeros(16, 16, 3, 3, dtype=torch.float64, device="cuda"), 5, 3, 0.0, True, 0.0)
+
+
+def test_config5_stack_reduced():
+    """configs[4] at (1,4,40,40), K=11: dilation(max) -> smorph(alpha=5, sum) -> erosion(min), fwd+bwd."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    C, K = 4, 11
+    x = seeded(0, 1, C, 40, 40)
+    ws = [seeded(1 + l, C, C, K, K, kind="randn", scale=0.05) for l in range(3)]
+    alpha = torch.full((C, C), 5.0)
+    g = seeded(9, 1, C, 40, 40, kind="randn")
+    # GPU, through the public API.
+    xd = x.to(dev).requires_grad_(True)
+    wd = [w.to(dev).requires_grad_(True) for w in ws]
+    ad = alpha.to(dev).requires_grad_(True)
+    y1 = mca.functional.dilation(xd, wd[0], "max", "replicate")
+    y2 = mca.functional.smorph(y1, wd[1], ad, channel_merge_mode="sum")
+    y3 = mca.functional.erosion(y2, wd[2], "min", "replicate")
+    y3.backward(g.to(dev))
+    # Oracle, layer by layer, with the GPU's own intermediate activations as inputs so that each
+    # layer is checked at its own tolerance.
+    r1, i1 = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x.numpy(), ws[0].numpy(), save_indices=True)
+    assert np.array_equal(_np(y1), r1)
+    wt = O.smorph_w_tilde(ws[1].numpy(), alpha.numpy(), "sum")
+    r2 = O.smorph_forward(O.ADD, _np(y1), wt, alpha.numpy())
+    assert normwise_error(_np(y2), r2) <= 1e-6
+    w3f = np.ascontiguousarray(ws[2].flip((-2, -1)).numpy())
+    r3, i3 = O.morpho_forward(O.EROSION, O.MIN, O.REPLICATE, 0.0, _np(y2), w3f, save_indices=True)
+    assert np.array_equal(_np(y3), r3)
+    gy2, gw3f = O.morpho_backward(O.EROSION, O.MIN, O.REPLICATE, 0.0, _np(y2), w3f, g.numpy(), indices=i3)
+    assert normwise_error(_np(wd[2].grad), gw3f[:, :, ::-1, ::-1]) <= 1e-6
+    assert np.isfinite(_np(xd.grad)).all() and np.isfinite(_np(wd[0].grad)).all() and np.isfinite(_np(ad.grad)).all()
+
+
+# ------------------------------------------------------------------------------------------------
+# Full BASELINE sizes: size-independent properties
+# ------------------------------------------------------------------------------------------------
+
+def test_config2_full_size_properties():
+    """configs[1] at full size (16,32,128,128): batch element 0 matches the oracle exactly; with an
+    all-ones output gradient, every (o, i) pair routes each pixel's gradient to exactly one tap, so
+    each grad_weight[o, i] sums to -B*H*W (erosion sign), exactly."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    x = seeded(0, 16, 32, 128, 128)
+    w = seeded(1, 32, 32, 5, 5, kind="randn", scale=0.05)
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    out = mca.functional.erosion(xd, wd, "sum", "replicate")
+    out.backward(torch.ones_like(out))
+    ref, _ = O.morpho_forward(O.EROSION, O.ADD, O.REPLICATE, 0.0, x[:1].numpy(), np.ascontiguousarray(w.flip((-2, -1)).numpy()))
+    assert np.array_equal(_np(out[:1]), ref)
+    row_sums = wd.grad.double().sum(dim=(2, 3))
+    assert torch.equal(row_sums, torch.full_like(row_sums, -16 * 128 * 128))
+    # Every input pixel's gradient counts the (o, pixel) pairs that picked it: a non-negative integer.
+    gx = xd.grad
+    assert torch.equal(gx, gx.round()) and bool((gx >= 0).all())
+    assert float(gx.double().sum()) <= 16 * 32 * 32 * 128 * 128

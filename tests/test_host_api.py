@@ -1,0 +1,94 @@
+"""Host-side behaviour of the Python API that needs no GPU: the string enums, the operator schemas,
+the argument checks and their messages (the reference's, see morpho_op_wrap.hxx, bindings.cpp,
+reshaper.cpp, smorph_cpu_kernels.hxx), the module parameters, and that a CPU tensor is refused
+rather than computed on a fallback path."""
+import pytest
+import torch
+
+import morphocore_amd as mca
+from morphocore_amd.functional import MorphoMerge, MorphoPadding, str_to_merge, str_to_padding
+
+ops = torch.ops.morphocore
+
+
+def test_enum_values_match_reference():
+    assert [int(m) for m in (MorphoMerge.MAX, MorphoMerge.MIN, MorphoMerge.ADD, MorphoMerge.AVERAGE, MorphoMerge.SMOOTH,
+                             MorphoMerge.IDENTITY)] == [0, 1, 2, 3, 4, 5]
+    assert [int(p) for p in (MorphoPadding.ZERO, MorphoPadding.GEODESIC, MorphoPadding.CONSTANT, MorphoPadding.REPLICATE)] == [0, 1, 2, 3]
+    assert str_to_merge("sum") == MorphoMerge.ADD and str_to_merge("mean") == MorphoMerge.AVERAGE
+    assert str_to_padding("replicate") == MorphoPadding.REPLICATE
+
+
+def test_unknown_strings_raise_value_error():
+    x, w = torch.randn(1, 1, 8, 8), torch.zeros(1, 1, 3, 3)
+    with pytest.raises(ValueError, match="Unknown padding mode"):
+        mca.functional.dilation(x, w, padding_mode="reflect")
+    with pytest.raises(ValueError, match="Unknown merge mode"):
+        mca.functional.erosion(x, w, channel_merge_mode="average")
+
+
+def test_schemas():
+    assert "float padding_value=0., bool save_indices=True, float noise_scale=0." in str(ops.dilation.default._schema)
+    assert str(ops.smorph.default._schema).startswith("morphocore::smorph(Tensor input, Tensor weight, Tensor alpha, int merge)")
+    assert "Tensor beta" in str(ops.smorph_scm.default._schema)
+
+
+def test_operator_argument_errors():
+    x, w = torch.randn(2, 3, 8, 8), torch.zeros(4, 3, 3, 3)
+    with pytest.raises(RuntimeError, match="Unknown merge mode 9"):
+        ops.dilation(x, w, 9, 0)
+    with pytest.raises(RuntimeError, match="Unknown padding mode 7"):
+        ops.erosion(x, w, 0, 7)
+    with pytest.raises(RuntimeError, match="Unsupported merge operation"):
+        ops.dilation(x, w, 4, 0)
+    with pytest.raises(RuntimeError, match="noise_scale must be non negative"):
+        ops.dilation(x, w, 0, 0, 0.0, True, -0.1)
+    with pytest.raises(RuntimeError, match="Input channels must match weight input channels"):
+        ops.dilation(x, torch.zeros(4, 2, 3, 3), 2, 0)
+    with pytest.raises(RuntimeError, match="Identity mode requires weight.shape\\[0\\] == input.shape\\[1\\]"):
+        ops.dilation(x, torch.zeros(4, 1, 3, 3), 5, 0)
+    with pytest.raises(RuntimeError, match="Identity mode requires weight.shape\\[1\\] == 1"):
+        ops.dilation(x, torch.zeros(3, 3, 3, 3), 5, 0)
+    with pytest.raises(RuntimeError, match="Invalid input tensor"):
+        ops.dilation(torch.zeros(1, 1, 1, 2, 2), w, 0, 0)
+    with pytest.raises(RuntimeError, match="Invalid weight tensor dimensions"):
+        ops.dilation(x, torch.zeros(3, 3, 3), 0, 0)
+
+
+def test_smorph_argument_errors():
+    x = torch.randn(2, 3, 8, 8)
+    w = torch.zeros(4, 3, 3, 3)
+    with pytest.raises(RuntimeError, match="Alpha must have one value, or shape \\[out_channels, in_channels\\]"):
+        ops.smorph(x, w, torch.zeros(5), 2)
+    with pytest.raises(RuntimeError, match="Alpha must have one value, or shape \\[channels\\]"):
+        ops.smorph(x, torch.zeros(3, 1, 3, 3), torch.zeros(4), 5)
+    with pytest.raises(RuntimeError, match="Identity mode requires weight.shape\\[1\\] == 1, got 3"):
+        ops.smorph(x, torch.zeros(3, 3, 3, 3), torch.zeros(3), 5)
+    with pytest.raises(RuntimeError, match="Unsupported merge operation for smorph"):
+        ops.smorph(x, w, torch.zeros(4, 3), 4)
+    with pytest.raises(NotImplementedError, match="smorph_scm"):
+        mca.functional.smorph(x, w, torch.zeros(4, 3), beta=torch.zeros(4, 3))
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    x, w = torch.randn(1, 2, 8, 8), torch.zeros(3, 2, 3, 3)
+    with pytest.raises(RuntimeError, match="runs on AMD GPUs"):
+        mca.functional.dilation(x, w, "max")
+    with pytest.raises(RuntimeError, match="runs on AMD GPUs"):
+        mca.functional.smorph(x, w, torch.zeros(3, 2))
+
+
+def test_module_parameters():
+    d = mca.nn.Dilation(3, 5, 7)
+    assert d.weight.shape == (5, 3, 7, 7) and d.weight.dtype == torch.float32 and not d.weight.any()
+    e = mca.nn.Erosion(4, 4, (3, 5), channel_merge_mode="identity", dtype=torch.float64)
+    assert e.weight.shape == (4, 1, 3, 5) and e.weight.dtype == torch.float64
+    with pytest.raises(ValueError, match="in_channels must be equal to out_channels"):
+        mca.nn.Dilation(3, 4, 3, channel_merge_mode="identity")
+    s = mca.nn.SMorph(3, 6, 5, init_alpha=2.0, dtype=torch.float64)
+    assert s.alpha.shape == (6, 3) and s.alpha.dtype == torch.float64 and float(s.alpha[0, 0]) == 2.0
+    assert s.weight.dtype == torch.float32  # the reference does not forward dtype to the weight
+    assert s.beta is None
+    s2 = mca.nn.SMorph(3, 3, 3, channel_merge_mode="identity", init_beta=1.0)
+    assert s2.alpha.shape == (3, 1) and s2.beta.shape == (3, 3)
+    assert set(dict(d.named_parameters())) == {"weight"} and set(dict(s.named_parameters())) == {"weight", "alpha"}

@@ -1,0 +1,88 @@
+"""The C ABI library (include/morphocore_amd.h): it loads, exports every declared symbol, and its
+argument validation answers with the reference's messages — all without a GPU (validation returns
+before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from morphocore_amd import _native
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "morphocore_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mca_\w+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.lib()
+    symbols = declared_symbols()
+    assert len(symbols) == 14
+    for name in symbols:
+        assert hasattr(lib, name), name
+    assert sorted(_native.EXPORTS) == symbols
+
+
+def test_version():
+    assert _native.version().startswith("0.13.1")
+
+
+GEOM = (2, 3, 4, 3, 16, 16, 3, 3)  # B, Cin, Cout, Cw, H, W, KH, KW
+
+
+def _forward(merge=2, geom=GEOM, op=0, indices=None):
+    lib = _native.lib()
+    return lib.mca_morpho_forward_f32(op, merge, 0, 0.0, None, None, 0, None, indices, *geom, None)
+
+
+@pytest.mark.parametrize("merge,message", [(9, "Unknown merge mode 9"), (-1, "Unknown merge mode -1"), (4, "Unsupported merge operation")])
+def test_rejects_merge(merge, message):
+    assert _forward(merge) == 1
+    assert _native.lib().mca_last_error().decode() == message
+
+
+def test_rejects_identity_shapes():
+    assert _forward(5, (2, 3, 4, 1, 8, 8, 3, 3)) == 1
+    assert "Identity mode requires weight.shape[0] == input.shape[1]" in _native.lib().mca_last_error().decode()
+    assert _forward(5, (2, 3, 3, 3, 8, 8, 3, 3)) == 1
+    assert "Identity mode requires weight.shape[1] == 1" in _native.lib().mca_last_error().decode()
+
+
+def test_rejects_channel_mismatch_and_operation():
+    assert _forward(2, (2, 3, 4, 2, 8, 8, 3, 3)) == 1
+    assert "Input channels must match weight input channels" in _native.lib().mca_last_error().decode()
+    assert _forward(2, op=7) == 1
+    assert "Unknown morphological operation" in _native.lib().mca_last_error().decode()
+
+
+def test_rejects_index_capacity():
+    # A non-null indices pointer for a 257 x 257 structuring element (taps >= 65536).
+    dummy = ctypes.c_void_p(16)
+    assert _forward(0, (1, 1, 1, 1, 8, 8, 257, 257), indices=dummy) == 1
+    assert "too large to save indices" in _native.lib().mca_last_error().decode()
+    assert _forward(2, indices=dummy) == 1
+    assert "only saved for the max and min merges" in _native.lib().mca_last_error().decode()
+
+
+def test_rejects_too_large_structuring_element_for_lds():
+    assert _forward(2, (1, 1, 1, 1, 8, 8, 200, 200)) == 1
+    assert "too large" in _native.lib().mca_last_error().decode()
+
+
+def test_workspace_sizes_and_rejection():
+    lib = _native.lib()
+    for merge in (0, 1, 2, 3):
+        assert lib.mca_morpho_backward_workspace_size_f32(merge, 0, *GEOM) > 0
+    assert lib.mca_morpho_backward_workspace_size_f32(0, 1, *GEOM) < lib.mca_morpho_backward_workspace_size_f32(0, 0, *GEOM)
+    assert lib.mca_morpho_backward_workspace_size_f64(2, 0, *GEOM) > lib.mca_morpho_backward_workspace_size_f32(2, 0, *GEOM)
+    assert lib.mca_morpho_backward_workspace_size_f32(9, 0, *GEOM) == 0
+    for merge in (0, 2, 3, 1):
+        assert lib.mca_smorph_backward_workspace_size_f32(merge, *GEOM) > 0
+    # A workspace that is too small is an argument error, before any device work.
+    rc = lib.mca_morpho_backward_f32(0, 2, 0, 0.0, None, None, 0, None, None, None, None, *GEOM, None, 16, None)
+    assert rc == 1 and "Workspace too small" in lib.mca_last_error().decode()
+    rc = lib.mca_smorph_backward_f32(2, None, None, None, None, None, None, None, None, *GEOM, None, 16, None)
+    assert rc == 1 and "Workspace too small" in lib.mca_last_error().decode()

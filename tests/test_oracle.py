@@ -1,0 +1,306 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP kernels.
+
+* against the reference's own CPU extension: vectors in tests/golden/ref_vectors.npz written by
+  tests/golden/make_golden.py from oracle/_ref (built from the reference sources);
+* against numpy brute force built like the reference's test references (tests/functional/utils.py:6-49,
+  test_padding.py:9-45 in the reference);
+* against the mathematics: float64 central finite differences for every gradient (including smorph's
+  alpha), closed-form gradient routing on exact inputs, the alpha -> +-inf and alpha = 0 limits of
+  smorph, and the reference's known-answer padding tests (test_padding.py:95-143);
+* the oracle's exponential against libm within the accuracy its method promises.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import normwise_error
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_vectors.npz")
+MERGES = ["max", "min", "sum", "mean", "identity"]
+PADDINGS = ["zero", "geodesic", "constant", "replicate"]
+TOLS = {"f32": 1e-6, "f64": 1e-12}
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)
+
+
+def _golden_morpho_cases(golden):
+    for key in golden.files:
+        parts = key.split("/")
+        if len(parts) == 7 and parts[1] == "morpho" and parts[6] == "out":
+            yield parts[0], parts[2], parts[3], parts[4], parts[5]
+
+
+def test_golden_morpho_forward_and_gradients(golden):
+    n = 0
+    for dname, op, merge, padding, variant in _golden_morpho_cases(golden):
+        key = f"{dname}/morpho/{op}/{merge}/{padding}/{variant}"
+        x = golden[f"{dname}/x" if variant == "rand" else f"{dname}/xq"]
+        w = golden[f"{dname}/wi" if merge == "identity" else f"{dname}/w"]
+        if variant == "quant":
+            w = np.zeros_like(w)
+        g = golden[f"{dname}/gi" if merge == "identity" else f"{dname}/g"]
+        opi = O.DILATION if op == "dilation" else O.EROSION
+        out, idx = O.morpho_forward(opi, O.MERGES[merge], O.PADDINGS[padding], 0.25, x, w, save_indices=merge in ("max", "min"))
+        assert np.array_equal(out, golden[key + "/out"]), key
+        assert np.array_equal(np.signbit(out), np.signbit(golden[key + "/out"])), key
+        gx, gw = O.morpho_backward(opi, O.MERGES[merge], O.PADDINGS[padding], 0.25, x, w, g, indices=idx)
+        assert normwise_error(gx, golden[key + "/gx"]) <= TOLS[dname], key
+        assert normwise_error(gw, golden[key + "/gw"]) <= TOLS[dname], key
+        n += 1
+    assert n >= 60
+
+
+def test_golden_smorph(golden):
+    n = 0
+    for dname in ("f32", "f64"):
+        x = golden[f"{dname}/x"]
+        for merge in MERGES:
+            wt = golden[f"{dname}/smorph/{merge}/w"]
+            g = golden[f"{dname}/gi" if merge == "identity" else f"{dname}/g"]
+            for aname in ("neg", "zero", "mixed", "shared"):
+                key = f"{dname}/smorph/{merge}/{aname}"
+                alpha = golden[key + "/alpha"]
+                out = O.smorph_forward(O.MERGES[merge], x, wt, alpha)
+                assert normwise_error(out, golden[key + "/out"]) <= TOLS[dname], key
+                gx, gw, ga = O.smorph_backward(O.MERGES[merge], x, wt, alpha, g)
+                assert normwise_error(gx, golden[key + "/gx"]) <= TOLS[dname], key
+                assert normwise_error(gw, golden[key + "/gw"]) <= TOLS[dname], key
+                assert normwise_error(ga, golden[key + "/ga"]) <= TOLS[dname], key
+                n += 1
+    assert n == 40
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("padding", PADDINGS)
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+def test_forward_matches_brute_force(op, merge, padding, dtype):
+    rng = np.random.default_rng(0)
+    for (B, Cin, Cout, H, W, KH, KW) in [(2, 3, 4, 6, 7, 3, 3), (1, 2, 3, 5, 4, 4, 2), (1, 2, 2, 3, 3, 5, 5)]:
+        if merge == "identity":
+            Cout = Cin
+        x = rng.standard_normal((B, Cin, H, W)).astype(dtype)
+        w = (rng.standard_normal((Cout, 1 if merge == "identity" else Cin, KH, KW)) * 0.3).astype(dtype)
+        out, idx = O.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding], -0.75, x, w, save_indices=merge in ("max", "min"))
+        ref, ref_idx = O.brute.forward(op, O.MERGES[merge], O.PADDINGS[padding], -0.75, x, w)
+        assert np.array_equal(out, ref)
+        if merge in ("max", "min"):
+            assert np.array_equal(idx, ref_idx)
+
+
+def test_forward_ties_first_tap_first_channel():
+    """Quantised input, zero weight: every window ties; the first tap and first channel win."""
+    rng = np.random.default_rng(1)
+    x = (rng.integers(0, 4, (1, 3, 6, 6)) / 4).astype(np.float32)
+    w = np.zeros((2, 3, 3, 3), np.float32)
+    for merge in ("max", "min"):
+        out, idx = O.morpho_forward(O.DILATION, O.MERGES[merge], O.REPLICATE, 0.0, x, w, save_indices=True)
+        ref, ref_idx = O.brute.forward(O.DILATION, O.MERGES[merge], O.REPLICATE, 0.0, x, w)
+        assert np.array_equal(out, ref) and np.array_equal(idx, ref_idx)
+    # All-minus-infinity windows keep tap 0 of channel 0, and the MAX merge clamps to lowest().
+    w_inf = np.full((1, 2, 3, 3), -np.inf, np.float32)
+    out, idx = O.morpho_forward(O.DILATION, O.MAX, O.GEODESIC, 0.0, x[:, :2], w_inf, save_indices=True)
+    assert np.all(out == np.finfo(np.float32).min) and np.all(idx == 0)
+
+
+def test_smorph_limits():
+    """alpha -> +inf / -inf gives dilation / erosion over in-image taps; alpha = 0 gives the plain
+    mean of the in-image values (reference tests/functional/utils.py:71-78)."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((1, 2, 7, 8))
+    w = rng.standard_normal((3, 2, 3, 3)) * 0.1
+    big = np.full((3, 2), 1000.0)
+    dil, _ = O.morpho_forward(O.DILATION, O.ADD, O.GEODESIC, 0.0, x, w)
+    np.testing.assert_allclose(O.smorph_forward(O.ADD, x, w, big), dil, rtol=0, atol=1e-2)
+    ero, _ = O.morpho_forward(O.EROSION, O.ADD, O.GEODESIC, 0.0, x, -w)
+    np.testing.assert_allclose(O.smorph_forward(O.ADD, x, w, -big), ero, rtol=0, atol=1e-2)
+    mean = O.smorph_forward(O.IDENTITY, x, w[:2, :1], np.zeros(2))
+    for c in range(2):
+        np.testing.assert_allclose(mean[0, c], O.brute.smorph_pair(x[0, c], w[c, 0], 0.0), rtol=1e-12)
+
+
+def test_smorph_matches_brute_force():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 3, 6, 5))
+    for merge in MERGES:
+        ident = merge == "identity"
+        Cout = 3 if ident else 4
+        w = rng.standard_normal((Cout, 1 if ident else 3, 3, 5)) * 0.2
+        alpha = rng.standard_normal(Cout if ident else (Cout, 3)) * 3
+        out = O.smorph_forward(O.MERGES[merge], x, w, alpha)
+        a = alpha.reshape(-1)
+        for b in range(2):
+            for o in range(Cout):
+                if ident:
+                    ref = O.brute.smorph_pair(x[b, o], w[o, 0], a[o])
+                else:
+                    pairs = [O.brute.smorph_pair(x[b, i], w[o, i], a[o * 3 + i]) for i in range(3)]
+                    if merge == "max":
+                        ref = np.maximum.reduce(pairs)
+                    elif merge == "min":
+                        ref = np.minimum.reduce(pairs)
+                    else:
+                        ref = sum(pairs) / (3 if merge == "mean" else 1)
+                np.testing.assert_allclose(out[b, o], ref, rtol=1e-13, atol=1e-13)
+
+
+def test_exp_accuracy():
+    """The restated vector exponential (morpho_cpu_simd.hpp:127-169) is within 1 ulp (float) and
+    2 ulp (double) of the correctly rounded exp on a dense grid."""
+    lib = O.lib()
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 20001), np.linspace(-1, 1, 2001)])
+    worst32 = worst64 = 0.0
+    for v in xs:
+        v32 = float(np.float32(v))
+        exact = math.exp(v32)
+        got = lib.oracle_expf(v32)
+        worst32 = max(worst32, abs(got - exact) / float(np.spacing(np.float32(exact))))
+        got64 = lib.oracle_exp(v)
+        worst64 = max(worst64, abs(got64 - math.exp(v)) / float(np.spacing(math.exp(v))))
+    assert worst32 <= 1.0 and worst64 <= 2.0, (worst32, worst64)
+
+
+def _finite_difference(f, arr, eps):
+    grad = np.zeros_like(arr)
+    flat = arr.reshape(-1)
+    gflat = grad.reshape(-1)
+    for j in range(flat.size):
+        keep = flat[j]
+        flat[j] = keep + eps
+        up = f()
+        flat[j] = keep - eps
+        down = f()
+        flat[j] = keep
+        gflat[j] = (up - down) / (2 * eps)
+    return grad
+
+
+@pytest.mark.parametrize("padding", ["geodesic", "zero", "constant"])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+def test_morpho_gradients_match_finite_differences(op, merge, padding):
+    """Gradients of a weighted sum of outputs, on inputs whose taps never tie (x*10 + arange, as the
+    reference's gradcheck separates ties, test_morpho_operation.py:333-337).
+
+    Fill paddings only: under 'replicate' the reference drops the gradient of a tap that read the
+    clamped edge pixel (morpho_op_cpu_backward.hxx:39-88), which is not the derivative of the
+    forward; that rule is pinned by the golden vectors of the reference build instead."""
+    rng = np.random.default_rng(4)
+    B, Cin, Cout, H, W, K = 1, 2, 3, 5, 6, 3
+    if merge == "identity":
+        Cout = Cin
+    x = rng.standard_normal((B, Cin, H, W)) * 10 + np.arange(B * Cin * H * W).reshape(B, Cin, H, W) * 0.37
+    w = rng.standard_normal((Cout, 1 if merge == "identity" else Cin, K, K)) * 10 + np.arange(Cout * (1 if merge == "identity" else Cin) * K * K).reshape(Cout, -1, K, K) * 0.11
+    g = rng.standard_normal((B, Cout, H, W))
+    m, p = O.MERGES[merge], O.PADDINGS[padding]
+
+    def loss():
+        out, _ = O.morpho_forward(op, m, p, 0.0, x, w)
+        return float(np.sum(out * g))
+
+    out, idx = O.morpho_forward(op, m, p, 0.0, x, w, save_indices=merge in ("max", "min"))
+    gx, gw = O.morpho_backward(op, m, p, 0.0, x, w, g, indices=idx)
+    np.testing.assert_allclose(gx, _finite_difference(loss, x, 1e-6), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(gw, _finite_difference(loss, w, 1e-6), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("merge", MERGES)
+def test_smorph_gradients_match_finite_differences(merge):
+    rng = np.random.default_rng(5)
+    B, Cin, H, W, K = 1, 2, 5, 4, 3
+    Cout = Cin if merge == "identity" else 3
+    x = rng.standard_normal((B, Cin, H, W))
+    w = rng.standard_normal((Cout, 1 if merge == "identity" else Cin, K, K)) * 0.3
+    alpha = rng.standard_normal(Cout if merge == "identity" else (Cout, Cin)) * 2
+    g = rng.standard_normal((B, Cout, H, W))
+    m = O.MERGES[merge]
+    if merge in ("max", "min"):
+        # Separate the channels so that no pair lies within the winner tolerance of another.
+        x = x + np.arange(Cin).reshape(1, Cin, 1, 1) * 5.0
+
+    def loss():
+        return float(np.sum(O.smorph_forward(m, x, w, alpha) * g))
+
+    gx, gw, ga = O.smorph_backward(m, x, w, alpha, g)
+    np.testing.assert_allclose(gx, _finite_difference(loss, x, 1e-6), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(gw, _finite_difference(loss, w, 1e-6), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(ga, _finite_difference(loss, alpha, 1e-6), rtol=1e-5, atol=1e-7)
+
+
+def test_gradient_routing_closed_form():
+    """Per-pair merges route each pixel's gradient to exactly one tap: with an all-ones gradient,
+    grad_weight[o, i] sums to sign * B * H * W and grad_input sums to the count of in-image picks."""
+    rng = np.random.default_rng(6)
+    x = rng.random((2, 3, 9, 10)).astype(np.float32)
+    w = (rng.standard_normal((4, 3, 5, 5)) * 0.05).astype(np.float32)
+    g = np.ones((2, 4, 9, 10), np.float32)
+    for op, sign in ((O.DILATION, 1.0), (O.EROSION, -1.0)):
+        gx, gw = O.morpho_backward(op, O.ADD, O.GEODESIC, 0.0, x, w, g)
+        assert np.array_equal(gw.sum(axis=(2, 3)), np.full((4, 3), sign * 2 * 9 * 10, np.float32))
+        # Geodesic borders never win, so every pick is in-image.
+        assert gx.sum() == 2 * 4 * 3 * 9 * 10
+
+
+class TestReferencePaddingKnownAnswers:
+    """The reference's known-answer padding tests (test_padding.py:95-143), on the oracle."""
+
+    @pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+    def test_zero_equals_constant_zero(self, op):
+        rng = np.random.default_rng(7)
+        x = rng.standard_normal((2, 3, 16, 16)).astype(np.float32)
+        w = rng.standard_normal((4, 3, 3, 3)).astype(np.float32)
+        for merge in (O.ADD, O.MAX):
+            a, _ = O.morpho_forward(op, merge, O.ZERO, 0.0, x, w)
+            b, _ = O.morpho_forward(op, merge, O.CONSTANT, 0.0, x, w)
+            assert np.array_equal(a, b)
+
+    @pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+    def test_geodesic_never_wins(self, op):
+        rng = np.random.default_rng(8)
+        x = rng.standard_normal((1, 1, 12, 12)).astype(np.float32)
+        w = np.zeros((1, 1, 5, 5), np.float32)
+        a, _ = O.morpho_forward(op, O.ADD, O.GEODESIC, 0.0, x, w)
+        b, _ = O.morpho_forward(op, O.ADD, O.CONSTANT, -1e9 if op == O.DILATION else 1e9, x, w)
+        assert np.array_equal(a, b)
+
+    @pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+    def test_constant_border_dominates(self, op):
+        rng = np.random.default_rng(9)
+        x = rng.random((1, 1, 8, 8)).astype(np.float32)
+        extreme = 50.0 if op == O.DILATION else -50.0
+        out, _ = O.morpho_forward(op, O.ADD, O.CONSTANT, extreme, x, np.zeros((1, 1, 3, 3), np.float32))
+        out = out[0, 0]
+        border = np.ones_like(out, dtype=bool)
+        border[1:-1, 1:-1] = False
+        assert np.all(out[border] == extreme) and np.all(out[~border] != extreme)
+
+    @pytest.mark.parametrize("padding", PADDINGS)
+    def test_interior_is_padding_independent(self, padding):
+        rng = np.random.default_rng(10)
+        x = rng.standard_normal((1, 1, 20, 20)).astype(np.float32)
+        w = rng.standard_normal((1, 1, 5, 5)).astype(np.float32)
+        ref, _ = O.morpho_forward(O.DILATION, O.ADD, O.GEODESIC, 0.0, x, w)
+        out, _ = O.morpho_forward(O.DILATION, O.ADD, O.PADDINGS[padding], 4.0, x, w)
+        assert np.array_equal(out[0, 0, 2:-2, 2:-2], ref[0, 0, 2:-2, 2:-2])
+
+
+def test_planted_mistakes_are_caught():
+    """Mistakes planted in a copy of the oracle's contract (on the CPU) fail the brute force: a
+    flipped tap orientation and a non-strict (last-tap) tie rule."""
+    rng = np.random.default_rng(11)
+    x = (rng.integers(0, 4, (1, 2, 6, 7)) / 4).astype(np.float32)
+    w = np.zeros((2, 2, 3, 3), np.float32)
+    w[:, :, 0, 1] = 0.5
+    out, idx = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, w, save_indices=True)
+    flipped, fidx = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, np.ascontiguousarray(w[:, :, ::-1, ::-1]), save_indices=True)
+    assert not np.array_equal(out, flipped) or not np.array_equal(idx, fidx)
+    # The last-tap rule on ties would select a later tap than the brute force's first one.
+    _, ref_idx = O.brute.forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, np.zeros_like(w))
+    _, tie_idx = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, np.zeros_like(w), save_indices=True)
+    assert np.array_equal(tie_idx, ref_idx) and np.any((ref_idx & 0xFFFF) != 8)
