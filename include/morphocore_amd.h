@@ -45,16 +45,27 @@ const char* mca_version(void);
  * c10::Error the reference's TORCH_CHECKs raise. */
 const char* mca_last_error(void);
 
+/* Bytes of the winners ("indices") the forward can save for the backward, by merge:
+ *   MAX / MIN: int32 (channel << 16) | tap per output pixel, [B, Cout, H, W], as the reference saves
+ *     them (morphocore/functional/csrc/cpp/morpho_op_cpu_kernels.hxx:36-41; requires
+ *     KH * KW < 65536 and Cin < 32768, morpho_op.cu:40-41);
+ *   ADD / AVERAGE / IDENTITY: the first extremal tap kh * KW + kw of every channel pair,
+ *     [B, Cout, Cpair, H, W] with Cpair = Cin (1 for IDENTITY), uint8 (uint16 when KH * KW > 256).
+ *     The reference recomputes these in its backward (morpho_op_cpu_backward.hxx:90-156); saving
+ *     them is this library's extension of the reference's save_indices flag.
+ * No reference counterpart (the reference sizes its index tensor inline, morpho_op_wrap.hxx:85-88). */
+size_t mca_morpho_indices_bytes(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW);
+
 /* Dilation / erosion forward, every merge.
  * Replaces morpho_forward_cuda<op, T> (morphocore/functional/csrc/cuda/morpho_op.cuh:16-17,
- * morpho_op.cu:30-74). `indices` may be NULL; when given, merge must be MAX or MIN and
- * KH * KW < 65536, Cin < 32768 (morpho_op.cu:40-41). */
+ * morpho_op.cu:30-74). `indices` may be NULL, else it receives the winners described by
+ * mca_morpho_indices_bytes. */
 int mca_morpho_forward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
-                           int64_t weight_batch_stride, float* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
-                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+                           int64_t weight_batch_stride, float* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                           int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
 int mca_morpho_forward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
-                           int64_t weight_batch_stride, double* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
-                           int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+                           int64_t weight_batch_stride, double* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                           int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
 
 /* Workspace bytes mca_morpho_backward_* needs for this merge and geometry; has_indices says
  * whether saved indices will be passed. No reference counterpart: the reference allocates its
@@ -67,14 +78,14 @@ size_t mca_morpho_backward_workspace_size_f64(int merge, int has_indices, int64_
 /* Dilation / erosion backward: overwrites grad_input [B, Cin, H, W] and grad_weight [Cout, Cw, KH, KW]
  * (summed over the batch when the structuring element is per batch element).
  * Replaces morpho_backward_cuda<op, T> (morphocore/functional/csrc/cuda/morpho_op.cuh:21-24,
- * morpho_op.cu:102-177). `indices` (MAX / MIN only) may be NULL, in which case the winners are
- * recomputed. */
+ * morpho_op.cu:102-177). `indices` holds the forward's winners (see mca_morpho_indices_bytes) or is
+ * NULL, in which case they are recomputed into the workspace. */
 int mca_morpho_backward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
-                            int64_t weight_batch_stride, const int32_t* indices, const float* grad_output, float* grad_input,
+                            int64_t weight_batch_stride, const void* indices, const float* grad_output, float* grad_input,
                             float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
-                            int64_t weight_batch_stride, const int32_t* indices, const double* grad_output, double* grad_input,
+                            int64_t weight_batch_stride, const void* indices, const double* grad_output, double* grad_input,
                             double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 

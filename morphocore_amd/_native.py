@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmorphoco
 EXPORTS = (
     "mca_version",
     "mca_last_error",
+    "mca_morpho_indices_bytes",
     "mca_morpho_forward_f32",
     "mca_morpho_forward_f64",
     "mca_morpho_backward_workspace_size_f32",
@@ -53,6 +54,8 @@ def lib() -> ctypes.CDLL:
     so.mca_version.argtypes = []
     so.mca_last_error.restype = ctypes.c_char_p
     so.mca_last_error.argtypes = []
+    so.mca_morpho_indices_bytes.argtypes = [_I] + _GEOM
+    so.mca_morpho_indices_bytes.restype = _SZ
     for sfx, real in (("f32", ctypes.c_float), ("f64", ctypes.c_double)):
         f = getattr(so, f"mca_morpho_forward_{sfx}")
         f.argtypes = [_I, _I, _I, real, _P, _P, _I64, _P, _P] + _GEOM + [_P]
@@ -103,6 +106,12 @@ def _stream(t: torch.Tensor) -> int:
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def indices_bytes(merge, geom) -> int:
+    """Bytes of the winners the forward can save for this merge (C ABI mca_morpho_indices_bytes):
+    packed int32 per output pixel for max / min, one tap per channel pair and pixel otherwise."""
+    return int(lib().mca_morpho_indices_bytes(merge, *geom))
 
 
 def morpho_forward(op, merge, replicate, fill, x, weight, weight_batch_stride, out, indices, geom):

@@ -1,5 +1,6 @@
 // C ABI of the morphocore_amd kernels: argument validation with the reference's messages, then the
-// asynchronous launchers of morpho.hip / smorph.hip. Declarations: include/morphocore_amd.h.
+// asynchronous launchers of morpho_fwd.hip / morpho_bwd.hip / smorph.hip. Declarations:
+// include/morphocore_amd.h.
 #include "../../include/morphocore_amd.h"
 
 #include <string>
@@ -68,18 +69,15 @@ int check_lds(size_t bytes)
 
 template <typename T>
 int morpho_forward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, T* output,
-                        int32_t* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                        void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
                         void* stream)
 {
     mca::Geom g{};
     if (op != mca::DILATION && op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(op));
     int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, wbs, g);
     if (rc != MCA_OK) return rc;
-    if (indices)
-    {
-        if (merge != mca::MERGE_MAX && merge != mca::MERGE_MIN) return fail("Indices are only saved for the max and min merges");
-        if (!(KH * KW < (1 << 16) && Cin < (1 << 15))) return fail("Structuring element or channel count too large to save indices");
-    }
+    if (indices && mca::packed_winners(merge) && !(KH * KW < (1 << 16) && Cin < (1 << 15)))
+        return fail("Structuring element or channel count too large to save indices");
     if ((rc = check_lds(mca::morpho_forward_lds<T>(g))) != MCA_OK) return rc;
     return hip_status(mca::morpho_forward<T>(op, merge, replicate != 0, fill, input, weight, output, indices, g, (hipStream_t)stream));
 }
@@ -94,7 +92,7 @@ size_t morpho_workspace_impl(int merge, int has_indices, int64_t B, int64_t Cin,
 }
 
 template <typename T>
-int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, const int32_t* indices,
+int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, const void* indices,
                          const T* grad_output, T* grad_input, T* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                          int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
 {
@@ -102,12 +100,10 @@ int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* inpu
     if (op != mca::DILATION && op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(op));
     int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, wbs, g);
     if (rc != MCA_OK) return rc;
-    if (indices && merge != mca::MERGE_MAX && merge != mca::MERGE_MIN) return fail("Indices are only saved for the max and min merges");
-    if ((merge == mca::MERGE_MAX || merge == mca::MERGE_MIN) && !(KH * KW < (1 << 16) && Cin < (1 << 15)))
+    if (mca::packed_winners(merge) && !(KH * KW < (1 << 16) && Cin < (1 << 15)))
         return fail("Structuring element or channel count too large to save indices");
     if ((rc = check_lds(mca::morpho_backward_lds<T>(merge, g))) != MCA_OK) return rc;
-    if (!indices && (merge == mca::MERGE_MAX || merge == mca::MERGE_MIN) && (rc = check_lds(mca::morpho_forward_lds<T>(g))) != MCA_OK)
-        return rc;
+    if (!indices && (rc = check_lds(mca::morpho_forward_lds<T>(g))) != MCA_OK) return rc;
     const size_t need = mca::morpho_backward_workspace<T>(merge, indices != nullptr, g);
     if (workspace_bytes < need || (need > 0 && !workspace))
         return fail("Workspace too small: " + std::to_string(workspace_bytes) + " bytes given, " + std::to_string(need) + " needed");
@@ -158,8 +154,15 @@ const char* mca_version(void) { return "0.13.1-mi355x"; }
 
 const char* mca_last_error(void) { return g_last_error.c_str(); }
 
+size_t mca_morpho_indices_bytes(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return mca::indices_bytes(merge, g);
+}
+
 int mca_morpho_forward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
-                           int64_t weight_batch_stride, float* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t weight_batch_stride, float* output, void* indices, int64_t B, int64_t Cin, int64_t Cout,
                            int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
 {
     return morpho_forward_impl<float>(op, merge, replicate, fill, input, weight, weight_batch_stride, output, indices, B, Cin, Cout, Cw,
@@ -167,7 +170,7 @@ int mca_morpho_forward_f32(int op, int merge, int replicate, float fill, const f
 }
 
 int mca_morpho_forward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
-                           int64_t weight_batch_stride, double* output, int32_t* indices, int64_t B, int64_t Cin, int64_t Cout,
+                           int64_t weight_batch_stride, double* output, void* indices, int64_t B, int64_t Cin, int64_t Cout,
                            int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
 {
     return morpho_forward_impl<double>(op, merge, replicate, fill, input, weight, weight_batch_stride, output, indices, B, Cin, Cout,
@@ -187,7 +190,7 @@ size_t mca_morpho_backward_workspace_size_f64(int merge, int has_indices, int64_
 }
 
 int mca_morpho_backward_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
-                            int64_t weight_batch_stride, const int32_t* indices, const float* grad_output, float* grad_input,
+                            int64_t weight_batch_stride, const void* indices, const float* grad_output, float* grad_input,
                             float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
 {
@@ -196,7 +199,7 @@ int mca_morpho_backward_f32(int op, int merge, int replicate, float fill, const 
 }
 
 int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const double* input, const double* weight,
-                            int64_t weight_batch_stride, const int32_t* indices, const double* grad_output, double* grad_input,
+                            int64_t weight_batch_stride, const void* indices, const double* grad_output, double* grad_input,
                             double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
 {

@@ -1,5 +1,6 @@
-// Host-side launchers of the HIP kernels (morpho.hip, smorph.hip), called by the C ABI (capi.cpp).
-// Arguments are assumed validated by the caller; every launch is asynchronous on `stream`.
+// Host-side launchers of the HIP kernels (morpho_fwd.hip, morpho_bwd.hip, smorph.hip, util.hip),
+// called by the C ABI (capi.cpp). Arguments are assumed validated by the caller; every launch is
+// asynchronous on `stream`.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -16,7 +17,7 @@ constexpr size_t WS_ALIGN = 256;
 
 inline size_t align_up(size_t v) { return (v + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
 
-// Rows of outputs each wave computes, per element size.
+// Rows of outputs each wave computes in the generic (runtime structuring element) kernels.
 template <typename T>
 constexpr int rows_per_wave()
 {
@@ -26,8 +27,24 @@ constexpr int rows_per_wave()
 // Largest LDS allocation a launch may request (bytes).
 constexpr size_t LDS_LIMIT = 64 * 1024;
 
+// Saved winners of the forward pass ("indices"):
+//   MAX / MIN merges: int32 (channel << 16) | tap per output pixel, [B, Cout, H, W];
+//   ADD / AVERAGE / IDENTITY: the first extremal tap of every channel pair, [B, Cout, Cpair, H, W]
+//   with Cpair = Cin (1 for IDENTITY), one byte per entry (two when KH * KW > 256).
+inline bool packed_winners(int merge) { return merge == MERGE_MAX || merge == MERGE_MIN; }
+
+inline size_t pair_tap_bytes(const Geom& g) { return g.taps() > 256 ? 2 : 1; }
+
+inline size_t indices_bytes(int merge, const Geom& g)
+{
+    const size_t pix = (size_t)g.B * g.Cout * g.plane();
+    if (packed_winners(merge)) return pix * sizeof(int32_t);
+    const size_t cpair = merge == MERGE_IDENTITY ? 1 : (size_t)g.Cin;
+    return pix * cpair * pair_tap_bytes(g);
+}
+
 template <typename T>
-hipError_t morpho_forward(int op, int merge, bool replicate, T fill, const T* x, const T* w, T* out, int32_t* indices, const Geom& g,
+hipError_t morpho_forward(int op, int merge, bool replicate, T fill, const T* x, const T* w, T* out, void* indices, const Geom& g,
                           hipStream_t stream);
 
 // Bytes of LDS the forward kernel needs; > LDS_LIMIT means the structuring element is too large.
@@ -41,7 +58,7 @@ template <typename T>
 size_t morpho_backward_lds(int merge, const Geom& g);
 
 template <typename T>
-hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const int32_t* indices, const T* grad_out,
+hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
                            T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 template <typename T>
@@ -57,7 +74,7 @@ template <typename T>
 hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, const T* out, const T* grad_out, T* grad_in, T* grad_w,
                            T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-// Shared helpers (morpho.hip).
+// Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);
 

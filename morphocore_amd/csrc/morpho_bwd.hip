@@ -1,0 +1,417 @@
+// Dilation / erosion backward for gfx950: gradient routing from the winners of the forward pass.
+//
+// MAX / MIN (morpho_bwd_packed_kernel): one workgroup per (output channel, pixel chunk) scatters each
+// output gradient to its packed (channel, tap): grad_input by global float atomics (one per output
+// pixel), grad_weight into LDS bins that become this workgroup's partial slot.
+// Reference semantics: morpho_op_cpu_backward.hxx:39-88 (run_single_winner).
+//
+// ADD / AVERAGE / IDENTITY (morpho_bwd_taps_kernel): every channel pair routes g * scale to its own
+// first extremal tap (morpho_op_cpu_backward.hxx:90-156, scale = 1 / Cin for AVERAGE). One workgroup
+// per (batch element, tile, group of IG input channels) walks the output channels, reads each pair's
+// saved tap (one byte), accumulates grad_input in an LDS copy of the tile plus halo (flushed once
+// with global atomics, the halo being shared with the neighbouring tiles) and grad_weight in
+// lane-striped LDS bins, written once per chunk of output channels into the workgroup's partial
+// slot. Partial slots are then summed in a fixed order (reduce_slots_async).
+//
+// A tap that read outside the image (including REPLICATE's clamped edge pixel) sends nothing to
+// grad_input; grad_weight always receives sign * g (sign -1 for erosion).
+// When the forward pass did not save its winners, the forward kernel recomputes them into the
+// workspace first.
+#include "launch.hpp"
+
+namespace mca
+{
+
+template <typename T>
+struct PackedParams
+{
+    const int32_t* __restrict__ idx;
+    const T* __restrict__ gout;
+    T* __restrict__ gin;
+    T* __restrict__ part;
+    Geom g;
+    int nchunks;
+    int lds_bins;
+    int64_t chunk;
+};
+
+template <typename T, int OP>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedParams<T> p)
+{
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    T* bins = reinterpret_cast<T*>(smem_raw);
+    const Geom g = p.g;
+    const int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int chunk = work % p.nchunks;
+    const int o = work / p.nchunks;
+    const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
+    const int64_t nb = (int64_t)g.Cin * K;
+    const int64_t plane = g.plane();
+    T* part = p.part + ((int64_t)chunk * g.Cout + o) * nb;
+    if (p.lds_bins)
+    {
+        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) bins[j] = T(0);
+        __syncthreads();
+    }
+    const int64_t total = (int64_t)g.B * plane;
+    const int64_t n_begin = (int64_t)chunk * p.chunk;
+    const int64_t n_end = min(n_begin + p.chunk, total);
+    const T sign = (T)OpTraits<OP, T>::sign;
+    for (int64_t n = n_begin + threadIdx.x; n < n_end; n += BLOCK)
+    {
+        const int64_t b = n / plane;
+        const int64_t pix = n - b * plane;
+        const int h = (int)(pix / g.W), wc = (int)(pix - (int64_t)h * g.W);
+        const int64_t gi = (b * g.Cout + o) * plane + pix;
+        const T gv = p.gout[gi];
+        if (gv == T(0)) continue;
+        const int32_t packed = p.idx[gi];
+        const int c = packed >> 16, k = packed & 0xFFFF;
+        const int kh = k / g.KW, kw = k - kh * g.KW;
+        const int iy = h + ph - kh, ix = wc + pw - kw;
+        if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], gv);
+        if (p.lds_bins)
+            lds_add(&bins[(int64_t)c * K + k], sign * gv);
+        else
+            global_add(&part[(int64_t)c * K + k], sign * gv);
+    }
+    if (p.lds_bins)
+    {
+        __syncthreads();
+        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) part[j] = bins[j];
+    }
+}
+
+template <typename T>
+struct TapsParams
+{
+    const void* __restrict__ taps;
+    const T* __restrict__ gout;
+    T* __restrict__ gin;
+    T* __restrict__ part;
+    Geom g;
+    Tiling t;
+    int ig;     // input channels per workgroup
+    int nig;    // groups of input channels
+    int oc;     // output channels per grad_weight flush
+    int ncopy;  // lane-striped copies of each grad_weight bin (power of two)
+    T scale;
+};
+
+template <typename T, int OP, typename AT, bool IDENT, int RH>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams<T> p)
+{
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
+    const int tile_elems = t.rows * t.pitch;
+    T* gx = reinterpret_cast<T*>(smem_raw);
+    T* bins = gx + (size_t)p.ig * tile_elems;
+    int* tapinfo = reinterpret_cast<int*>(bins + (size_t)p.oc * p.ig * K * p.ncopy);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int igi = work % p.nig;
+    work /= p.nig;
+    const int tile = work % t.ntiles();
+    const int b = work / t.ntiles();
+    const int ty = tile / t.ntx, tx = tile - ty * t.ntx;
+    const int h0 = ty * t.th, w0 = tx * TILE_W, wc = w0 + lane;
+    const int y0 = h0 + ph - (g.KH - 1), x0 = w0 + pw - (g.KW - 1);
+    const int i0 = igi * p.ig;
+    const int ni = min(p.ig, g.Cin - i0);
+    const int64_t plane = g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
+    T* part = p.part + ((int64_t)b * t.ntiles() + tile) * wnumel;
+    const T sign = (T)OpTraits<OP, T>::sign;
+    const int copy = lane & (p.ncopy - 1);
+    const int cpair = IDENT ? 1 : g.Cin;
+    const AT* __restrict__ taps = static_cast<const AT*>(p.taps);
+
+    for (int k = threadIdx.x; k < K; k += BLOCK) tapinfo[k] = ((k / g.KW) << 16) | (k % g.KW);
+    for (int j = threadIdx.x; j < p.ig * tile_elems; j += BLOCK) gx[j] = T(0);
+    const int nbins = p.oc * p.ig * K * p.ncopy;
+    for (int j = threadIdx.x; j < nbins; j += BLOCK) bins[j] = T(0);
+    __syncthreads();
+
+    // Route the gradient of output channel o, pair with input channel i = i0 + il.
+    auto route = [&](int o, int il, int oc_local, const T (&gr)[RH]) {
+        const int i = i0 + il;
+        const AT* __restrict__ tp = taps + (((int64_t)b * g.Cout + o) * cpair + (IDENT ? 0 : i)) * plane;
+        T* gxl = gx + il * tile_elems;
+        T* bl = bins + (size_t)(oc_local * p.ig + il) * K * p.ncopy;
+#pragma unroll
+        for (int r = 0; r < RH; ++r)
+        {
+            const int h = h0 + wave * RH + r;
+            if (gr[r] == T(0)) continue;  // also every pixel outside the image
+            const int k = (int)tp[(int64_t)h * g.W + wc];
+            const int info = tapinfo[k];
+            const int kh = info >> 16, kw = info & 0xFFFF;
+            const int iy = h + ph - kh, ix = wc + pw - kw;
+            if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) lds_add(&gxl[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], gr[r]);
+            lds_add(&bl[k * p.ncopy + copy], sign * gr[r]);
+        }
+    };
+    auto load_grad = [&](int o, T (&gr)[RH]) {
+#pragma unroll
+        for (int r = 0; r < RH; ++r)
+        {
+            const int h = h0 + wave * RH + r;
+            gr[r] = (h < g.H && wc < g.W) ? p.gout[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] * p.scale : T(0);
+        }
+    };
+    // Sum the copies of every bin of output channels [oc0, oc0 + noc) into this workgroup's slot.
+    auto flush_bins = [&](int oc0, int noc) {
+        __syncthreads();
+        const int n = noc * p.ig * K;
+        for (int j = threadIdx.x; j < n; j += BLOCK)
+        {
+            const int k = j % K;
+            const int il = (j / K) % p.ig;
+            const int ol = j / (K * p.ig);
+            T s = T(0);
+            for (int c = 0; c < p.ncopy; ++c)
+            {
+                s += bins[(size_t)j * p.ncopy + c];
+                bins[(size_t)j * p.ncopy + c] = T(0);
+            }
+            if (il < ni)
+            {
+                const int o = IDENT ? i0 + il : oc0 + ol;
+                part[((int64_t)o * g.Cw + (IDENT ? 0 : i0 + il)) * K + k] = s;
+            }
+        }
+        __syncthreads();
+    };
+
+    if constexpr (IDENT)
+    {
+        for (int il = 0; il < ni; ++il)
+        {
+            T gr[RH];
+            load_grad(i0 + il, gr);
+            route(i0 + il, il, 0, gr);
+        }
+        flush_bins(0, 1);
+    }
+    else
+    {
+        for (int oc0 = 0; oc0 < g.Cout; oc0 += p.oc)
+        {
+            const int noc = min(p.oc, g.Cout - oc0);
+            for (int ol = 0; ol < noc; ++ol)
+            {
+                T gr[RH];
+                load_grad(oc0 + ol, gr);
+                for (int il = 0; il < ni; ++il) route(oc0 + ol, il, ol, gr);
+            }
+            flush_bins(oc0, noc);
+        }
+    }
+
+    // grad_input of the tile and its halo (shared with the neighbouring tiles: atomics).
+    for (int il = 0; il < ni; ++il)
+    {
+        T* gplane = p.gin + ((int64_t)b * g.Cin + i0 + il) * plane;
+        const T* gxl = gx + il * tile_elems;
+        for (int ly = wave; ly < t.rows; ly += NWAVES)
+        {
+            const int iy = y0 + ly;
+            if (iy < 0 || iy >= g.H) continue;
+            for (int lx = lane; lx < t.cols; lx += WAVE)
+            {
+                const int ix = x0 + lx;
+                if (ix < 0 || ix >= g.W) continue;
+                const T v = gxl[ly * t.pitch + lx];
+                if (v != T(0)) global_add(&gplane[(int64_t)iy * g.W + ix], v);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Launch
+// ------------------------------------------------------------------------------------------------
+
+struct PackedPlan
+{
+    int nchunks;
+    int64_t chunk;
+    bool lds_bins;
+    size_t part_bytes;
+    size_t lds;
+};
+
+template <typename T>
+static PackedPlan plan_packed(const Geom& g)
+{
+    PackedPlan s{};
+    const int64_t total = (int64_t)g.B * g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cin * g.taps();
+    int64_t nchunks = (4096 + g.Cout - 1) / g.Cout;
+    const int64_t max_chunks = (total + BLOCK - 1) / BLOCK;
+    if (nchunks > max_chunks) nchunks = max_chunks;
+    while (nchunks > 1 && (size_t)nchunks * wnumel * sizeof(T) > ((size_t)256 << 20)) nchunks /= 2;
+    if (nchunks < 1) nchunks = 1;
+    s.nchunks = (int)nchunks;
+    s.chunk = (total + nchunks - 1) / nchunks;
+    const size_t bins = (size_t)g.Cin * g.taps() * sizeof(T);
+    s.lds_bins = bins <= (size_t)48 * 1024;
+    s.lds = s.lds_bins ? bins : 0;
+    s.part_bytes = (size_t)nchunks * wnumel * sizeof(T);
+    return s;
+}
+
+struct TapsPlan
+{
+    Tiling t;
+    int ig, nig, oc, ncopy;
+    size_t part_bytes;
+    size_t lds;
+};
+
+template <typename T>
+static TapsPlan plan_taps(int merge, const Geom& g)
+{
+    TapsPlan s{};
+    s.t = make_tiling(g, rows_per_wave<T>());
+    const size_t tile = (size_t)s.t.rows * s.t.pitch * sizeof(T);
+    const size_t K = (size_t)g.taps();
+    const size_t budget = 48 * 1024 - K * sizeof(int);
+    const bool ident = merge == MERGE_IDENTITY;
+    s.ncopy = 4;
+    s.ig = ident ? 4 : 2;
+    // Fewer input channels per workgroup when one tile each does not leave room for the bins of one
+    // output channel.
+    while (s.ig > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(T) > budget) s.ig /= 2;
+    if (s.ig > g.Cin) s.ig = g.Cin > 0 ? g.Cin : 1;
+    while (s.ncopy > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(T) > budget) s.ncopy /= 2;
+    if (ident)
+    {
+        s.oc = 1;
+    }
+    else
+    {
+        const size_t per_oc = (size_t)s.ig * K * s.ncopy * sizeof(T);
+        const size_t room = budget > s.ig * tile ? budget - s.ig * tile : 0;
+        s.oc = (int)(room / per_oc);
+        if (s.oc > g.Cout) s.oc = g.Cout;
+        if (s.oc < 1) s.oc = 1;
+    }
+    s.nig = (g.Cin + s.ig - 1) / s.ig;
+    s.lds = s.ig * tile + (size_t)s.oc * s.ig * K * s.ncopy * sizeof(T) + K * sizeof(int);
+    s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
+    return s;
+}
+
+template <typename T>
+size_t morpho_backward_lds(int merge, const Geom& g)
+{
+    if (packed_winners(merge)) return plan_packed<T>(g).lds;
+    return plan_taps<T>(merge, g).lds;
+}
+
+template <typename T>
+size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
+{
+    size_t bytes = packed_winners(merge) ? align_up(plan_packed<T>(g).part_bytes) : align_up(plan_taps<T>(merge, g).part_bytes);
+    if (!has_indices) bytes += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(T));
+    return bytes;
+}
+
+template <typename T, int OP>
+static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
+                              T* grad_in, T* grad_w, const Geom& g, unsigned char* ws, hipStream_t stream)
+{
+    hipError_t err;
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
+    if ((int64_t)g.B * g.Cout * g.plane() == 0) return fill_async<T>(grad_w, wnumel, T(0), stream);
+
+    const bool packed = packed_winners(merge);
+    const size_t part_bytes = packed ? plan_packed<T>(g).part_bytes : plan_taps<T>(merge, g).part_bytes;
+    T* part = reinterpret_cast<T*>(ws);
+    ws += align_up(part_bytes);
+    if (!indices)
+    {
+        // The forward pass did not keep its winners: recompute them (and a scratch output).
+        void* idx = ws;
+        T* tmp_out = reinterpret_cast<T*>(ws + align_up(indices_bytes(merge, g)));
+        if ((err = morpho_forward<T>(OP, merge, replicate, fill, x, w, tmp_out, idx, g, stream)) != hipSuccess) return err;
+        indices = idx;
+    }
+
+    if (packed)
+    {
+        const PackedPlan s = plan_packed<T>(g);
+        if (!s.lds_bins)
+            if ((err = fill_async<T>(part, (int64_t)s.nchunks * wnumel, T(0), stream)) != hipSuccess) return err;
+        PackedParams<T> p{};
+        p.idx = static_cast<const int32_t*>(indices);
+        p.gout = grad_out;
+        p.gin = grad_in;
+        p.part = part;
+        p.g = g;
+        p.nchunks = s.nchunks;
+        p.lds_bins = s.lds_bins ? 1 : 0;
+        p.chunk = s.chunk;
+        morpho_bwd_packed_kernel<T, OP><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        return reduce_slots_async<T>(part, s.nchunks, wnumel, grad_w, stream);
+    }
+
+    const TapsPlan s = plan_taps<T>(merge, g);
+    TapsParams<T> p{};
+    p.taps = indices;
+    p.gout = grad_out;
+    p.gin = grad_in;
+    p.part = part;
+    p.g = g;
+    p.t = s.t;
+    p.ig = s.ig;
+    p.nig = s.nig;
+    p.oc = s.oc;
+    p.ncopy = s.ncopy;
+    p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
+    constexpr int RH = rows_per_wave<T>();
+    const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
+    const bool wide = pair_tap_bytes(g) == 2;
+    if (merge == MERGE_IDENTITY)
+    {
+        if (wide)
+            morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+        else
+            morpho_bwd_taps_kernel<T, OP, uint8_t, true, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+    }
+    else
+    {
+        if (wide)
+            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+        else
+            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+    }
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    return reduce_slots_async<T>(part, g.B * s.t.ntiles(), wnumel, grad_w, stream);
+}
+
+template <typename T>
+hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
+                           T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+    if (workspace_bytes < morpho_backward_workspace<T>(merge, indices != nullptr, g)) return hipErrorInvalidValue;
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    return op == DILATION ? backward_op<T, DILATION>(merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, ws, stream)
+                          : backward_op<T, EROSION>(merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, ws, stream);
+}
+
+#define MCA_INSTANTIATE_BWD(T)                                                                                                          \
+    template size_t morpho_backward_workspace<T>(int, bool, const Geom&);                                                               \
+    template size_t morpho_backward_lds<T>(int, const Geom&);                                                                           \
+    template hipError_t morpho_backward<T>(int, int, bool, T, const T*, const T*, const void*, const T*, T*, T*, const Geom&, void*,    \
+                                           size_t, hipStream_t);
+
+MCA_INSTANTIATE_BWD(float)
+MCA_INSTANTIATE_BWD(double)
+
+}  // namespace mca

@@ -1,0 +1,54 @@
+// Small helper kernels shared by the launchers: fill (zeroing accumulators without hipMemsetAsync,
+// so that the launches stay valid under stream capture) and the fixed-order sum of per-workgroup
+// partial slots.
+#include "launch.hpp"
+
+namespace mca
+{
+
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void fill_kernel(T* __restrict__ p, int64_t n, T v)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) p[j] = v;
+}
+
+// out[j] = sum over slots s = 0, 1, ... of part[s * n + j], always in slot order.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void reduce_slots_kernel(const T* __restrict__ part, int nslots, int64_t n, T* __restrict__ out)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
+    {
+        T s = T(0);
+        for (int slot = 0; slot < nslots; ++slot) s += part[(int64_t)slot * n + j];
+        out[j] = s;
+    }
+}
+
+static int grid_for(int64_t n)
+{
+    const int64_t blocks = (n + BLOCK - 1) / BLOCK;
+    return (int)(blocks < 8192 ? (blocks < 1 ? 1 : blocks) : 8192);
+}
+
+template <typename T>
+hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    fill_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(p, n, v);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    reduce_slots_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(part, nslots, n, out);
+    return hipGetLastError();
+}
+
+template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
+template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
+template hipError_t reduce_slots_async<float>(const float*, int, int64_t, float*, hipStream_t);
+template hipError_t reduce_slots_async<double>(const double*, int, int64_t, double*, hipStream_t);
+
+}  // namespace mca

@@ -9,6 +9,8 @@ a TORCH_CHECK becomes in Python), same saved state. The arithmetic runs only in 
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from .. import _native
@@ -16,9 +18,23 @@ from .merge_enum import MorphoMerge, MorphoPadding
 
 DILATION, EROSION = 0, 1
 
-# Indices are saved only while the reference's CUDA grid could address every (batch, output channel)
-# pair (morpho_op_wrap.hxx:65-66).
+# Max / min winners are saved only while the reference's CUDA grid could address every (batch,
+# output channel) pair (morpho_op_wrap.hxx:65-66).
 _MAX_GRID_DIM = 65535
+
+# The per-pair taps of the sum / mean / identity merges (one byte per channel pair and output
+# pixel) are kept for the backward pass up to this many bytes per call; beyond it the backward
+# recomputes them. MORPHOCORE_AMD_SAVED_TAPS_LIMIT overrides it (bytes, 0 disables saving).
+_SAVED_TAPS_LIMIT = int(os.environ.get("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", 8 << 30))
+
+
+def _should_save(merge: MorphoMerge, save_indices: bool, needs_grad: bool, B: int, Cout: int, nbytes: int) -> bool:
+    """Whether the forward keeps its winners for the backward. The result never depends on it."""
+    if not (save_indices and needs_grad):
+        return False
+    if merge in (MorphoMerge.MAX, MorphoMerge.MIN):
+        return Cout * B < _MAX_GRID_DIM
+    return nbytes <= _SAVED_TAPS_LIMIT
 
 
 def to_merge(merge: int) -> MorphoMerge:
@@ -122,7 +138,7 @@ class _MorphoFunction(torch.autograd.Function):
     """MorphoOperation<op, merge, kind> (morpho_op_wrap.hxx:24-211) on 4-D, checked arguments."""
 
     @staticmethod
-    def forward(ctx, x4, w4, op, merge, padding, padding_value, save_indices, noise_scale):
+    def forward(ctx, x4, w4, op, merge, padding, padding_value, save_indices, noise_scale, needs_grad):
         geom = _geom(x4, w4)
         B, Cin, Cout, Cw, H, W, KH, KW = geom
         x4c = x4.contiguous()
@@ -135,9 +151,11 @@ class _MorphoFunction(torch.autograd.Function):
             sample_weight = (w4c.unsqueeze(0) + noise).contiguous()
         kernel_weight = sample_weight if sample_weight is not None else w4c
         wbs = Cout * Cw * KH * KW if sample_weight is not None else 0
-        should_save = bool(save_indices) and merge in (MorphoMerge.MAX, MorphoMerge.MIN) and Cout * B < _MAX_GRID_DIM
+        nbytes = _native.indices_bytes(int(merge), geom)
+        should_save = _should_save(merge, bool(save_indices), needs_grad, B, Cout, nbytes)
         out = torch.empty((B, Cout, H, W), dtype=x4c.dtype, device=x4c.device)
-        indices = torch.empty((B, Cout, H, W), dtype=torch.int32, device=x4c.device) if should_save else None
+        # Layout per mca_morpho_indices_bytes: packed int32 winners (max / min) or per-pair taps.
+        indices = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x4c.device) if should_save else None
         replicate = padding == MorphoPadding.REPLICATE
         fill = fill_value(op, padding, padding_value)
         _native.morpho_forward(op, int(merge), replicate, fill, x4c, kernel_weight, wbs, out, indices, geom)
@@ -167,7 +185,7 @@ class _MorphoFunction(torch.autograd.Function):
         fill = fill_value(ctx.op, ctx.padding, ctx.padding_value)
         _native.morpho_backward(ctx.op, ctx.merge, replicate, fill, x4, kernel_weight, wbs, indices, grad_output, grad_input, grad_weight,
                                 geom)
-        return grad_input, grad_weight, None, None, None, None, None, None
+        return grad_input, grad_weight, None, None, None, None, None, None, None
 
 
 def morpho_operation(op: int, input: torch.Tensor, weight: torch.Tensor, merge: int, padding: int, padding_value: float = 0.0,
@@ -189,7 +207,8 @@ def morpho_operation(op: int, input: torch.Tensor, weight: torch.Tensor, merge: 
     if merge == MorphoMerge.IDENTITY:
         _check_identity(x4, w4, smorph=False)
     _check_device(x4, w4, name="morpho_operation_forward_hip")
-    out = _MorphoFunction.apply(x4, w4, op, merge, padding, float(padding_value), bool(save_indices), float(noise_scale))
+    needs_grad = torch.is_grad_enabled() and (input.requires_grad or weight.requires_grad)
+    out = _MorphoFunction.apply(x4, w4, op, merge, padding, float(padding_value), bool(save_indices), float(noise_scale), needs_grad)
     return output_to_original(out, input_dims)
 
 

@@ -393,3 +393,67 @@ def test_config2_full_size_properties():
     gx = xd.grad
     assert torch.equal(gx, gx.round()) and bool((gx >= 0).all())
     assert float(gx.double().sum()) <= 16 * 32 * 32 * 128 * 128
+
+
+# ------------------------------------------------------------------------------------------------
+# Saved per-pair taps (sum / mean / identity) and the recompute path
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("merge", ["sum", "identity"])
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+@pytest.mark.parametrize("shape", [(2, 3, 4, 21, 70, 3, 3), (1, 3, 5, 17, 66, 5, 5), (1, 2, 2, 9, 20, 7, 7), (1, 2, 3, 12, 11, 4, 2),
+                                   (1, 2, 2, 30, 70, 11, 11)])
+def test_saved_pair_taps_are_first_extremal_taps(op, merge, dtype, shape):
+    """The taps the forward saves for the per-pair merges are each pair's first extremal tap (the
+    strict scan of morpho_op_cpu_kernels.hxx:211-252), on quantised inputs full of ties."""
+    _, native, A = _mca()
+    B, Cin, Cout, H, W, KH, KW = shape
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(31, B, Cin, H, W, dtype=dtype, kind="quant")
+    w = (seeded(32, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="quant") * 4).round() / 4
+    dev = torch.device("cuda")
+    geom = (B, Cin, Cout, w.shape[1], H, W, KH, KW)
+    nbytes = native.indices_bytes(O.MERGES[merge], geom)
+    taps = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
+    native.morpho_forward(op, O.MERGES[merge], True, 0.0, x.to(dev), w.to(dev), 0, out, taps, geom)
+    cpair = 1 if merge == "identity" else Cin
+    got = _np(taps).reshape(B, Cout, cpair, H, W)
+    xn, wn = x.numpy(), w.numpy()
+    for b in range(B):
+        for o in range(Cout):
+            for c in range(cpair):
+                i = o if merge == "identity" else c
+                _, arg = O.brute.pair(xn[b, i], wn[o, c], op, O.REPLICATE, 0.0)
+                assert np.array_equal(got[b, o, c], arg), (b, o, c)
+    ref, _ = O.morpho_forward(op, O.MERGES[merge], O.REPLICATE, 0.0, xn, wn)
+    assert np.array_equal(_np(out), ref)
+
+
+@pytest.mark.parametrize("merge", MERGES)
+def test_saved_and_recomputed_winners_give_the_same_gradients(merge):
+    """save_indices=True (winners kept by the forward) and False (recomputed by the backward) give
+    bit-identical gradients; so does a forward run without autograd."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    B, Cin, Cout, H, W, K = 2, 3, 4, 33, 65, 5
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(33, B, Cin, H, W).to(dev)
+    w = seeded(34, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1).to(dev)
+    g = seeded(35, B, Cout, H, W, kind="quant").to(dev)
+    grads = []
+    for save in (True, False):
+        xd = x.clone().requires_grad_(True)
+        wd = w.clone().requires_grad_(True)
+        out = mca.functional.erosion(xd, wd, merge, "replicate", save_indices=save)
+        out.backward(g)
+        grads.append((out.detach(), xd.grad, wd.grad))
+    with torch.no_grad():
+        plain = mca.functional.erosion(x, w, merge, "replicate")
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][0], plain)
+    # Accumulation order of float atomics may differ between runs: compare within the contract.
+    assert normwise_error(_np(grads[0][1]), _np(grads[1][1])) <= 1e-6
+    assert normwise_error(_np(grads[0][2]), _np(grads[1][2])) <= 1e-6

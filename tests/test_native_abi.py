@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 14
+    assert len(symbols) == 15
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -63,8 +63,15 @@ def test_rejects_index_capacity():
     dummy = ctypes.c_void_p(16)
     assert _forward(0, (1, 1, 1, 1, 8, 8, 257, 257), indices=dummy) == 1
     assert "too large to save indices" in _native.lib().mca_last_error().decode()
-    assert _forward(2, indices=dummy) == 1
-    assert "only saved for the max and min merges" in _native.lib().mca_last_error().decode()
+
+
+def test_indices_bytes():
+    lib = _native.lib()
+    B, Cin, Cout, Cw, H, W, KH, KW = GEOM
+    assert lib.mca_morpho_indices_bytes(0, *GEOM) == B * Cout * H * W * 4  # packed int32 winners
+    assert lib.mca_morpho_indices_bytes(2, *GEOM) == B * Cout * Cin * H * W  # one tap byte per pair
+    assert lib.mca_morpho_indices_bytes(5, 2, 3, 3, 1, 16, 16, 3, 3) == 2 * 3 * 16 * 16
+    assert lib.mca_morpho_indices_bytes(3, 1, 2, 2, 2, 4, 4, 17, 17) == 1 * 2 * 2 * 4 * 4 * 2  # 289 taps: uint16
 
 
 def test_rejects_too_large_structuring_element_for_lds():
