@@ -129,6 +129,8 @@ struct OpTraits<EROSION, T>
     static constexpr int sign = -1;
 };
 
+__host__ __device__ inline size_t align16(size_t v) { return (v + 15) / 16 * 16; }
+
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // Value a tap reads at input position (y, x) of `plane`: the pixel, the clamped edge pixel for
@@ -167,6 +169,11 @@ __device__ __forceinline__ void stage_tile(T* tile, const T* __restrict__ plane,
         }
     }
 }
+
+// Gradient accumulators kept in LDS are double, for float and double tensors alike: on gfx950 an
+// LDS float64 atomic add (ds_add_f64) issues in ~10 cycles per wave instruction while the float32
+// one (ds_add_f32) takes ~190 (measured), and the wider sums are also the more accurate.
+using Acc = double;
 
 template <typename T>
 __device__ __forceinline__ void lds_add(T* p, T v)

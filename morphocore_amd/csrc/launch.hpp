@@ -78,7 +78,15 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);
 
+// Slots summed per group by the first stage of a long reduction.
+constexpr int REDUCE_GROUP = 32;
+
+// Scratch bytes reduce_slots_async needs for nslots partial slots of n values.
 template <typename T>
-hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, hipStream_t stream);
+size_t reduce_slots_scratch(int nslots, int64_t n);
+
+// out[j] = sum of part[s * n + j] over the slots s, in a fixed order (deterministic).
+template <typename T>
+hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, T* scratch, hipStream_t stream);
 
 }  // namespace mca

@@ -8,10 +8,11 @@
 // ADD / AVERAGE / IDENTITY (morpho_bwd_taps_kernel): every channel pair routes g * scale to its own
 // first extremal tap (morpho_op_cpu_backward.hxx:90-156, scale = 1 / Cin for AVERAGE). One workgroup
 // per (batch element, tile, group of IG input channels) walks the output channels, reads each pair's
-// saved tap (one byte), accumulates grad_input in an LDS copy of the tile plus halo (flushed once
-// with global atomics, the halo being shared with the neighbouring tiles) and grad_weight in
-// lane-striped LDS bins, written once per chunk of output channels into the workgroup's partial
-// slot. Partial slots are then summed in a fixed order (reduce_slots_async).
+// saved tap (one byte), accumulates grad_input in an LDS copy of the tile plus halo (flushed once:
+// plain stores where only this tile's outputs land, atomics on the halo shared with neighbouring
+// tiles) and grad_weight in lane-striped LDS bins, written once per chunk of output channels into
+// the workgroup's partial slot. Partial slots are then summed in a fixed order (reduce_slots_async).
+// LDS accumulators are double (see Acc).
 //
 // A tap that read outside the image (including REPLICATE's clamped edge pixel) sends nothing to
 // grad_input; grad_weight always receives sign * g (sign -1 for erosion).
@@ -39,7 +40,7 @@ template <typename T, int OP>
 __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedParams<T> p)
 {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    T* bins = reinterpret_cast<T*>(smem_raw);
+    Acc* bins = reinterpret_cast<Acc*>(smem_raw);
     const Geom g = p.g;
     const int work = xcd_work_index(blockIdx.x, gridDim.x);
     const int chunk = work % p.nchunks;
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
     T* part = p.part + ((int64_t)chunk * g.Cout + o) * nb;
     if (p.lds_bins)
     {
-        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) bins[j] = T(0);
+        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) bins[j] = Acc(0);
         __syncthreads();
     }
     const int64_t total = (int64_t)g.B * plane;
@@ -71,14 +72,14 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
         const int iy = h + ph - kh, ix = wc + pw - kw;
         if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], gv);
         if (p.lds_bins)
-            lds_add(&bins[(int64_t)c * K + k], sign * gv);
+            lds_add(&bins[(int64_t)c * K + k], (Acc)(sign * gv));
         else
             global_add(&part[(int64_t)c * K + k], sign * gv);
     }
     if (p.lds_bins)
     {
         __syncthreads();
-        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) part[j] = bins[j];
+        for (int64_t j = threadIdx.x; j < nb; j += BLOCK) part[j] = (T)bins[j];
     }
 }
 
@@ -106,8 +107,8 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
     const Tiling t = p.t;
     const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
     const int tile_elems = t.rows * t.pitch;
-    T* gx = reinterpret_cast<T*>(smem_raw);
-    T* bins = gx + (size_t)p.ig * tile_elems;
+    Acc* gx = reinterpret_cast<Acc*>(smem_raw);
+    Acc* bins = gx + (size_t)p.ig * tile_elems;
     int* tapinfo = reinterpret_cast<int*>(bins + (size_t)p.oc * p.ig * K * p.ncopy);
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int work = xcd_work_index(blockIdx.x, gridDim.x);
@@ -129,36 +130,57 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
     const AT* __restrict__ taps = static_cast<const AT*>(p.taps);
 
     for (int k = threadIdx.x; k < K; k += BLOCK) tapinfo[k] = ((k / g.KW) << 16) | (k % g.KW);
-    for (int j = threadIdx.x; j < p.ig * tile_elems; j += BLOCK) gx[j] = T(0);
+    for (int j = threadIdx.x; j < p.ig * tile_elems; j += BLOCK) gx[j] = Acc(0);
     const int nbins = p.oc * p.ig * K * p.ncopy;
-    for (int j = threadIdx.x; j < nbins; j += BLOCK) bins[j] = T(0);
+    for (int j = threadIdx.x; j < nbins; j += BLOCK) bins[j] = Acc(0);
     __syncthreads();
 
-    // Route the gradient of output channel o, pair with input channel i = i0 + il.
-    auto route = [&](int o, int il, int oc_local, const T (&gr)[RH]) {
-        const int i = i0 + il;
-        const AT* __restrict__ tp = taps + (((int64_t)b * g.Cout + o) * cpair + (IDENT ? 0 : i)) * plane;
-        T* gxl = gx + il * tile_elems;
-        T* bl = bins + (size_t)(oc_local * p.ig + il) * K * p.ncopy;
+    // Every load below reads a valid (clamped) pixel so that the loads of a whole step can be issued
+    // together; pixels outside the image are then masked out with a zero gradient.
+    const int wcc = min(wc, g.W - 1);
+    int64_t pix[RH];
+    bool inside[RH];
+#pragma unroll
+    for (int r = 0; r < RH; ++r)
+    {
+        const int h = h0 + wave * RH + r;
+        pix[r] = (int64_t)min(h, g.H - 1) * g.W + wcc;
+        inside[r] = h < g.H && wc < g.W;
+    }
+    // Taps of the pairs (o, i0 + il) of this lane's RH pixels.
+    auto load_taps = [&](int o, int il, int (&k)[RH]) {
+        const AT* __restrict__ tp = taps + (((int64_t)b * g.Cout + o) * cpair + (IDENT ? 0 : i0 + il)) * plane;
+#pragma unroll
+        for (int r = 0; r < RH; ++r) k[r] = (int)tp[pix[r]];
+    };
+    // Route the gradient of output channel o, pair with input channel i = i0 + il. Straight-line
+    // code: a contribution that must not land (tap outside the image, or a pixel outside it, whose
+    // gradient is 0) adds 0 at its in-tile address instead of branching, so that the loads and LDS
+    // lookups of all RH pixels are issued together.
+    auto route = [&](int il, int oc_local, const T (&gr)[RH], const int (&k)[RH]) {
+        Acc* gxl = gx + il * tile_elems;
+        Acc* bl = bins + (size_t)(oc_local * p.ig + il) * K * p.ncopy;
+        int info[RH];
+#pragma unroll
+        for (int r = 0; r < RH; ++r) info[r] = tapinfo[k[r]];
 #pragma unroll
         for (int r = 0; r < RH; ++r)
         {
             const int h = h0 + wave * RH + r;
-            if (gr[r] == T(0)) continue;  // also every pixel outside the image
-            const int k = (int)tp[(int64_t)h * g.W + wc];
-            const int info = tapinfo[k];
-            const int kh = info >> 16, kw = info & 0xFFFF;
+            const int kh = info[r] >> 16, kw = info[r] & 0xFFFF;
             const int iy = h + ph - kh, ix = wc + pw - kw;
-            if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) lds_add(&gxl[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], gr[r]);
-            lds_add(&bl[k * p.ncopy + copy], sign * gr[r]);
+            const bool lands = iy >= 0 && iy < g.H && ix >= 0 && ix < g.W;
+            lds_add(&gxl[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)(lands ? gr[r] : T(0)));
+            lds_add(&bl[k[r] * p.ncopy + copy], (Acc)(sign * gr[r]));
         }
     };
     auto load_grad = [&](int o, T (&gr)[RH]) {
+        const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + o) * plane;
 #pragma unroll
         for (int r = 0; r < RH; ++r)
         {
-            const int h = h0 + wave * RH + r;
-            gr[r] = (h < g.H && wc < g.W) ? p.gout[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] * p.scale : T(0);
+            const T v = gp[pix[r]];
+            gr[r] = inside[r] ? v * p.scale : T(0);
         }
     };
     // Sum the copies of every bin of output channels [oc0, oc0 + noc) into this workgroup's slot.
@@ -170,51 +192,70 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
             const int k = j % K;
             const int il = (j / K) % p.ig;
             const int ol = j / (K * p.ig);
-            T s = T(0);
+            Acc s = Acc(0);
             for (int c = 0; c < p.ncopy; ++c)
             {
                 s += bins[(size_t)j * p.ncopy + c];
-                bins[(size_t)j * p.ncopy + c] = T(0);
+                bins[(size_t)j * p.ncopy + c] = Acc(0);
             }
             if (il < ni)
             {
                 const int o = IDENT ? i0 + il : oc0 + ol;
-                part[((int64_t)o * g.Cw + (IDENT ? 0 : i0 + il)) * K + k] = s;
+                part[((int64_t)o * g.Cw + (IDENT ? 0 : i0 + il)) * K + k] = (T)s;
             }
         }
         __syncthreads();
     };
 
+    // Steps (output channel, input channel of the group) of one flush chunk, the loads of step s + 1
+    // in flight while step s routes.
+    auto run_chunk = [&](int oc0, int noc) {
+        const int nsteps = IDENT ? ni : noc * ni;
+        auto step_o = [&](int s) { return IDENT ? i0 + s : oc0 + s / ni; };
+        auto step_il = [&](int s) { return IDENT ? s : s % ni; };
+        T gcur[RH];
+        int kcur[RH];
+        load_grad(step_o(0), gcur);
+        load_taps(step_o(0), step_il(0), kcur);
+        for (int s = 0; s < nsteps; ++s)
+        {
+            T gnext[RH];
+            int knext[RH];
+            const bool more = s + 1 < nsteps;
+            if (more)
+            {
+                load_grad(step_o(s + 1), gnext);
+                load_taps(step_o(s + 1), step_il(s + 1), knext);
+            }
+            route(step_il(s), IDENT ? 0 : s / ni, gcur, kcur);
+            if (more)
+            {
+#pragma unroll
+                for (int r = 0; r < RH; ++r)
+                {
+                    gcur[r] = gnext[r];
+                    kcur[r] = knext[r];
+                }
+            }
+        }
+        flush_bins(oc0, IDENT ? 1 : noc);
+    };
     if constexpr (IDENT)
     {
-        for (int il = 0; il < ni; ++il)
-        {
-            T gr[RH];
-            load_grad(i0 + il, gr);
-            route(i0 + il, il, 0, gr);
-        }
-        flush_bins(0, 1);
+        if (ni > 0) run_chunk(0, 1);
     }
     else
     {
-        for (int oc0 = 0; oc0 < g.Cout; oc0 += p.oc)
-        {
-            const int noc = min(p.oc, g.Cout - oc0);
-            for (int ol = 0; ol < noc; ++ol)
-            {
-                T gr[RH];
-                load_grad(oc0 + ol, gr);
-                for (int il = 0; il < ni; ++il) route(oc0 + ol, il, ol, gr);
-            }
-            flush_bins(oc0, noc);
-        }
+        for (int oc0 = 0; oc0 < g.Cout; oc0 += p.oc) run_chunk(oc0, min(p.oc, g.Cout - oc0));
     }
 
-    // grad_input of the tile and its halo (shared with the neighbouring tiles: atomics).
+    // grad_input of the tile and its halo. Rows [KH - 1, th) and columns [KW - 1, 64) of the staged
+    // region receive contributions from this tile's outputs only: plain stores. The rest is shared
+    // with the neighbouring tiles' footprints: atomics onto the zero-filled gradient.
     for (int il = 0; il < ni; ++il)
     {
         T* gplane = p.gin + ((int64_t)b * g.Cin + i0 + il) * plane;
-        const T* gxl = gx + il * tile_elems;
+        const Acc* gxl = gx + il * tile_elems;
         for (int ly = wave; ly < t.rows; ly += NWAVES)
         {
             const int iy = y0 + ly;
@@ -223,8 +264,12 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
             {
                 const int ix = x0 + lx;
                 if (ix < 0 || ix >= g.W) continue;
-                const T v = gxl[ly * t.pitch + lx];
-                if (v != T(0)) global_add(&gplane[(int64_t)iy * g.W + ix], v);
+                const T v = (T)gxl[ly * t.pitch + lx];
+                const bool own = ly >= g.KH - 1 && ly < t.th && lx >= g.KW - 1 && lx < TILE_W;
+                if (own)
+                    gplane[(int64_t)iy * g.W + ix] = v;
+                else if (v != T(0))
+                    global_add(&gplane[(int64_t)iy * g.W + ix], v);
             }
         }
     }
@@ -256,8 +301,8 @@ static PackedPlan plan_packed(const Geom& g)
     if (nchunks < 1) nchunks = 1;
     s.nchunks = (int)nchunks;
     s.chunk = (total + nchunks - 1) / nchunks;
-    const size_t bins = (size_t)g.Cin * g.taps() * sizeof(T);
-    s.lds_bins = bins <= (size_t)48 * 1024;
+    const size_t bins = (size_t)g.Cin * g.taps() * sizeof(Acc);
+    s.lds_bins = bins <= LDS_LIMIT;
     s.lds = s.lds_bins ? bins : 0;
     s.part_bytes = (size_t)nchunks * wnumel * sizeof(T);
     return s;
@@ -276,31 +321,31 @@ static TapsPlan plan_taps(int merge, const Geom& g)
 {
     TapsPlan s{};
     s.t = make_tiling(g, rows_per_wave<T>());
-    const size_t tile = (size_t)s.t.rows * s.t.pitch * sizeof(T);
+    const size_t tile = (size_t)s.t.rows * s.t.pitch * sizeof(Acc);
     const size_t K = (size_t)g.taps();
-    const size_t budget = 48 * 1024 - K * sizeof(int);
+    const size_t budget = LDS_LIMIT - K * sizeof(int);
     const bool ident = merge == MERGE_IDENTITY;
     s.ncopy = 4;
     s.ig = ident ? 4 : 2;
     // Fewer input channels per workgroup when one tile each does not leave room for the bins of one
     // output channel.
-    while (s.ig > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(T) > budget) s.ig /= 2;
+    while (s.ig > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(Acc) > budget) s.ig /= 2;
     if (s.ig > g.Cin) s.ig = g.Cin > 0 ? g.Cin : 1;
-    while (s.ncopy > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(T) > budget) s.ncopy /= 2;
+    while (s.ncopy > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(Acc) > budget) s.ncopy /= 2;
     if (ident)
     {
         s.oc = 1;
     }
     else
     {
-        const size_t per_oc = (size_t)s.ig * K * s.ncopy * sizeof(T);
+        const size_t per_oc = (size_t)s.ig * K * s.ncopy * sizeof(Acc);
         const size_t room = budget > s.ig * tile ? budget - s.ig * tile : 0;
         s.oc = (int)(room / per_oc);
         if (s.oc > g.Cout) s.oc = g.Cout;
         if (s.oc < 1) s.oc = 1;
     }
     s.nig = (g.Cin + s.ig - 1) / s.ig;
-    s.lds = s.ig * tile + (size_t)s.oc * s.ig * K * s.ncopy * sizeof(T) + K * sizeof(int);
+    s.lds = s.ig * tile + (size_t)s.oc * s.ig * K * s.ncopy * sizeof(Acc) + K * sizeof(int);
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     return s;
 }
@@ -312,10 +357,32 @@ size_t morpho_backward_lds(int merge, const Geom& g)
     return plan_taps<T>(merge, g).lds;
 }
 
+// Partial slots of grad_weight (one per workgroup that writes them) and their count.
+template <typename T>
+static void partials(int merge, const Geom& g, size_t& part_bytes, int& nslots)
+{
+    if (packed_winners(merge))
+    {
+        const PackedPlan s = plan_packed<T>(g);
+        part_bytes = s.part_bytes;
+        nslots = s.nchunks;
+    }
+    else
+    {
+        const TapsPlan s = plan_taps<T>(merge, g);
+        part_bytes = s.part_bytes;
+        nslots = g.B * s.t.ntiles();
+    }
+}
+
+// Workspace layout: [partial slots | reduction scratch | (recomputed winners | scratch output)].
 template <typename T>
 size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
 {
-    size_t bytes = packed_winners(merge) ? align_up(plan_packed<T>(g).part_bytes) : align_up(plan_taps<T>(merge, g).part_bytes);
+    size_t part_bytes;
+    int nslots;
+    partials<T>(merge, g, part_bytes, nslots);
+    size_t bytes = align_up(part_bytes) + align_up(reduce_slots_scratch<T>(nslots, (int64_t)g.Cout * g.Cw * g.taps()));
     if (!has_indices) bytes += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(T));
     return bytes;
 }
@@ -330,9 +397,13 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return fill_async<T>(grad_w, wnumel, T(0), stream);
 
     const bool packed = packed_winners(merge);
-    const size_t part_bytes = packed ? plan_packed<T>(g).part_bytes : plan_taps<T>(merge, g).part_bytes;
+    size_t part_bytes;
+    int nslots;
+    partials<T>(merge, g, part_bytes, nslots);
     T* part = reinterpret_cast<T*>(ws);
     ws += align_up(part_bytes);
+    T* scratch = reinterpret_cast<T*>(ws);
+    ws += align_up(reduce_slots_scratch<T>(nslots, wnumel));
     if (!indices)
     {
         // The forward pass did not keep its winners: recompute them (and a scratch output).
@@ -358,7 +429,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         p.chunk = s.chunk;
         morpho_bwd_packed_kernel<T, OP><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
         if ((err = hipGetLastError()) != hipSuccess) return err;
-        return reduce_slots_async<T>(part, s.nchunks, wnumel, grad_w, stream);
+        return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
     }
 
     const TapsPlan s = plan_taps<T>(merge, g);
@@ -392,7 +463,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
             morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
     }
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    return reduce_slots_async<T>(part, g.B * s.t.ntiles(), wnumel, grad_w, stream);
+    return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
 }
 
 template <typename T>

@@ -290,9 +290,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
     const int tile_elems = t.rows * t.pitch;
     const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
     T* tile = reinterpret_cast<T*>(smem_raw);
-    T* gtile = tile + tile_elems;
-    T* bins = gtile + tile_elems;
-    T* abins = bins + K * p.ncopy;
+    Acc* gtile = reinterpret_cast<Acc*>(smem_raw + align16((size_t)tile_elems * sizeof(T)));
+    Acc* bins = gtile + tile_elems;
+    Acc* abins = bins + K * p.ncopy;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int work = xcd_work_index(blockIdx.x, gridDim.x);
     const int strip = work % p.nstrips;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
     const int copy = lane & (p.ncopy - 1);
     const T nan = std::numeric_limits<T>::quiet_NaN();
 
-    for (int j = threadIdx.x; j < (K + 1) * p.ncopy; j += BLOCK) bins[j] = T(0);
+    for (int j = threadIdx.x; j < (K + 1) * p.ncopy; j += BLOCK) bins[j] = Acc(0);
 
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
         const int wc = w0 + lane;
         __syncthreads();
         stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, nan);
-        for (int j = threadIdx.x; j < tile_elems; j += BLOCK) gtile[j] = T(0);
+        for (int j = threadIdx.x; j < tile_elems; j += BLOCK) gtile[j] = Acc(0);
         __syncthreads();
 
         const int o_begin = MK == MK_IDENT ? i : 0;
@@ -369,28 +369,28 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
                         const T pg = e * scaled[r];
                         const T centered = v - outp[r];
                         const T c = fma(a * pg, centered, pg);
-                        lds_add(&gtile[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], c);
-                        lds_add(&bins[k * p.ncopy + copy], c);
+                        lds_add(&gtile[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)c);
+                        lds_add(&bins[k * p.ncopy + copy], (Acc)c);
                         asum[r] = asum[r] + pg * (v - ref[r]) * centered;
                     }
                 }
             T as = T(0);
 #pragma unroll
             for (int r = 0; r < RH; ++r) as += asum[r];
-            if (as != T(0)) lds_add(&abins[copy], as);
+            if (as != T(0)) lds_add(&abins[copy], (Acc)as);
             __syncthreads();
             for (int j = threadIdx.x; j <= K; j += BLOCK)
             {
-                T s = T(0);
+                Acc s = Acc(0);
                 for (int c = 0; c < p.ncopy; ++c)
                 {
                     s += bins[j * p.ncopy + c];
-                    bins[j * p.ncopy + c] = T(0);
+                    bins[j * p.ncopy + c] = Acc(0);
                 }
                 if (j < K)
-                    part_w[((int64_t)o * g.Cw + wi) * K + j] += s;
+                    part_w[((int64_t)o * g.Cw + wi) * K + j] += (T)s;
                 else
-                    part_a[pair] += s;
+                    part_a[pair] += (T)s;
             }
             __syncthreads();
         }
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
             {
                 const int ix = x0 + lx;
                 if (ix < 0 || ix >= g.W) continue;
-                const T v = gtile[ly * t.pitch + lx];
+                const T v = (T)gtile[ly * t.pitch + lx];
                 if (v != T(0)) global_add(&gplane[(int64_t)iy * g.W + ix], v);
             }
         }
@@ -446,7 +446,7 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g)
     s.part_w_bytes = nslots * wnumel * sizeof(T);
     s.part_a_bytes = nslots * s.npairs * sizeof(T);
     s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
-    s.lds = (2 * (size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(T);
+    s.lds = align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + ((size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(Acc);
     return s;
 }
 
@@ -462,7 +462,10 @@ template <typename T>
 size_t smorph_backward_workspace(int merge, const Geom& g)
 {
     const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g);
-    return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes);
+    const int nslots = g.B * s.nstrips;
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes) +
+           align_up(reduce_slots_scratch<T>(nslots, wnumel > s.npairs ? wnumel : s.npairs));
 }
 
 template <typename T, int MK, bool STATS>
@@ -517,6 +520,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     T* part_w = reinterpret_cast<T*>(ws);
     T* part_a = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes));
     T* counts = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
+    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes));
     const int nslots = g.B * s.nstrips;
     if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
     if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
@@ -565,8 +569,8 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
         default: return hipErrorInvalidValue;
     }
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, stream)) != hipSuccess) return err;
-    return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, stream);
+    if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
+    return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
 }
 
 #define MCA_INSTANTIATE_SMORPH(T)                                                                                                   \

@@ -24,6 +24,21 @@ __global__ __launch_bounds__(BLOCK) void reduce_slots_kernel(const T* __restrict
     }
 }
 
+// First stage of a long reduction: group blockIdx.y sums slots [y * REDUCE_GROUP, (y + 1) *
+// REDUCE_GROUP) in slot order into tmp[y * n + j]; the groups are then summed in group order.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void reduce_groups_kernel(const T* __restrict__ part, int nslots, int64_t n, T* __restrict__ tmp)
+{
+    const int s0 = blockIdx.y * REDUCE_GROUP;
+    const int s1 = min(s0 + REDUCE_GROUP, nslots);
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
+    {
+        T s = T(0);
+        for (int slot = s0; slot < s1; ++slot) s += part[(int64_t)slot * n + j];
+        tmp[(int64_t)blockIdx.y * n + j] = s;
+    }
+}
+
 static int grid_for(int64_t n)
 {
     const int64_t blocks = (n + BLOCK - 1) / BLOCK;
@@ -39,16 +54,32 @@ hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream)
 }
 
 template <typename T>
-hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, hipStream_t stream)
+size_t reduce_slots_scratch(int nslots, int64_t n)
+{
+    return nslots > REDUCE_GROUP ? (size_t)((nslots + REDUCE_GROUP - 1) / REDUCE_GROUP) * (size_t)n * sizeof(T) : 0;
+}
+
+template <typename T>
+hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, T* scratch, hipStream_t stream)
 {
     if (n <= 0) return hipSuccess;
-    reduce_slots_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(part, nslots, n, out);
+    if (nslots <= REDUCE_GROUP)
+    {
+        reduce_slots_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(part, nslots, n, out);
+        return hipGetLastError();
+    }
+    const int groups = (nslots + REDUCE_GROUP - 1) / REDUCE_GROUP;
+    const dim3 grid((unsigned)grid_for(n), (unsigned)groups);
+    reduce_groups_kernel<T><<<grid, BLOCK, 0, stream>>>(part, nslots, n, scratch);
+    reduce_slots_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(scratch, groups, n, out);
     return hipGetLastError();
 }
 
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
 template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
-template hipError_t reduce_slots_async<float>(const float*, int, int64_t, float*, hipStream_t);
-template hipError_t reduce_slots_async<double>(const double*, int, int64_t, double*, hipStream_t);
+template size_t reduce_slots_scratch<float>(int, int64_t);
+template size_t reduce_slots_scratch<double>(int, int64_t);
+template hipError_t reduce_slots_async<float>(const float*, int, int64_t, float*, float*, hipStream_t);
+template hipError_t reduce_slots_async<double>(const double*, int, int64_t, double*, double*, hipStream_t);
 
 }  // namespace mca
