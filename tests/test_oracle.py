@@ -304,3 +304,30 @@ def test_planted_mistakes_are_caught():
     _, ref_idx = O.brute.forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, np.zeros_like(w))
     _, tie_idx = O.morpho_forward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x, np.zeros_like(w), save_indices=True)
     assert np.array_equal(tie_idx, ref_idx) and np.any((ref_idx & 0xFFFF) != 8)
+
+
+@pytest.mark.parametrize("merge", MERGES)
+def test_per_sample_weights_equal_per_sample_calls(merge):
+    """The oracle's per-sample structuring element (weight noise, morpho_op_wrap.hxx:55-64) equals one
+    call per batch element with that element's weight; grad_weight is their sum (the reference's own
+    noise test, test_weight_noise.py:42-60)."""
+    rng = np.random.default_rng(12)
+    B, Cin, Cout, H, W, K = 3, 2, 3, 7, 8, 3
+    if merge == "identity":
+        Cout = Cin
+    Cw = 1 if merge == "identity" else Cin
+    x = rng.standard_normal((B, Cin, H, W))
+    w = rng.standard_normal((Cout, Cw, K, K)) * 0.2
+    sample = w[None] + rng.uniform(-0.05, 0.05, (B, Cout, Cw, K, K))
+    g = rng.standard_normal((B, Cout, H, W))
+    m = O.MERGES[merge]
+    out, idx = O.morpho_forward(O.DILATION, m, O.GEODESIC, 0.0, x, w, save_indices=merge in ("max", "min"), sample_weight=sample)
+    gx, gw = O.morpho_backward(O.DILATION, m, O.GEODESIC, 0.0, x, w, g, indices=idx, sample_weight=sample)
+    gw_sum = np.zeros_like(w)
+    for b in range(B):
+        ob, ib = O.morpho_forward(O.DILATION, m, O.GEODESIC, 0.0, x[b:b + 1], sample[b], save_indices=merge in ("max", "min"))
+        assert np.array_equal(out[b:b + 1], ob)
+        gxb, gwb = O.morpho_backward(O.DILATION, m, O.GEODESIC, 0.0, x[b:b + 1], sample[b], g[b:b + 1], indices=ib)
+        np.testing.assert_allclose(gx[b:b + 1], gxb, rtol=1e-12, atol=1e-12)
+        gw_sum += gwb
+    np.testing.assert_allclose(gw, gw_sum, rtol=1e-12, atol=1e-12)
