@@ -92,24 +92,36 @@ struct TapsParams
     T* __restrict__ part;
     Geom g;
     Tiling t;
-    int ig;     // input channels per workgroup
-    int nig;    // groups of input channels
-    int oc;     // output channels per grad_weight flush
-    int ncopy;  // lane-striped copies of each grad_weight bin (power of two)
+    int ig;           // input channels per workgroup
+    int nig;          // groups of input channels
+    int oc;           // output channels per grad_weight flush
+    int ncopy_log2;   // log2 of the lane-striped copies of each grad_weight bin
+    unsigned kw_div;  // ceil(2^16 / KW): kh = (k * kw_div) >> 16 exactly for every k < 256
     T scale;
 };
 
-template <typename T, int OP, typename AT, bool IDENT, int RH>
+// Bits of v when keep, +0 otherwise (a select the compiler cannot turn into a branch around the
+// load that produced v).
+__device__ __forceinline__ float keep_bits(float v, bool keep) { return __uint_as_float(__float_as_uint(v) & (keep ? ~0u : 0u)); }
+__device__ __forceinline__ double keep_bits(double v, bool keep)
+{
+    return __longlong_as_double(__double_as_longlong(v) & (keep ? ~0ll : 0ll));
+}
+
+// NI: channel pairs routed per step (IG input channels of one output channel; 1 for IDENTITY, whose
+// steps walk the group's channels).
+template <typename T, int OP, typename AT, bool IDENT, int RH, int NI>
 __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams<T> p)
 {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const Geom g = p.g;
     const Tiling t = p.t;
-    const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
+    const int K = g.KH * g.KW;
     const int tile_elems = t.rows * t.pitch;
+    const int ncopy = 1 << p.ncopy_log2;
     Acc* gx = reinterpret_cast<Acc*>(smem_raw);
     Acc* bins = gx + (size_t)p.ig * tile_elems;
-    int* tapinfo = reinterpret_cast<int*>(bins + (size_t)p.oc * p.ig * K * p.ncopy);
+    int* tapoff = reinterpret_cast<int*>(bins + (size_t)p.oc * p.ig * K * ncopy);
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int work = xcd_work_index(blockIdx.x, gridDim.x);
     const int igi = work % p.nig;
@@ -118,25 +130,27 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
     const int b = work / t.ntiles();
     const int ty = tile / t.ntx, tx = tile - ty * t.ntx;
     const int h0 = ty * t.th, w0 = tx * TILE_W, wc = w0 + lane;
-    const int y0 = h0 + ph - (g.KH - 1), x0 = w0 + pw - (g.KW - 1);
+    const int y0 = h0 + g.pad_h() - (g.KH - 1), x0 = w0 + g.pad_w() - (g.KW - 1);
     const int i0 = igi * p.ig;
     const int ni = min(p.ig, g.Cin - i0);
     const int64_t plane = g.plane();
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
     T* part = p.part + ((int64_t)b * t.ntiles() + tile) * wnumel;
-    const T sign = (T)OpTraits<OP, T>::sign;
-    const int copy = lane & (p.ncopy - 1);
+    const int copy = lane & (ncopy - 1);
     const int cpair = IDENT ? 1 : g.Cin;
     const AT* __restrict__ taps = static_cast<const AT*>(p.taps);
 
-    for (int k = threadIdx.x; k < K; k += BLOCK) tapinfo[k] = ((k / g.KW) << 16) | (k % g.KW);
+    // Tap k = kh * KW + kw lands kh * pitch + kw elements before the tap-0 position of the pixel.
+    if constexpr (sizeof(AT) > 1)
+        for (int k = threadIdx.x; k < K; k += BLOCK) tapoff[k] = (k / g.KW) * t.pitch + k % g.KW;
     for (int j = threadIdx.x; j < p.ig * tile_elems; j += BLOCK) gx[j] = Acc(0);
-    const int nbins = p.oc * p.ig * K * p.ncopy;
+    const int nbins = p.oc * p.ig * K * ncopy;
     for (int j = threadIdx.x; j < nbins; j += BLOCK) bins[j] = Acc(0);
     __syncthreads();
 
-    // Every load below reads a valid (clamped) pixel so that the loads of a whole step can be issued
-    // together; pixels outside the image are then masked out with a zero gradient.
+    // Every load reads a valid (clamped) pixel of a valid (clamped) step, so that the loads of a step
+    // are issued unconditionally, one step ahead of their use; pixels outside the image are masked
+    // to a zero gradient where the values are used.
     const int wcc = min(wc, g.W - 1);
     int64_t pix[RH];
     bool inside[RH];
@@ -147,40 +161,57 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
         pix[r] = (int64_t)min(h, g.H - 1) * g.W + wcc;
         inside[r] = h < g.H && wc < g.W;
     }
-    // Taps of the pairs (o, i0 + il) of this lane's RH pixels.
-    auto load_taps = [&](int o, int il, int (&k)[RH]) {
-        const AT* __restrict__ tp = taps + (((int64_t)b * g.Cout + o) * cpair + (IDENT ? 0 : i0 + il)) * plane;
-#pragma unroll
-        for (int r = 0; r < RH; ++r) k[r] = (int)tp[pix[r]];
+    // gx element of tap 0 of this lane's row-r pixel.
+    const int base0 = (wave * RH + g.KH - 1) * t.pitch + lane + g.KW - 1;
+    const int rowskip = t.pitch - g.KW;
+
+    struct Step
+    {
+        T g[RH];
+        int k[NI][RH];
     };
-    // Route the gradient of output channel o, pair with input channel i = i0 + il. Straight-line
-    // code: a contribution that must not land (tap outside the image, or a pixel outside it, whose
-    // gradient is 0) adds 0 at its in-tile address instead of branching, so that the loads and LDS
-    // lookups of all RH pixels are issued together.
-    auto route = [&](int il, int oc_local, const T (&gr)[RH], const int (&k)[RH]) {
-        Acc* gxl = gx + il * tile_elems;
-        Acc* bl = bins + (size_t)(oc_local * p.ig + il) * K * p.ncopy;
-        int info[RH];
-#pragma unroll
-        for (int r = 0; r < RH; ++r) info[r] = tapinfo[k[r]];
-#pragma unroll
-        for (int r = 0; r < RH; ++r)
-        {
-            const int h = h0 + wave * RH + r;
-            const int kh = info[r] >> 16, kw = info[r] & 0xFFFF;
-            const int iy = h + ph - kh, ix = wc + pw - kw;
-            const bool lands = iy >= 0 && iy < g.H && ix >= 0 && ix < g.W;
-            lds_add(&gxl[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)(lands ? gr[r] : T(0)));
-            lds_add(&bl[k[r] * p.ncopy + copy], (Acc)(sign * gr[r]));
-        }
-    };
-    auto load_grad = [&](int o, T (&gr)[RH]) {
+    // Output channel and first channel pair of step s of a chunk of output channels [oc0, oc0 + noc).
+    auto load_step = [&](int oc0, int noc, int s, Step& st) {
+        const int sc = min(s, (IDENT ? ni : noc) - 1);
+        const int o = IDENT ? i0 + sc : oc0 + sc;
         const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + o) * plane;
 #pragma unroll
-        for (int r = 0; r < RH; ++r)
+        for (int r = 0; r < RH; ++r) st.g[r] = gp[pix[r]];
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
         {
-            const T v = gp[pix[r]];
-            gr[r] = inside[r] ? v * p.scale : T(0);
+            const int il = IDENT ? 0 : min(j, ni - 1);
+            const AT* __restrict__ tp = taps + (((int64_t)b * g.Cout + o) * cpair + (IDENT ? 0 : i0 + il)) * plane;
+#pragma unroll
+            for (int r = 0; r < RH; ++r) st.k[j][r] = (int)tp[pix[r]];
+        }
+    };
+    // Route step s: for every pair, g * scale to the pair's tap in grad_input and sign * g * scale to
+    // its grad_weight bin. A tap outside the image lands in the staged halo, outside the image, and
+    // is dropped when the tile is flushed.
+    auto route = [&](const Step& st, int s) {
+        Acc gd[RH];
+#pragma unroll
+        for (int r = 0; r < RH; ++r) gd[r] = (Acc)(keep_bits(st.g[r], inside[r]) * p.scale);
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+        {
+            if (!IDENT && j >= ni) break;
+            const int il = IDENT ? s : j;
+            Acc* gxl = gx + il * tile_elems + base0;
+            Acc* bl = bins + (size_t)((IDENT ? 0 : s) * p.ig + il) * K * ncopy + copy;
+#pragma unroll
+            for (int r = 0; r < RH; ++r)
+            {
+                const int k = st.k[j][r];
+                int off;
+                if constexpr (sizeof(AT) == 1)
+                    off = k + (int)__umul24(__umul24((unsigned)k, p.kw_div) >> 16, (unsigned)rowskip);
+                else
+                    off = tapoff[k];
+                lds_add(&gxl[r * t.pitch - off], gd[r]);
+                lds_add(&bl[k << p.ncopy_log2], OP == DILATION ? gd[r] : -gd[r]);
+            }
         }
     };
     // Sum the copies of every bin of output channels [oc0, oc0 + noc) into this workgroup's slot.
@@ -193,10 +224,10 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
             const int il = (j / K) % p.ig;
             const int ol = j / (K * p.ig);
             Acc s = Acc(0);
-            for (int c = 0; c < p.ncopy; ++c)
+            for (int c = 0; c < ncopy; ++c)
             {
-                s += bins[(size_t)j * p.ncopy + c];
-                bins[(size_t)j * p.ncopy + c] = Acc(0);
+                s += bins[(size_t)j * ncopy + c];
+                bins[(size_t)j * ncopy + c] = Acc(0);
             }
             if (il < ni)
             {
@@ -207,36 +238,18 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
         __syncthreads();
     };
 
-    // Steps (output channel, input channel of the group) of one flush chunk, the loads of step s + 1
-    // in flight while step s routes.
+    // Steps of one flush chunk, ping-ponging two register buffers: the loads of step s + 1 are in
+    // flight while step s routes (the last one re-reads its own step, harmlessly).
     auto run_chunk = [&](int oc0, int noc) {
-        const int nsteps = IDENT ? ni : noc * ni;
-        auto step_o = [&](int s) { return IDENT ? i0 + s : oc0 + s / ni; };
-        auto step_il = [&](int s) { return IDENT ? s : s % ni; };
-        T gcur[RH];
-        int kcur[RH];
-        load_grad(step_o(0), gcur);
-        load_taps(step_o(0), step_il(0), kcur);
-        for (int s = 0; s < nsteps; ++s)
+        const int nsteps = IDENT ? ni : noc;
+        Step a, c;
+        load_step(oc0, noc, 0, a);
+        for (int s = 0; s < nsteps; s += 2)
         {
-            T gnext[RH];
-            int knext[RH];
-            const bool more = s + 1 < nsteps;
-            if (more)
-            {
-                load_grad(step_o(s + 1), gnext);
-                load_taps(step_o(s + 1), step_il(s + 1), knext);
-            }
-            route(step_il(s), IDENT ? 0 : s / ni, gcur, kcur);
-            if (more)
-            {
-#pragma unroll
-                for (int r = 0; r < RH; ++r)
-                {
-                    gcur[r] = gnext[r];
-                    kcur[r] = knext[r];
-                }
-            }
+            load_step(oc0, noc, s + 1, c);
+            route(a, s);
+            load_step(oc0, noc, s + 2, a);
+            if (s + 1 < nsteps) route(c, s + 1);
         }
         flush_bins(oc0, IDENT ? 1 : noc);
     };
@@ -323,29 +336,32 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     s.t = make_tiling(g, rows_per_wave<T>());
     const size_t tile = (size_t)s.t.rows * s.t.pitch * sizeof(Acc);
     const size_t K = (size_t)g.taps();
-    const size_t budget = LDS_LIMIT - K * sizeof(int);
+    const size_t table = align16(K * sizeof(int));
     const bool ident = merge == MERGE_IDENTITY;
+    auto need = [&](int ig, int oc, int ncopy) { return ig * tile + (size_t)oc * ig * K * ncopy * sizeof(Acc) + table; };
+    // Three workgroups per CU (160 KiB of LDS each) when the tiles and the bins of one output channel
+    // fit that share, one launch's maximum otherwise.
+    const size_t target = (160 * 1024) / 3 / 1024 * 1024;
     s.ncopy = 4;
     s.ig = ident ? 4 : 2;
-    // Fewer input channels per workgroup when one tile each does not leave room for the bins of one
-    // output channel.
-    while (s.ig > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(Acc) > budget) s.ig /= 2;
-    if (s.ig > g.Cin) s.ig = g.Cin > 0 ? g.Cin : 1;
-    while (s.ncopy > 1 && s.ig * tile + s.ig * K * s.ncopy * sizeof(Acc) > budget) s.ncopy /= 2;
+    while (s.ig > 1 && s.ig > g.Cin) s.ig /= 2;
+    while (s.ig > 1 && need(s.ig, 1, s.ncopy) > target) s.ig /= 2;
+    while (s.ncopy > 1 && need(s.ig, 1, s.ncopy) > LDS_LIMIT) s.ncopy /= 2;
     if (ident)
     {
         s.oc = 1;
     }
     else
     {
+        const size_t budget = need(s.ig, 1, s.ncopy) <= target ? target : LDS_LIMIT;
         const size_t per_oc = (size_t)s.ig * K * s.ncopy * sizeof(Acc);
-        const size_t room = budget > s.ig * tile ? budget - s.ig * tile : 0;
-        s.oc = (int)(room / per_oc);
+        const size_t fixed = s.ig * tile + table;
+        s.oc = budget > fixed ? (int)((budget - fixed) / per_oc) : 1;
         if (s.oc > g.Cout) s.oc = g.Cout;
         if (s.oc < 1) s.oc = 1;
     }
     s.nig = (g.Cin + s.ig - 1) / s.ig;
-    s.lds = s.ig * tile + (size_t)s.oc * s.ig * K * s.ncopy * sizeof(Acc) + K * sizeof(int);
+    s.lds = need(s.ig, s.oc, s.ncopy);
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     return s;
 }
@@ -443,7 +459,8 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     p.ig = s.ig;
     p.nig = s.nig;
     p.oc = s.oc;
-    p.ncopy = s.ncopy;
+    p.ncopy_log2 = s.ncopy == 4 ? 2 : (s.ncopy == 2 ? 1 : 0);
+    p.kw_div = (65536u + (unsigned)g.KW - 1) / (unsigned)g.KW;
     p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
     constexpr int RH = rows_per_wave<T>();
     const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
@@ -451,16 +468,23 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     if (merge == MERGE_IDENTITY)
     {
         if (wide)
-            morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+            morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
         else
-            morpho_bwd_taps_kernel<T, OP, uint8_t, true, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+            morpho_bwd_taps_kernel<T, OP, uint8_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
+    }
+    else if (s.ig == 2)
+    {
+        if (wide)
+            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+        else
+            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
     }
     else
     {
         if (wide)
-            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
         else
-            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
     }
     if ((err = hipGetLastError()) != hipSuccess) return err;
     return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
