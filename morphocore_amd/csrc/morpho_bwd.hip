@@ -5,14 +5,20 @@
 // pixel), grad_weight into LDS bins that become this workgroup's partial slot.
 // Reference semantics: morpho_op_cpu_backward.hxx:39-88 (run_single_winner).
 //
-// ADD / AVERAGE / IDENTITY (morpho_bwd_taps_kernel): every channel pair routes g * scale to its own
-// first extremal tap (morpho_op_cpu_backward.hxx:90-156, scale = 1 / Cin for AVERAGE). One workgroup
-// per (batch element, tile, group of IG input channels) walks the output channels, reads each pair's
-// saved tap (one byte), accumulates grad_input in an LDS copy of the tile plus halo (flushed once:
-// plain stores where only this tile's outputs land, atomics on the halo shared with neighbouring
-// tiles) and grad_weight in lane-striped LDS bins, written once per chunk of output channels into
-// the workgroup's partial slot. Partial slots are then summed in a fixed order (reduce_slots_async).
-// LDS accumulators are double (see Acc).
+// ADD / AVERAGE / IDENTITY: every channel pair routes g * scale to its own first extremal tap
+// (morpho_op_cpu_backward.hxx:90-156, scale = 1 / Cin for AVERAGE). One workgroup per (batch
+// element, tile, input channels) walks the output channels, reads each pair's saved tap (one byte),
+// accumulates grad_input in LDS over the tile plus halo (flushed once: plain stores where only this
+// tile's outputs land, atomics on the halo shared with neighbouring tiles) and grad_weight in
+// lane-striped LDS bins, written once per chunk of output channels into the workgroup's partial
+// slot. Partial slots are then summed in a fixed order (reduce_slots_async). LDS accumulators are
+// double (see Acc). Two kernels:
+//   morpho_bwd_planes_kernel  ADD / AVERAGE whose KW planes of the tile fit in LDS: one input
+//                             channel per workgroup, grad_input split into one plane per
+//                             structuring-element column, which makes the atomic adds bank-conflict
+//                             free (measured: the scattered adds of one shared tile spend ~3x their
+//                             conflict-free time in bank and address conflicts);
+//   morpho_bwd_taps_kernel    IDENTITY and larger structuring elements: one shared tile per channel.
 //
 // A tap that read outside the image (including REPLICATE's clamped edge pixel) sends nothing to
 // grad_input; grad_weight always receives sign * g (sign -1 for erosion).
@@ -288,6 +294,165 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_taps_kernel(const TapsParams
     }
 }
 
+// Barrier for LDS traffic only: waits for this wave's LDS operations, not for its global loads in
+// flight (prefetched steps stay in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ADD / AVERAGE with small structuring elements: one workgroup per (batch element, tile, input
+// channel i) walks every output channel o, routing the pair (o, i). grad_input accumulates in KW
+// planes of the staged tile: plane kw, row y, column c holds the contributions to staged position
+// (y, c + KW - 1 - kw), so every contribution of a lane lands in the lane's own column of some
+// plane; with plane and row strides multiples of 32 doubles, the 64 lanes of each atomic add hit
+// distinct banks. The planes are summed into grad_input once at the end. Loads run D steps ahead.
+template <typename T, int OP, int RH>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_planes_kernel(const TapsParams<T> p)
+{
+    constexpr int D = 3;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int K = g.KH * g.KW;
+    const int ncopy = 1 << p.ncopy_log2;
+    const int PS = t.rows * WAVE;  // plane stride (elements)
+    Acc* planes = reinterpret_cast<Acc*>(smem_raw);
+    Acc* bins = planes + (size_t)g.KW * PS;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int i = work % g.Cin;
+    work /= g.Cin;
+    const int tile = work % t.ntiles();
+    const int b = work / t.ntiles();
+    const int ty = tile / t.ntx, tx = tile - ty * t.ntx;
+    const int h0 = ty * t.th, w0 = tx * TILE_W, wc = w0 + lane;
+    const int y0 = h0 + g.pad_h() - (g.KH - 1), x0 = w0 + g.pad_w() - (g.KW - 1);
+    const int64_t plane = g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
+    T* part = p.part + ((int64_t)b * t.ntiles() + tile) * wnumel;
+    const int copy = lane & (ncopy - 1);
+    const uint8_t* __restrict__ taps = static_cast<const uint8_t*>(p.taps) + ((int64_t)b * g.Cout * g.Cin + i) * plane;
+    const T* __restrict__ gout = p.gout + (int64_t)b * g.Cout * plane;
+    const int64_t tap_ostride = (int64_t)g.Cin * plane;
+
+    for (int j = threadIdx.x; j < g.KW * PS; j += BLOCK) planes[j] = Acc(0);
+    for (int j = threadIdx.x; j < p.oc * K * ncopy; j += BLOCK) bins[j] = Acc(0);
+    __syncthreads();
+
+    const int wcc = min(wc, g.W - 1);
+    int pix[RH];
+    bool inside[RH];
+#pragma unroll
+    for (int r = 0; r < RH; ++r)
+    {
+        const int h = h0 + wave * RH + r;
+        pix[r] = min(h, g.H - 1) * g.W + wcc;
+        inside[r] = h < g.H && wc < g.W;
+    }
+    const int base0 = (wave * RH + g.KH - 1) * WAVE + lane;
+    const int khstep = g.KW * PS + WAVE;
+
+    struct Step
+    {
+        T g[RH];
+        int k[RH];
+    };
+    // Loads of output channel o (clamped to the last one: the steps past the end re-read it).
+    auto load = [&](int o, Step& st) {
+        o = min(o, g.Cout - 1);
+        const T* __restrict__ gp = gout + (int64_t)o * plane;
+        const uint8_t* __restrict__ tp = taps + (int64_t)o * tap_ostride;
+#pragma unroll
+        for (int r = 0; r < RH; ++r) st.g[r] = gp[pix[r]];
+#pragma unroll
+        for (int r = 0; r < RH; ++r) st.k[r] = (int)tp[pix[r]];
+    };
+    auto flush_bins = [&](int oc0, int noc) {
+        lds_barrier();
+        const int n = noc * K;
+        for (int j = threadIdx.x; j < n; j += BLOCK)
+        {
+            Acc s = Acc(0);
+            for (int c = 0; c < ncopy; ++c)
+            {
+                s += bins[(size_t)j * ncopy + c];
+                bins[(size_t)j * ncopy + c] = Acc(0);
+            }
+            const int ol = j / K, k = j - ol * K;
+            part[((int64_t)(oc0 + ol) * g.Cw + i) * K + k] = (T)s;
+        }
+        lds_barrier();
+    };
+    int oc0 = 0;
+    auto step = [&](const Step& st, int o) {
+        if (o >= g.Cout) return;
+        Acc* bl = bins + (size_t)(o - oc0) * K * ncopy + copy;
+#pragma unroll
+        for (int r = 0; r < RH; ++r)
+        {
+            const Acc gd = (Acc)(keep_bits(st.g[r], inside[r]) * p.scale);
+            // Tap k = kh * KW + kw lands kw * PS - kh * 64 elements from the pixel's tap-0 position.
+            const int k = st.k[r];
+            const unsigned kh = __umul24((unsigned)k, p.kw_div) >> 16;
+            const int off = (int)__umul24((unsigned)k, (unsigned)PS) - (int)__umul24(kh, (unsigned)khstep);
+            lds_add(&planes[base0 + r * WAVE + off], gd);
+            lds_add(&bl[k << p.ncopy_log2], OP == DILATION ? gd : -gd);
+        }
+        if (o + 1 == g.Cout || o + 1 - oc0 == p.oc)
+        {
+            flush_bins(oc0, o + 1 - oc0);
+            oc0 = o + 1;
+        }
+    };
+    // The prologue issues its loads in the loop's order (compiler barriers between the steps), so
+    // that the first iteration waits for no more of them than the later ones do.
+    Step s0, s1, s2, s3;
+    load(0, s0);
+    asm volatile("" ::: "memory");
+    load(1, s1);
+    asm volatile("" ::: "memory");
+    load(2, s2);
+    asm volatile("" ::: "memory");
+    static_assert(D == 3, "four step buffers");
+    for (int o = 0; o < g.Cout; o += D + 1)
+    {
+        load(o + 3, s3);
+        step(s0, o);
+        load(o + 4, s0);
+        step(s1, o + 1);
+        load(o + 5, s1);
+        step(s2, o + 2);
+        load(o + 6, s2);
+        step(s3, o + 3);
+    }
+
+    // grad_input of the tile and its halo: the sum of the planes at each staged position. Rows
+    // [KH - 1, th) and columns [KW - 1, 64) receive contributions from this tile's outputs only:
+    // plain stores. The rest is shared with the neighbouring tiles' footprints: atomics onto the
+    // zero-filled gradient.
+    T* gplane = p.gin + ((int64_t)b * g.Cin + i) * plane;
+    for (int ly = wave; ly < t.rows; ly += NWAVES)
+    {
+        const int iy = y0 + ly;
+        if (iy < 0 || iy >= g.H) continue;
+        for (int lx = lane; lx < t.cols; lx += WAVE)
+        {
+            const int ix = x0 + lx;
+            if (ix < 0 || ix >= g.W) continue;
+            Acc s = Acc(0);
+            for (int kw = 0; kw < g.KW; ++kw)
+            {
+                const int c = lx - (g.KW - 1 - kw);
+                if (c >= 0 && c < WAVE) s += planes[kw * PS + ly * WAVE + c];
+            }
+            const T v = (T)s;
+            const bool own = ly >= g.KH - 1 && ly < t.th && lx >= g.KW - 1 && lx < TILE_W;
+            if (own)
+                gplane[(int64_t)iy * g.W + ix] = v;
+            else if (v != T(0))
+                global_add(&gplane[(int64_t)iy * g.W + ix], v);
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Launch
 // ------------------------------------------------------------------------------------------------
@@ -325,6 +490,7 @@ struct TapsPlan
 {
     Tiling t;
     int ig, nig, oc, ncopy;
+    bool planes;  // morpho_bwd_planes_kernel (else morpho_bwd_taps_kernel)
     size_t part_bytes;
     size_t lds;
 };
@@ -338,10 +504,34 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     const size_t K = (size_t)g.taps();
     const size_t table = align16(K * sizeof(int));
     const bool ident = merge == MERGE_IDENTITY;
-    auto need = [&](int ig, int oc, int ncopy) { return ig * tile + (size_t)oc * ig * K * ncopy * sizeof(Acc) + table; };
-    // Three workgroups per CU (160 KiB of LDS each) when the tiles and the bins of one output channel
-    // fit that share, one launch's maximum otherwise.
+    // Three workgroups per CU (160 KiB of LDS each) when the accumulators of one output channel fit
+    // that share, one launch's maximum otherwise.
     const size_t target = (160 * 1024) / 3 / 1024 * 1024;
+    s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
+    if (!ident && g.plane() <= 0x7fffffff && K <= 256)
+    {
+        // The planes kernel, with 16-row (else 8-row) tiles when KW planes of the tile fit (never
+        // the case for more than 256 taps, which would need two-byte taps).
+        for (int rh = 4; rh >= 2; rh /= 2)
+        {
+            const Tiling t = make_tiling(g, rh);
+            const size_t planes = (size_t)g.KW * t.rows * WAVE * sizeof(Acc);
+            const size_t per_oc = K * 4 * sizeof(Acc);
+            if (planes + per_oc > LDS_LIMIT) continue;
+            const size_t budget = planes + per_oc <= target ? target : LDS_LIMIT;
+            s.t = t;
+            s.planes = true;
+            s.ig = 1;
+            s.nig = g.Cin;
+            s.ncopy = 4;
+            s.oc = (int)((budget - planes) / per_oc);
+            if (s.oc > g.Cout) s.oc = g.Cout;
+            s.lds = planes + (size_t)s.oc * per_oc;
+            s.part_bytes = (size_t)g.B * t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
+            return s;
+        }
+    }
+    auto need = [&](int ig, int oc, int ncopy) { return ig * tile + (size_t)oc * ig * K * ncopy * sizeof(Acc) + table; };
     s.ncopy = 4;
     s.ig = ident ? 4 : 2;
     while (s.ig > 1 && s.ig > g.Cin) s.ig /= 2;
@@ -362,7 +552,6 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     }
     s.nig = (g.Cin + s.ig - 1) / s.ig;
     s.lds = need(s.ig, s.oc, s.ncopy);
-    s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     return s;
 }
 
@@ -459,13 +648,20 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     p.ig = s.ig;
     p.nig = s.nig;
     p.oc = s.oc;
-    p.ncopy_log2 = s.ncopy == 4 ? 2 : (s.ncopy == 2 ? 1 : 0);
+    p.ncopy_log2 = __builtin_ctz((unsigned)s.ncopy);
     p.kw_div = (65536u + (unsigned)g.KW - 1) / (unsigned)g.KW;
     p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
     constexpr int RH = rows_per_wave<T>();
     const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
     const bool wide = pair_tap_bytes(g) == 2;
-    if (merge == MERGE_IDENTITY)
+    if (s.planes)
+    {
+        if (s.t.rh == 4)
+            morpho_bwd_planes_kernel<T, OP, 4><<<blocks, BLOCK, s.lds, stream>>>(p);
+        else
+            morpho_bwd_planes_kernel<T, OP, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+    }
+    else if (merge == MERGE_IDENTITY)
     {
         if (wide)
             morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);

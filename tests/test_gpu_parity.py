@@ -133,6 +133,33 @@ def test_backward_parity(op, merge, padding, dtype):
     assert normwise_error(gw, rgw) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("merge", ["sum", "mean"])
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 3, 7, 37, 70, 5, 5),  # 16-row planes, grad_weight flushed in chunks of 3 output channels
+        (2, 2, 3, 19, 130, 3, 3),  # 16-row planes, one chunk
+        (1, 2, 5, 19, 66, 7, 7),  # 8-row planes
+        (1, 2, 3, 30, 70, 11, 11),  # one shared tile per channel (planes do not fit)
+        (2, 1, 1, 17, 64, 5, 1),  # single channels, one-column element
+        (1, 4, 9, 20, 130, 1, 5),  # one-row element
+    ],
+)
+def test_backward_parity_kernel_variants(shape, op, merge, dtype):
+    """Per-pair merges through each backward kernel layout the launch can choose."""
+    B, Cin, Cout, H, W, KH, KW = shape
+    x = seeded(41, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(42, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="randn", scale=0.2)
+    g = seeded(43, B, Cout, H, W, dtype=dtype, kind="randn")
+    for padding in ("replicate", "geodesic"):
+        out, ref, gx, rgx, gw, rgw = _backward_case(op, merge, padding, dtype, x, w, g)
+        assert np.array_equal(out, ref), padding
+        assert normwise_error(gx, rgx) <= TOL[dtype], padding
+        assert normwise_error(gw, rgw) <= TOL[dtype], padding
+
+
 @pytest.mark.parametrize("save_indices", [True, False])
 @pytest.mark.parametrize("merge", MERGES)
 @pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
