@@ -403,28 +403,34 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
 #pragma unroll
                 for (int r = 0; r < RH; ++r)
                 {
-                    T best = Tr::init();
-                    int krow = 0;
+                    // Row extrema m[kh] (NaN when a whole row is NaN), the pair's extremum from the
+                    // start value, then the first row holding it: rows that hold only NaN never
+                    // compare equal, and a pair that never improves on the start value keeps tap 0.
+                    T m[KH];
 #pragma unroll
                     for (int kh = 0; kh < KH; ++kh)
                     {
-                        T m = Tr::init();
+                        T v[KW];
 #pragma unroll
-                        for (int kw = 0; kw + 1 < KW; kw += 2)
-                            m = Tr::pick(m, Tr::pick(Tr::combine(wnd[r + KH - 1 - kh][kw], wp[kh * KW + kw]),
-                                                     Tr::combine(wnd[r + KH - 1 - kh][kw + 1], wp[kh * KW + kw + 1])));
-                        if constexpr (KW % 2 == 1) m = Tr::pick(m, Tr::combine(wnd[r + KH - 1 - kh][KW - 1], wp[kh * KW + KW - 1]));
-                        if (Tr::better(m, best))
-                        {
-                            best = m;
-                            krow = kh;
-                        }
+                        for (int kw = 0; kw < KW; ++kw) v[kw] = Tr::combine(wnd[r + KH - 1 - kh][kw], wp[kh * KW + kw]);
+                        // A linear chain, which the compiler folds into max3 / min3 pairs.
+                        T mm = v[0];
+#pragma unroll
+                        for (int kw = 1; kw < KW; ++kw) mm = Tr::pick(mm, v[kw]);
+                        m[kh] = mm;
                     }
+                    T best = Tr::init();
+#pragma unroll
+                    for (int kh = 0; kh < KH; ++kh) best = Tr::pick(best, m[kh]);
+                    int krow = 0;
+#pragma unroll
+                    for (int kh = KH - 1; kh >= 0; --kh) krow = m[kh] == best ? kh : krow;
                     const T* xrow = tb + (r + KH - 1 - krow) * COLS;
                     const T* wrow = wp + krow * KW;
-                    int arg = krow * KW;
+                    int kcol = 0;
 #pragma unroll
-                    for (int kw = KW - 1; kw >= 0; --kw) arg = Tr::combine(xrow[-kw], wrow[kw]) == best ? krow * KW + kw : arg;
+                    for (int kw = KW - 1; kw >= 0; --kw) kcol = Tr::combine(xrow[-kw], wrow[kw]) == best ? kw : kcol;
+                    int arg = krow * KW + kcol;
                     if (best == Tr::init()) arg = 0;
                     merge_pair<T, MK>(best, i, acc[ob][r], win[ob][r]);
                     const int h = h0 + wave * RH + r;
