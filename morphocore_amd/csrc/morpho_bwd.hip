@@ -18,7 +18,10 @@
 //                             structuring-element column, which makes the atomic adds bank-conflict
 //                             free (measured: the scattered adds of one shared tile spend ~3x their
 //                             conflict-free time in bank and address conflicts);
-//   morpho_bwd_taps_kernel    IDENTITY and larger structuring elements: one shared tile per channel.
+//   morpho_bwd_ident_gather_kernel  IDENTITY 3x3 / 5x5: grad_input gathered per input pixel from
+//                             the taps of its window, written once (no fill, no atomics);
+//   morpho_bwd_taps_kernel    other IDENTITY and larger structuring elements: one shared tile per
+//                             channel.
 //
 // A tap that read outside the image (including REPLICATE's clamped edge pixel) sends nothing to
 // grad_input; grad_weight always receives sign * g (sign -1 for erosion).
@@ -453,6 +456,90 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_planes_kernel(const TapsPara
     }
 }
 
+// IDENTITY with 3x3 and 5x5 structuring elements, in gather form: output channel c reads
+// input channel c only, so the grad_input of pixel q is the sum of g(p) over the window pixels
+// p = q + (kh - KH/2, kw - KW/2) whose saved tap is k = kh * KW + kw, the tap that read q (a tap that
+// read outside the image matches no pixel). One workgroup per (batch element, channel, tile)
+// stages g and the taps of the tile plus halo in LDS, gathers from a register window, and writes
+// each grad_input pixel of the tile once: no zero fill, no atomics on grad_input. grad_weight sums
+// sign * g by saved tap in LDS bins with one copy per lane of a half wave (conflict free), one
+// partial slot per (batch element, tile). IDENTITY has no 1 / Cin scale.
+template <typename T, int OP, int KH, int KW, int RH>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const TapsParams<T> p)
+{
+    constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
+    constexpr int TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, WR = RH + KH - 1;
+    constexpr int NC = 32;
+    __shared__ T gs[ROWS * COLS];
+    __shared__ int ts[ROWS * COLS];
+    __shared__ Acc bins[K * NC];
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int c = work % g.Cin;
+    work /= g.Cin;
+    const int tile = work % t.ntiles();
+    const int b = work / t.ntiles();
+    const int ty = tile / t.ntx, tx = tile - ty * t.ntx;
+    const int h0 = ty * TH, w0 = tx * TILE_W;
+    const int y0 = h0 - PH, x0 = w0 - PW;
+    const int64_t plane = g.plane();
+    const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + c) * plane;
+    const uint8_t* __restrict__ tp = static_cast<const uint8_t*>(p.taps) + ((int64_t)b * g.Cout + c) * plane;
+
+    for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
+    // Output pixels of the tile plus halo; outside the image: no gradient, a tap that matches none.
+    for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+    {
+        const int ly = idx / COLS, lx = idx - ly * COLS;
+        const int y = y0 + ly, x = x0 + lx;
+        const bool in = y >= 0 && y < g.H && x >= 0 && x < g.W;
+        const int64_t o = in ? (int64_t)y * g.W + x : 0;
+        const T gv = gp[o];
+        const int tv = tp[o];
+        gs[idx] = in ? gv : T(0);
+        ts[idx] = in ? tv : -1;
+    }
+    __syncthreads();
+
+    T gw[WR][KW];
+    int tw[WR][KW];
+#pragma unroll
+    for (int rr = 0; rr < WR; ++rr)
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            gw[rr][kw] = gs[(wave * RH + rr) * COLS + lane + kw];
+            tw[rr][kw] = ts[(wave * RH + rr) * COLS + lane + kw];
+        }
+    T* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + c) * plane;
+    const int wc = w0 + lane;
+    Acc* bl = bins + (lane & (NC - 1));
+#pragma unroll
+    for (int r = 0; r < RH; ++r)
+    {
+        // Window rows r .. r + KH - 1 hold the pixels p of q = (row r, this lane's column).
+        Acc s = Acc(0);
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw) s += tw[r + kh][kw] == kh * KW + kw ? (Acc)gw[r + kh][kw] : Acc(0);
+        const int h = h0 + wave * RH + r;
+        if (h < g.H && wc < g.W) gplane[(int64_t)h * g.W + wc] = (T)s;
+        // grad_weight: this lane's own output pixel (h, wc), staged at (row r + PH, column PW).
+        const int k = tw[r + PH][PW];
+        if (k >= 0) lds_add(&bl[k * NC], (Acc)(OP == DILATION ? gw[r + PH][PW] : -gw[r + PH][PW]));
+    }
+    __syncthreads();
+    if (threadIdx.x < K)
+    {
+        Acc s = Acc(0);
+        for (int j = 0; j < NC; ++j) s += bins[threadIdx.x * NC + j];
+        p.part[((int64_t)b * t.ntiles() + tile) * g.Cout * K + (int64_t)c * K + threadIdx.x] = (T)s;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Launch
 // ------------------------------------------------------------------------------------------------
@@ -490,7 +577,8 @@ struct TapsPlan
 {
     Tiling t;
     int ig, nig, oc, ncopy;
-    bool planes;  // morpho_bwd_planes_kernel (else morpho_bwd_taps_kernel)
+    bool planes;  // morpho_bwd_planes_kernel
+    bool gather;  // morpho_bwd_ident_gather_kernel (else morpho_bwd_taps_kernel)
     size_t part_bytes;
     size_t lds;
 };
@@ -508,6 +596,16 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     // that share, one launch's maximum otherwise.
     const size_t target = (160 * 1024) / 3 / 1024 * 1024;
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
+    if (ident && g.KH == g.KW && (g.KH == 3 || g.KH == 5))
+    {
+        s.gather = true;
+        s.ig = 1;
+        s.nig = g.Cin;
+        s.oc = 1;
+        s.ncopy = 32;
+        s.lds = 0;  // static
+        return s;
+    }
     if (!ident && g.plane() <= 0x7fffffff && K <= 256)
     {
         // The planes kernel, with 16-row (else 8-row) tiles when KW planes of the tile fit (never
@@ -598,10 +696,13 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
 {
     hipError_t err;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
-    if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
+    const bool packed = packed_winners(merge);
+    // The gather kernel writes every grad_input pixel itself; the others accumulate onto zeros.
+    const bool gather = !packed && (int64_t)g.B * g.Cout * g.plane() > 0 && plan_taps<T>(merge, g).gather;
+    if (!gather)
+        if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return fill_async<T>(grad_w, wnumel, T(0), stream);
 
-    const bool packed = packed_winners(merge);
     size_t part_bytes;
     int nslots;
     partials<T>(merge, g, part_bytes, nslots);
@@ -654,7 +755,15 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     constexpr int RH = rows_per_wave<T>();
     const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
     const bool wide = pair_tap_bytes(g) == 2;
-    if (s.planes)
+    if (s.gather)
+    {
+        switch (g.KH)
+        {
+            case 3: morpho_bwd_ident_gather_kernel<T, OP, 3, 3, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+            default: morpho_bwd_ident_gather_kernel<T, OP, 5, 5, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+        }
+    }
+    else if (s.planes)
     {
         if (s.t.rh == 4)
             morpho_bwd_planes_kernel<T, OP, 4><<<blocks, BLOCK, s.lds, stream>>>(p);

@@ -160,6 +160,30 @@ def test_backward_parity_kernel_variants(shape, op, merge, dtype):
         assert normwise_error(gw, rgw) <= TOL[dtype], padding
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 3, 37, 70, 3, 3),  # gathered grad_input
+        (1, 4, 19, 130, 5, 5),  # gathered grad_input
+        (1, 2, 19, 66, 7, 7),  # scattered (shared tile per channel)
+        (1, 2, 20, 70, 5, 3),  # scattered
+        (1, 1, 3, 4, 5, 5),  # element larger than the image
+    ],
+)
+def test_backward_parity_identity_variants(shape, op, dtype):
+    B, C, H, W, KH, KW = shape
+    x = seeded(44, B, C, H, W, dtype=dtype, kind="randn")
+    w = seeded(45, *_weight_shape("identity", C, C, KH, KW), dtype=dtype, kind="randn", scale=0.2)
+    g = seeded(46, B, C, H, W, dtype=dtype, kind="randn")
+    for padding in PADDINGS:
+        out, ref, gx, rgx, gw, rgw = _backward_case(op, "identity", padding, dtype, x, w, g)
+        assert np.array_equal(out, ref), padding
+        assert normwise_error(gx, rgx) <= TOL[dtype], padding
+        assert normwise_error(gw, rgw) <= TOL[dtype], padding
+
+
 @pytest.mark.parametrize("save_indices", [True, False])
 @pytest.mark.parametrize("merge", MERGES)
 @pytest.mark.parametrize("op", [O.DILATION, O.EROSION])
