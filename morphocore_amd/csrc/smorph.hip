@@ -17,106 +17,10 @@
 // to an LDS copy of the tile's grad_input, to lane-striped LDS bins of grad_weight and to the
 // pair's grad_alpha (sum of p_k (v_k - ref)(v_k - out) g); the bins become this workgroup's partial
 // slot, summed over slots in a fixed order afterwards.
-#include "launch.hpp"
+#include "smorph_common.hpp"
 
 namespace mca
 {
-
-// The exponential of the reference's CPU smorph (morpho_cpu_simd.hpp:127-169), one lane at a time:
-// Cody-Waite reduction x = n ln2 + r with ln2 split in a high and a low part, exp(r) by its Taylor
-// series in Horner form with fused multiply-adds (degree 7 for float, 13 for double, coefficients
-// 1/k! by repeated division in the element type), 2^n assembled in the exponent bits; inputs below
-// the log of the smallest normal give 0, inputs above the overflow threshold are clamped.
-// The kernels need these exact roundings: the smorph gradients scale the rounding error of each
-// pair's output by alpha, so an exponential that differs by an ulp (even a correctly rounded one)
-// moves float32 gradients by ~1e-6 relative at |alpha| = 20.
-template <typename T>
-struct ExpConsts;
-
-template <>
-struct ExpConsts<float>
-{
-    using Bits = int32_t;
-    static constexpr int degree = 7;
-    static constexpr float max_input = 88.0f, min_input = -87.33654f;
-    static constexpr float log2e = 1.44269504088896340736f;
-    static constexpr float ln2_hi = 0.693359375f, ln2_lo = -2.12194440e-4f;
-    static constexpr float magic = 12582912.0f;  // 1.5 * 2^23: adding then subtracting rounds to an integer
-    static constexpr int mant = 23, bias = 127;
-};
-
-template <>
-struct ExpConsts<double>
-{
-    using Bits = int64_t;
-    static constexpr int degree = 13;
-    static constexpr double max_input = 709.0, min_input = -708.39641;
-    static constexpr double log2e = 1.44269504088896340736;
-    static constexpr double ln2_hi = 6.93145751953125e-1, ln2_lo = 1.42860682030941723212e-6;
-    static constexpr double magic = 6755399441055744.0;  // 1.5 * 2^52
-    static constexpr int mant = 52, bias = 1023;
-};
-
-template <typename T, int K>
-struct InvFact
-{
-    static constexpr T value = InvFact<T, K - 1>::value / T(K);
-};
-
-template <typename T>
-struct InvFact<T, 0>
-{
-    static constexpr T value = T(1);
-};
-
-template <typename T, int K>
-__device__ __forceinline__ T horner(T r)
-{
-    if constexpr (K == ExpConsts<T>::degree)
-        return InvFact<T, K>::value;
-    else
-        return fma(horner<T, K + 1>(r), r, InvFact<T, K>::value);
-}
-
-template <typename T>
-__device__ __forceinline__ T exp_t(T x)
-{
-    using C = ExpConsts<T>;
-    using Bits = typename C::Bits;
-    const T xc = fmin(fmax(x, C::min_input), C::max_input);
-    const T nm = fma(xc, C::log2e, C::magic);
-    const T n = nm - C::magic;
-    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));
-    const T p = horner<T, 0>(r);
-    // The low bits of nm hold n (two's complement): shifting them into the exponent field and
-    // adding the bias builds 2^n without a float to int conversion.
-    const Bits bits = (Bits)(((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant) + ((uint64_t)C::bias << C::mant));
-    const T scale = x < C::min_input ? T(0) : __builtin_bit_cast(T, bits);
-    return p * scale;
-}
-
-// Tolerance within which a channel counts as a MAX / MIN winner (reference: smorph.cu:7-9,
-// smorph_cpu_kernels.hxx:622-627).
-template <typename T>
-__device__ __forceinline__ bool is_winner(T out, T target)
-{
-    const T d = out - target;
-    const T tol = T(1e-6);
-    return d < tol && d > -tol;
-}
-
-template <typename T>
-struct SmorphFwdParams
-{
-    const T* __restrict__ x;
-    const T* __restrict__ w;
-    const T* __restrict__ alpha;
-    T* __restrict__ out;           // forward output, or the winner counts in STATS mode
-    const T* __restrict__ target;  // STATS mode: the forward output
-    Geom g;
-    Tiling t;
-    int average;
-};
 
 // ref, S and W of one pair for the RH pixels of this lane, from the staged tile.
 template <typename T, int RH>
@@ -259,27 +163,6 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
         p.out[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = v;
     }
 }
-
-template <typename T>
-struct SmorphBwdParams
-{
-    const T* __restrict__ x;
-    const T* __restrict__ w;
-    const T* __restrict__ alpha;
-    const T* __restrict__ out;     // forward output (MAX / MIN)
-    const T* __restrict__ counts;  // winner counts (MAX / MIN)
-    const T* __restrict__ gout;
-    T* __restrict__ gin;
-    T* __restrict__ part_w;
-    T* __restrict__ part_a;
-    Geom g;
-    Tiling t;
-    int nstrips;
-    int tps;
-    int ncopy;
-    int npairs;
-    T scale;
-};
 
 template <typename T, int MK, int RH>
 __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams<T> p)
@@ -430,12 +313,14 @@ template <typename T>
 static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g)
 {
     SmorphBwdPlan s{};
-    s.t = make_tiling(g, rows_per_wave<T>());
+    // The static kernels (smorph_static.hip) use one output row per wave and static LDS.
+    const bool stat = smorph_static_supported<T>(g);
+    s.t = make_tiling(g, stat ? 1 : rows_per_wave<T>());
     s.ncopy = 16;
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
     const int64_t units = (int64_t)g.B * g.Cin;
     const int ntiles = s.t.ntiles();
-    int64_t nstrips = (2048 + units - 1) / units;
+    int64_t nstrips = ((stat ? 8192 : 2048) + units - 1) / units;
     if (nstrips > ntiles) nstrips = ntiles;
     if (nstrips < 1) nstrips = 1;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
@@ -446,7 +331,8 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g)
     s.part_w_bytes = nslots * wnumel * sizeof(T);
     s.part_a_bytes = nslots * s.npairs * sizeof(T);
     s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
-    s.lds = align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + ((size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(Acc);
+    s.lds = stat ? 0
+                 : align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + ((size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(Acc);
     return s;
 }
 
@@ -454,6 +340,7 @@ template <typename T>
 size_t smorph_lds(int merge, const Geom& g, bool backward)
 {
     if (backward) return plan_smorph_bwd<T>(merge, g).lds;
+    if (smorph_static_supported<T>(g)) return 0;  // static LDS
     const Tiling t = make_tiling(g, rows_per_wave<T>());
     return (size_t)t.rows * t.pitch * sizeof(T);
 }
@@ -471,6 +358,8 @@ size_t smorph_backward_workspace(int merge, const Geom& g)
 template <typename T, int MK, bool STATS>
 static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t stream)
 {
+    if constexpr (sizeof(T) == 4)
+        if (smorph_static_supported<T>(p.g)) return launch_smorph_fwd_static(MK, STATS, p, stream);
     constexpr int RH = rows_per_wave<T>();
     const int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout;
     const size_t lds = (size_t)p.t.rows * p.t.pitch * sizeof(T);
@@ -489,7 +378,8 @@ hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* 
     p.out = out;
     p.target = nullptr;
     p.g = g;
-    p.t = make_tiling(g, rows_per_wave<T>());
+    // The static kernels (smorph_static.hip) put one output row on each wave.
+    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
     p.average = merge == MERGE_AVERAGE;
     switch (merge)
     {
@@ -534,7 +424,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
         f.out = counts;
         f.target = out;
         f.g = g;
-        f.t = make_tiling(g, rows_per_wave<T>());
+        f.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
         f.average = 0;
         err = merge == MERGE_MAX ? launch_smorph_fwd<T, MK_MAX, true>(f, stream) : launch_smorph_fwd<T, MK_MIN, true>(f, stream);
         if (err != hipSuccess) return err;
@@ -557,6 +447,16 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     p.ncopy = s.ncopy;
     p.npairs = s.npairs;
     p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
+    const int mk = merge == MERGE_MAX ? MK_MAX : (merge == MERGE_MIN ? MK_MIN : (merge == MERGE_IDENTITY ? MK_IDENT : MK_SUM));
+    if constexpr (sizeof(T) == 4)
+    {
+        if (smorph_static_supported<T>(g))
+        {
+            if ((err = launch_smorph_bwd_static(mk, p, stream)) != hipSuccess) return err;
+            if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
+            return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
+        }
+    }
     constexpr int RH = rows_per_wave<T>();
     const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
     switch (merge)

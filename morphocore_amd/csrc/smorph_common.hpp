@@ -1,0 +1,161 @@
+// Definitions shared by the smorph kernels (smorph.hip: any structuring-element size; smorph_static.hip:
+// the common square sizes in float32).
+#pragma once
+
+#include "launch.hpp"
+
+namespace mca
+{
+
+// The exponential of the reference's CPU smorph (morpho_cpu_simd.hpp:127-169), one lane at a time:
+// Cody-Waite reduction x = n ln2 + r with ln2 split in a high and a low part, exp(r) by its Taylor
+// series in Horner form with fused multiply-adds (degree 7 for float, 13 for double, coefficients
+// 1/k! by repeated division in the element type), 2^n assembled in the exponent bits; inputs below
+// the log of the smallest normal give 0, inputs above the overflow threshold are clamped.
+// The kernels need these exact roundings: the smorph gradients scale the rounding error of each
+// pair's output by alpha, so an exponential that differs by an ulp (even a correctly rounded one)
+// moves float32 gradients by ~1e-6 relative at |alpha| = 20.
+template <typename T>
+struct ExpConsts;
+
+template <>
+struct ExpConsts<float>
+{
+    using Bits = int32_t;
+    static constexpr int degree = 7;
+    static constexpr float max_input = 88.0f, min_input = -87.33654f;
+    static constexpr float log2e = 1.44269504088896340736f;
+    static constexpr float ln2_hi = 0.693359375f, ln2_lo = -2.12194440e-4f;
+    static constexpr float magic = 12582912.0f;  // 1.5 * 2^23: adding then subtracting rounds to an integer
+    static constexpr int mant = 23, bias = 127;
+};
+
+template <>
+struct ExpConsts<double>
+{
+    using Bits = int64_t;
+    static constexpr int degree = 13;
+    static constexpr double max_input = 709.0, min_input = -708.39641;
+    static constexpr double log2e = 1.44269504088896340736;
+    static constexpr double ln2_hi = 6.93145751953125e-1, ln2_lo = 1.42860682030941723212e-6;
+    static constexpr double magic = 6755399441055744.0;  // 1.5 * 2^52
+    static constexpr int mant = 52, bias = 1023;
+};
+
+template <typename T, int K>
+struct InvFact
+{
+    static constexpr T value = InvFact<T, K - 1>::value / T(K);
+};
+
+template <typename T>
+struct InvFact<T, 0>
+{
+    static constexpr T value = T(1);
+};
+
+template <typename T, int K>
+__device__ __forceinline__ T horner(T r)
+{
+    if constexpr (K == ExpConsts<T>::degree)
+        return InvFact<T, K>::value;
+    else
+        return fma(horner<T, K + 1>(r), r, InvFact<T, K>::value);
+}
+
+template <typename T>
+__device__ __forceinline__ T exp_t(T x)
+{
+    using C = ExpConsts<T>;
+    using Bits = typename C::Bits;
+    const T xc = fmin(fmax(x, C::min_input), C::max_input);
+    const T nm = fma(xc, C::log2e, C::magic);
+    const T n = nm - C::magic;
+    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));
+    const T p = horner<T, 0>(r);
+    // The low bits of nm hold n (two's complement): shifting them into the exponent field and
+    // adding the bias builds 2^n without a float to int conversion.
+    const Bits bits = (Bits)(((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant) + ((uint64_t)C::bias << C::mant));
+    const T scale = x < C::min_input ? T(0) : __builtin_bit_cast(T, bits);
+    return p * scale;
+}
+
+// Tolerance within which a channel counts as a MAX / MIN winner (reference: smorph.cu:7-9,
+// smorph_cpu_kernels.hxx:622-627).
+template <typename T>
+__device__ __forceinline__ bool is_winner(T out, T target)
+{
+    const T d = out - target;
+    const T tol = T(1e-6);
+    return d < tol && d > -tol;
+}
+
+template <typename T>
+struct SmorphFwdParams
+{
+    const T* __restrict__ x;
+    const T* __restrict__ w;
+    const T* __restrict__ alpha;
+    T* __restrict__ out;           // forward output, or the winner counts in STATS mode
+    const T* __restrict__ target;  // STATS mode: the forward output
+    Geom g;
+    Tiling t;
+    int average;
+};
+
+// The same exponential for the arguments the smorph kernels pass, alpha (v - ref) with ref the
+// extremum of the window: never positive, or NaN. Bit for bit equal to exp_t on (-inf, max_input];
+// a NaN argument gives NaN, as in the reference (whose range checks let NaN through), and the upper
+// clamp is dropped since no argument reaches it.
+template <typename T>
+__device__ __forceinline__ T exp_ref(T x)
+{
+    using C = ExpConsts<T>;
+    using Bits = typename C::Bits;
+    const bool under = x < C::min_input;
+    const T xc = under ? T(C::min_input) : x;
+    const T nm = fma(xc, C::log2e, C::magic);
+    const T n = nm - C::magic;
+    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));
+    const T p = horner<T, 0>(r);
+    const Bits bits = (Bits)(((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant) + ((uint64_t)C::bias << C::mant));
+    const T scale = under ? T(0) : __builtin_bit_cast(T, bits);
+    return p * scale;
+}
+
+template <typename T>
+struct SmorphBwdParams
+{
+    const T* __restrict__ x;
+    const T* __restrict__ w;
+    const T* __restrict__ alpha;
+    const T* __restrict__ out;     // forward output (MAX / MIN)
+    const T* __restrict__ counts;  // winner counts (MAX / MIN)
+    const T* __restrict__ gout;
+    T* __restrict__ gin;
+    T* __restrict__ part_w;
+    T* __restrict__ part_a;
+    Geom g;
+    Tiling t;
+    int nstrips;
+    int tps;
+    int ncopy;
+    int npairs;
+    T scale;
+};
+
+// Structuring-element sizes with static-size smorph kernels (smorph_static.hip).
+template <typename T>
+inline bool smorph_static_supported(const Geom& g)
+{
+    if constexpr (sizeof(T) != 4)
+        return false;
+    else
+        return g.KH == g.KW && (g.KH == 3 || g.KH == 5 || g.KH == 7 || g.KH == 11) && g.plane() <= 0x7fffffff;
+}
+
+// Launchers of the static-size kernels (smorph_static.hip), float32.
+hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream);
+hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream);
+
+}  // namespace mca

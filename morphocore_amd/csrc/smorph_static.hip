@@ -1,0 +1,577 @@
+// Smorph forward and backward for the common square structuring elements (3, 5, 7, 11) in float32
+// (reference semantics: smorph_cpu_kernels.hxx:14-229, 387-638).
+//
+// Same arithmetic as the any-size kernels of smorph.hip, organised for gfx950's VALU:
+//  * every tap loop is unrolled, and the pair's structuring element and alpha are read from LDS
+//    into vector registers: a VALU operation that reads a scalar register issues at about half the
+//    rate of one whose operands are vector registers or constants (measured on MI355X);
+//  * one output pixel per lane, one output row per wave: the validity of a tap row is uniform over
+//    the wave (a scalar branch), only the KW tap columns carry per-lane masks, and tiles whose
+//    windows lie inside the image take a path without any check. Out-of-image taps are excluded by
+//    position, as in the reference (SmorphBlockMask, smorph_valid_rows); an in-image NaN propagates
+//    as in the reference;
+//  * the backward keeps every tap's e (and v, up to 7x7) in registers between the pass that forms S
+//    and W and the pass that routes the gradient, so each exponential is evaluated once per
+//    backward (the any-size kernel evaluates it twice). Every lane of a wave routes the same tap at
+//    once, so the grad_input and grad_weight LDS atomics hit consecutive or lane-striped addresses
+//    (no bank conflicts).
+#include "smorph_common.hpp"
+
+namespace mca
+{
+
+// Copies of each grad_weight / grad_alpha bin of the backward, one per lane of a half wave.
+constexpr int SMORPH_BIN_COPIES = 32;
+
+namespace
+{
+
+__device__ __forceinline__ float smorph_init(bool dilation_like)
+{
+    return dilation_like ? -std::numeric_limits<float>::infinity() : std::numeric_limits<float>::infinity();
+}
+
+// Validity of this wave's tap rows (bit kh: the input row lies in the image, uniform over the wave)
+// and of this lane's tap columns.
+template <int KH, int KW>
+struct TapMask
+{
+    unsigned rows;
+    bool col[KW];
+
+    __device__ __forceinline__ void init(const Geom& g, int h, int wc)
+    {
+        unsigned r = 0;
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+        {
+            const int y = h + KH / 2 - kh;
+            r |= (y >= 0 && y < g.H) ? 1u << kh : 0u;
+        }
+        rows = __builtin_amdgcn_readfirstlane(r);
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            const int c = wc + KW / 2 - kw;
+            col[kw] = c >= 0 && c < g.W;
+        }
+    }
+    __device__ __forceinline__ bool row(int kh) const { return (rows >> kh) & 1u; }
+};
+
+// Pass 1 of a pair: the extremum of the valid taps (NaN never wins, as with the reference's strict
+// scan). xb: this lane's tap-0 input in the staged tile; tap (kh, kw) reads xb[-(kh * COLS + kw)].
+template <int KH, int KW, bool MASKED>
+__device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bool dil, const TapMask<KH, KW>& tm)
+{
+    constexpr int COLS = TILE_W + KW - 1;
+    float ref = smorph_init(dil);
+    if (dil)
+    {
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+        {
+            if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw)
+            {
+                float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+                if constexpr (MASKED) v = tm.col[kw] ? v : -std::numeric_limits<float>::infinity();
+                ref = fmaxf(ref, v);
+            }
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+        {
+            if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw)
+            {
+                float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+                if constexpr (MASKED) v = tm.col[kw] ? v : std::numeric_limits<float>::infinity();
+                ref = fminf(ref, v);
+            }
+        }
+    }
+    return ref;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------
+// Forward: one workgroup per (batch element, output channel, 64 x 4 tile), walking the input
+// channels with the next channel's tile prefetched into registers.
+// ------------------------------------------------------------------------------------------------
+
+// Pass 2 of a pair: S and W in tap order (kh, then kw), W fused as in the reference's AVX2 build.
+template <int KH, int KW, bool MASKED>
+__device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, float a, float ref, const TapMask<KH, KW>& tm, float& S, float& Wsum)
+{
+    constexpr int COLS = TILE_W + KW - 1;
+    float s = 0.0f, wsum = 0.0f;
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+    {
+        if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            const float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+            const float e = exp_ref((v - ref) * a);
+            if constexpr (MASKED)
+            {
+                s = tm.col[kw] ? s + e : s;
+                wsum = tm.col[kw] ? fmaf(e, v, wsum) : wsum;
+            }
+            else
+            {
+                s = s + e;
+                wsum = fmaf(e, v, wsum);
+            }
+        }
+    }
+    S = s;
+    Wsum = wsum;
+}
+
+template <int MK, int KH, int KW, bool STATS>
+__global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams<float> p)
+{
+    constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
+    constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, ELEMS = ROWS * COLS;
+    constexpr int NS = (ELEMS + BLOCK - 1) / BLOCK;
+    __shared__ float tile[2][ELEMS];
+    __shared__ float wl[2][K + 1];  // the pair's structuring element, then its alpha
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int o = work % g.Cout;
+    work /= g.Cout;
+    const int tx = work % t.ntx;
+    work /= t.ntx;
+    const int ty = work % t.nty;
+    const int b = work / t.nty;
+    const int h0 = ty * TH, w0 = tx * TILE_W;
+    const int y0 = h0 + PH - (KH - 1), x0 = w0 + PW - (KW - 1);
+    const int64_t plane = g.plane();
+    const int h = h0 + wave, wc = w0 + lane;
+    const bool in = h < g.H && wc < g.W;
+    const bool interior = y0 >= 0 && y0 + ROWS <= g.H && x0 >= 0 && x0 + COLS <= g.W;
+    TapMask<KH, KW> tm;
+    tm.init(g, h, wc);
+
+    // Staging plan, the same for every input channel: the clamped in-image offset of each element
+    // this thread stages, and whether it lies in the image (else it stages 0, never read unmasked).
+    int off[NS];
+    bool ok[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+    {
+        const int idx = min((int)threadIdx.x + j * BLOCK, ELEMS - 1);
+        const int ly = idx / COLS, lx = idx - ly * COLS;
+        const int y = y0 + ly, x = x0 + lx;
+        ok[j] = y >= 0 && y < g.H && x >= 0 && x < g.W;
+        off[j] = clampi(y, 0, g.H - 1) * g.W + clampi(x, 0, g.W - 1);
+    }
+    const int i_begin = MK == MK_IDENT ? o : 0;
+    const int i_end = MK == MK_IDENT ? o + 1 : g.Cin;
+    const int wt = min((int)threadIdx.x, K);
+    float pre[NS], wpre;
+    auto load = [&](int i) {
+        i = min(i, i_end - 1);
+        const float* __restrict__ xp = p.x + ((int64_t)b * g.Cin + i) * plane;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) pre[j] = xp[off[j]];
+        const int pair = MK == MK_IDENT ? o : o * g.Cin + i;
+        wpre = wt < K ? p.w[((int64_t)o * g.Cw + (MK == MK_IDENT ? 0 : i)) * K + wt] : p.alpha[pair];
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+        {
+            const int idx = threadIdx.x + j * BLOCK;
+            if (j < NS - 1 || idx < ELEMS) tile[buf][idx] = ok[j] ? pre[j] : 0.0f;
+        }
+        if (threadIdx.x <= K) wl[buf][threadIdx.x] = wpre;
+    };
+
+    float m = STATS ? 0.0f : (MK == MK_MAX ? lowest_of<float>() : (MK == MK_MIN ? max_of<float>() : 0.0f));
+    float tgt = 0.0f;
+    if constexpr (STATS)
+    {
+        if (in) tgt = p.target[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc];
+    }
+
+    load(i_begin);
+    store(0);
+    __syncthreads();
+    for (int i = i_begin; i < i_end; ++i)
+    {
+        const int buf = (i - i_begin) & 1;
+        load(i + 1);  // in flight while this channel computes (the last one re-reads itself)
+        const float* xb = &tile[buf][(wave + KH - 1) * COLS + lane + KW - 1];
+        const float* w = wl[buf];
+        const float a = w[K];
+        const bool dil = a >= 0.0f;
+        float S, Wsum;
+        if (interior)
+        {
+            const float ref = smorph_ref<KH, KW, false>(xb, w, dil, tm);
+            smorph_sums<KH, KW, false>(xb, w, a, ref, tm, S, Wsum);
+        }
+        else
+        {
+            const float ref = smorph_ref<KH, KW, true>(xb, w, dil, tm);
+            smorph_sums<KH, KW, true>(xb, w, a, ref, tm, S, Wsum);
+        }
+        const float inv = 1.0f / S;
+        if constexpr (STATS)
+        {
+            if (is_winner(Wsum * inv, tgt)) m = m + 1.0f;
+        }
+        else if constexpr (MK == MK_MAX)
+        {
+            const float c = Wsum * inv;
+            m = m < c ? c : m;
+        }
+        else if constexpr (MK == MK_MIN)
+        {
+            const float c = Wsum * inv;
+            m = c < m ? c : m;
+        }
+        else if constexpr (MK == MK_SUM)
+        {
+            m = fmaf(Wsum, inv, m);
+        }
+        else
+        {
+            m = Wsum * inv;
+        }
+        if (i + 1 < i_end) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!in) return;
+    float v = m;
+    if constexpr (MK == MK_SUM && !STATS)
+    {
+        if (p.average) v = v / (float)g.Cin;
+    }
+    p.out[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Backward: one workgroup per (batch element, input channel, strip of 64 x 4 tiles), one output row
+// per wave; for each tile it walks every output channel o.
+// ------------------------------------------------------------------------------------------------
+
+// One pair (o, i) at this lane's pixel: the forward's ref, S and W (every tap's e, and v up to 7x7,
+// kept), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input (the LDS tile), to
+// the grad_weight bin of tap k and to grad_alpha (returned: the sum of p_k (v_k - ref)(v_k - out)
+// over the taps). gv is g * scale (0 outside the image); for MAX / MIN it is divided by the pixel's
+// winner count, and only a pair within 1e-6 of the merged output outv routes.
+template <int MK, int KH, int KW, bool MASKED>
+__device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
+                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl)
+{
+    constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
+    constexpr bool KEEPV = false;  // v re-read from LDS in each pass: fewer registers, more waves (measured faster)
+    constexpr bool GATE = MASKED || MK == MK_MAX || MK == MK_MIN;
+    const bool dil = a >= 0.0f;
+    float v[KEEPV ? K : 1], e[K];
+    float ref;
+    if constexpr (KEEPV)
+    {
+        // v of every tap, read once; the extremum over the valid ones.
+        ref = smorph_init(dil);
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw) v[kh * KW + kw] = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+        if (dil)
+        {
+#pragma unroll
+            for (int kh = 0; kh < KH; ++kh)
+            {
+                if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+                for (int kw = 0; kw < KW; ++kw) ref = fmaxf(ref, (!MASKED || tm.col[kw]) ? v[kh * KW + kw] : -std::numeric_limits<float>::infinity());
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int kh = 0; kh < KH; ++kh)
+            {
+                if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+                for (int kw = 0; kw < KW; ++kw) ref = fminf(ref, (!MASKED || tm.col[kw]) ? v[kh * KW + kw] : std::numeric_limits<float>::infinity());
+            }
+        }
+    }
+    else
+    {
+        ref = smorph_ref<KH, KW, MASKED>(xb, wl, dil, tm);
+        // Larger elements re-read v from LDS in each pass: keep the compiler from holding the first
+        // pass's loads in registers across the passes.
+        asm volatile("" ::: "memory");
+    }
+    float s = 0.0f, wsum = 0.0f;
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+    {
+        if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            const int k = kh * KW + kw;
+            const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
+            const float ek = exp_ref((vk - ref) * a);
+            if constexpr (MASKED)
+            {
+                s = tm.col[kw] ? s + ek : s;
+                wsum = tm.col[kw] ? fmaf(ek, vk, wsum) : wsum;
+            }
+            else
+            {
+                s = s + ek;
+                wsum = fmaf(ek, vk, wsum);
+            }
+            e[k] = ek;
+        }
+    }
+    if constexpr (!KEEPV) asm volatile("" ::: "memory");
+    const float inv = 1.0f / s;
+    const float outp = wsum * inv;
+    bool route = in;
+    if constexpr (MK == MK_MAX || MK == MK_MIN)
+    {
+        gv = gv / (cnt > 0.0f ? cnt : 1.0f);
+        route = route && is_winner(outp, outv);
+    }
+    const float scaled = gv * inv;
+    float asum = 0.0f;
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+    {
+        if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            const int k = kh * KW + kw;
+            const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
+            const float pg = e[k] * scaled;
+            const float centered = vk - outp;
+            float c = fmaf(a * pg, centered, pg);
+            float ad = pg * (vk - ref) * centered;
+            if constexpr (GATE)
+            {
+                const bool ok = route && (!MASKED || tm.col[kw]);
+                c = ok ? c : 0.0f;
+                ad = ok ? ad : 0.0f;
+            }
+            lds_add(&gxb[-(kh * COLS + kw)], (Acc)c);
+            lds_add(&bl[k * SMORPH_BIN_COPIES], (Acc)c);
+            asum = asum + ad;
+        }
+    }
+    return asum;
+}
+
+template <int MK, int KH, int KW>
+__global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams<float> p)
+{
+    constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
+    constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
+    constexpr int NC = SMORPH_BIN_COPIES;
+    __shared__ float tile[ROWS * COLS];
+    __shared__ Acc gtile[ROWS * COLS];
+    __shared__ __align__(32) Acc bins[(K + 1) * NC];  // grad_weight bins of the K taps, then grad_alpha; NC copies each
+    __shared__ float wl[2][K + 1];      // structuring element and alpha of the current / next pair
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int strip = work % p.nstrips;
+    work /= p.nstrips;
+    const int i = work % g.Cin;
+    const int b = work / g.Cin;
+    const int64_t plane = g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
+    const int slot = b * p.nstrips + strip;
+    float* __restrict__ part_w = p.part_w + (int64_t)slot * wnumel;
+    float* __restrict__ part_a = p.part_a + (int64_t)slot * p.npairs;
+    const int wi = MK == MK_IDENT ? 0 : i;
+    const int o_begin = MK == MK_IDENT ? i : 0;
+    const int o_end = MK == MK_IDENT ? i + 1 : g.Cout;
+    const float* __restrict__ xp = p.x + ((int64_t)b * g.Cin + i) * plane;
+    float* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + i) * plane;
+    auto pair_index = [&](int o) { return MK == MK_IDENT ? o : o * g.Cin + i; };
+    auto stage_weights = [&](int o, int buf) {
+        if (threadIdx.x < K)
+            wl[buf][threadIdx.x] = p.w[((int64_t)o * g.Cw + wi) * K + threadIdx.x];
+        else if (threadIdx.x == K)
+            wl[buf][K] = p.alpha[pair_index(o)];
+    };
+
+    for (int j = threadIdx.x; j < (K + 1) * NC; j += BLOCK) bins[j] = Acc(0);
+    const int tile_begin = strip * p.tps;
+    const int tile_end = min(tile_begin + p.tps, t.ntiles());
+    const float* xb = tile + (wave + KH - 1) * COLS + lane + KW - 1;
+    Acc* gxb = gtile + (wave + KH - 1) * COLS + lane + KW - 1;
+    Acc* bl = bins + (lane & (NC - 1));
+    for (int tid = tile_begin; tid < tile_end; ++tid)
+    {
+        const int ty = tid / t.ntx, tx = tid - ty * t.ntx;
+        const int h0 = ty * TH, w0 = tx * TILE_W;
+        const int y0 = h0 + PH - (KH - 1), x0 = w0 + PW - (KW - 1);
+        const int h = h0 + wave, wc = w0 + lane;
+        const bool in = h < g.H && wc < g.W;
+        const bool interior = y0 >= 0 && y0 + ROWS <= g.H && x0 >= 0 && x0 + COLS <= g.W;
+        TapMask<KH, KW> tm;
+        tm.init(g, h, wc);
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+        {
+            const int ly = idx / COLS, lx = idx - ly * COLS;
+            const int y = y0 + ly, x = x0 + lx;
+            tile[idx] = (y >= 0 && y < g.H && x >= 0 && x < g.W) ? xp[(int64_t)y * g.W + x] : 0.0f;
+            gtile[idx] = Acc(0);
+        }
+        stage_weights(o_begin, 0);
+        // The output gradient (and, for MAX / MIN, the merged output and winner count) of this lane's
+        // pixel, one output channel ahead.
+        const int64_t pix = (int64_t)min(h, g.H - 1) * g.W + min(wc, g.W - 1);
+        float gv_n = 0.0f, cnt_n = 0.0f, out_n = 0.0f;
+        auto load_g = [&](int o) {
+            o = min(o, o_end - 1);
+            const int64_t oi = ((int64_t)b * g.Cout + o) * plane + pix;
+            gv_n = p.gout[oi];
+            if constexpr (MK == MK_MAX || MK == MK_MIN)
+            {
+                cnt_n = p.counts[oi];
+                out_n = p.out[oi];
+            }
+        };
+        load_g(o_begin);
+        __syncthreads();
+        for (int o = o_begin; o < o_end; ++o)
+        {
+            const int buf = (o - o_begin) & 1;
+            const float gv = in ? gv_n * p.scale : 0.0f, cnt = cnt_n, outv = out_n;
+            load_g(o + 1);
+            const float* w = wl[buf];
+            const float a = w[K];
+            float asum;
+            if (interior)
+                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl);
+            else
+                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl);
+            lds_add(&bl[K * NC], (Acc)asum);
+            if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
+            __syncthreads();
+            // Sum the NC copies of each bin: 8 threads per bin each add 4 adjacent copies (two 16-byte
+            // LDS reads) and clear them, a butterfly over the 8 finishes; the sums go to this
+            // workgroup's slot. (K + 1) * 8 is a multiple of 8, so every group of 8 lanes is whole.
+            static_assert(NC == 32, "8 threads x 4 copies per bin");
+            for (int j = threadIdx.x; j < (K + 1) * 8; j += BLOCK)
+            {
+                double4* q = reinterpret_cast<double4*>(&bins[j * 4]);
+                const double4 c4 = *q;
+                *q = make_double4(0.0, 0.0, 0.0, 0.0);
+                Acc v = (c4.x + c4.y) + (c4.z + c4.w);
+#pragma unroll
+                for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
+                if ((j & 7) == 0)
+                {
+                    const int k = j >> 3;
+                    if (k < K)
+                        global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
+                    else
+                        global_add(&part_a[pair_index(o)], (float)v);
+                }
+            }
+            __syncthreads();
+        }
+        // grad_input of the tile and its halo: every cell may be shared with neighbouring tiles (the
+        // tile is no taller than the element), so all go by atomics onto the zero-filled gradient.
+        for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+        {
+            const int ly = idx / COLS, lx = idx - ly * COLS;
+            const int y = y0 + ly, x = x0 + lx;
+            if (y < 0 || y >= g.H || x < 0 || x >= g.W) continue;
+            const float v = (float)gtile[idx];
+            if (v != 0.0f) global_add(&gplane[(int64_t)y * g.W + x], v);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Launch
+// ------------------------------------------------------------------------------------------------
+
+template <int KS>
+static hipError_t fwd_size(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
+{
+    const unsigned blocks = (unsigned)((int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout);
+    if (stats)
+    {
+        if (mk == MK_MAX)
+            smorph_fwd_static<MK_MAX, KS, KS, true><<<blocks, BLOCK, 0, stream>>>(p);
+        else
+            smorph_fwd_static<MK_MIN, KS, KS, true><<<blocks, BLOCK, 0, stream>>>(p);
+        return hipGetLastError();
+    }
+    switch (mk)
+    {
+        case MK_SUM: smorph_fwd_static<MK_SUM, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_fwd_static<MK_MAX, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_fwd_static<MK_MIN, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_fwd_static<MK_IDENT, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
+{
+    switch (p.g.KH)
+    {
+        case 3: return fwd_size<3>(mk, stats, p, stream);
+        case 5: return fwd_size<5>(mk, stats, p, stream);
+        case 7: return fwd_size<7>(mk, stats, p, stream);
+        default: return fwd_size<11>(mk, stats, p, stream);
+    }
+}
+
+template <int KS>
+static hipError_t bwd_size(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
+{
+    const unsigned blocks = (unsigned)((int64_t)p.g.B * p.g.Cin * p.nstrips);
+    switch (mk)
+    {
+        case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_bwd_static<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
+{
+    switch (p.g.KH)
+    {
+        case 3: return bwd_size<3>(mk, p, stream);
+        case 5: return bwd_size<5>(mk, p, stream);
+        case 7: return bwd_size<7>(mk, p, stream);
+        default: return bwd_size<11>(mk, p, stream);
+    }
+}
+
+}  // namespace mca
