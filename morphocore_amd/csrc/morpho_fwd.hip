@@ -456,6 +456,10 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
 #pragma unroll
             for (int kw = 0; kw < KW; ++kw)
             {
+                // One column at a time: keeps the scheduler from gathering the LDS reads of every
+                // column (window and structuring element) ahead of the arithmetic, which needs more
+                // registers than a SIMD has.
+                __builtin_amdgcn_sched_barrier(0);
                 T col[WR];
 #pragma unroll
                 for (int rr = 0; rr < WR; ++rr) col[rr] = tb[rr * COLS - kw];
@@ -479,7 +483,13 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
 #pragma unroll
             for (int ob = 0; ob < OB; ++ob)
 #pragma unroll
-                for (int r = 0; r < RH; ++r) merge_pair<T, MK>(best[ob][r], i, acc[ob][r], win[ob][r]);
+                for (int r = 0; r < RH; ++r)
+                {
+                    // Pins the column folds before the next tile's LDS store (the compiler would sink
+                    // them past it, keeping every column's window and weights live at once).
+                    asm volatile("" ::"v"(best[ob][r]));
+                    merge_pair<T, MK>(best[ob][r], i, acc[ob][r], win[ob][r]);
+                }
         }
 
         if (more) store(buf ^ 1);
