@@ -10,9 +10,9 @@
 //    windows lie inside the image take a path without any check. Out-of-image taps are excluded by
 //    position, as in the reference (SmorphBlockMask, smorph_valid_rows); an in-image NaN propagates
 //    as in the reference;
-//  * the backward keeps every tap's e (and v, up to 7x7) in registers between the pass that forms S
-//    and W and the pass that routes the gradient, so each exponential is evaluated once per
-//    backward (the any-size kernel evaluates it twice). Every lane of a wave routes the same tap at
+//  * the backward keeps every tap's e in registers (up to 7x7) between the pass that forms S and W
+//    and the pass that routes the gradient, so each exponential is evaluated once per backward
+//    (11x11 re-evaluates it: 121 more registers cost more waves than the exponentials cost VALU). Every lane of a wave routes the same tap at
 //    once, so the grad_input and grad_weight LDS atomics hit consecutive or lane-striped addresses
 //    (no bank conflicts).
 #include "smorph_common.hpp"
@@ -283,7 +283,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     constexpr bool KEEPV = false;  // v re-read from LDS in each pass: fewer registers, more waves (measured faster)
     constexpr bool GATE = MASKED || MK == MK_MAX || MK == MK_MIN;
     const bool dil = a >= 0.0f;
-    float v[KEEPV ? K : 1], e[K];
+    float v[KEEPV ? K : 1], e[K <= 49 ? K : 1];
     float ref;
     if constexpr (KEEPV)
     {
@@ -342,7 +342,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
                 s = s + ek;
                 wsum = fmaf(ek, vk, wsum);
             }
-            e[k] = ek;
+            if constexpr (K <= 49) e[k] = ek;
         }
     }
     if constexpr (!KEEPV) asm volatile("" ::: "memory");
@@ -365,7 +365,17 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         {
             const int k = kh * KW + kw;
             const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
-            const float pg = e[k] * scaled;
+            float ekr;
+            if constexpr (K > 49)
+            {
+                ekr = exp_ref((vk - ref) * a);
+                if constexpr (MASKED) ekr = tm.col[kw] ? ekr : 0.0f;
+            }
+            else
+            {
+                ekr = e[k];
+            }
+            const float pg = ekr * scaled;
             const float centered = vk - outp;
             float c = fmaf(a * pg, centered, pg);
             float ad = pg * (vk - ref) * centered;
