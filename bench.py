@@ -5,10 +5,14 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu-ba
 A step is one forward + backward pass of the configuration's operator(s) over one batch of synthetic,
 seeded input already resident in HBM (default configs[1], "C2"). The timed
 region is exactly K steps between device synchronisations. Prints one JSON line with the whole-job
-throughput in output elements per second, the roofline of the dominant kernel (measured with HIP
-events on the stream the kernels run on, torch's current stream) and the CPU baseline (the
-reference's own CPU extension, or the C oracle, on a bounded sample on the host cores, in a child
-process).
+throughput in output elements per second, the roofline of the config's dominant kernel (launched
+through the C ABI after the timed region and timed with HIP events on torch's current stream, the
+stream it runs on; HBM traffic from the committed rocprofv3 counter summary) and the CPU baseline
+(the reference's own CPU extension, or the C oracle, on a bounded sample on the host cores, in a
+child process).
+
+--kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
+rocprofv3 counter runs.
 """
 import argparse
 import json
@@ -53,6 +57,10 @@ def parse():
     p.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--kernel-only", action="store_true",
+                   help="launch only the config's dominant kernel --steps times (for rocprofv3 counter runs)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="copy a MIB-sized device buffer --steps times (scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -61,27 +69,6 @@ def taps(cfg, x_shape=None):
     Cout, Cw, KH, KW = cfg["w"]
     cin_eff = 1 if cfg.get("merge") == "identity" else Cin
     return B * Cout * H * W * cin_eff * KH * KW
-
-
-def work(cfg):
-    """Algorithmic work of one forward and one backward launch (flop, or bytes for the HBM-bound
-    config): every tap counts, border included; a max-plus tap is 2 flop, a smorph tap 8 flop forward
-    and 18 flop backward; the backward of a per-pair merge adds the routing add of every pair."""
-    B, Cin, H, W = cfg["x"]
-    Cout = cfg["w"][0]
-    t = taps(cfg)
-    if cfg["kind"] == "morpho":
-        if cfg["bound"] == "hbm":
-            esz = 8 if cfg["dtype"] == "f64" else 4
-            n_in, n_out = B * Cin * H * W, B * Cout * H * W
-            return {"fwd": (n_in + n_out) * esz, "bwd": (2 * n_in + n_out) * esz, "unit": "bytes"}
-        bwd = 2 * t + (2 * B * Cout * Cin * H * W if cfg["merge"] in ("sum", "mean") else 0)
-        return {"fwd": 2 * t, "bwd": bwd, "unit": "flop"}
-    if cfg["kind"] == "smorph":
-        n = len(cfg["alphas"])
-        return {"fwd": 8 * t * n, "bwd": 18 * t * n, "unit": "flop"}
-    # stack: two max-plus layers and one smorph layer.
-    return {"fwd": 2 * t + 8 * t + 2 * t, "bwd": 2 * t + 18 * t + 2 * t, "unit": "flop"}
 
 
 def make_inputs(cfg, torch, dev):
@@ -154,6 +141,83 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
     return step, n_out
 
 
+MERGE_CODE = {"max": 0, "min": 1, "sum": 2, "mean": 3, "identity": 5}
+
+
+def dominant(cfg, torch, native, x, ws, dtype, dev):
+    """The kernel a config's roofline is quoted on (the largest share of its step on MI355X),
+    launched through the C ABI on torch's current stream with the step's own inputs, and its
+    algorithmic work per launch (all taps, border included; a max-plus tap 2 flop, a smorph
+    backward tap 18 flop; HBM bytes: x, w, out and saved taps once)."""
+    B, Cin, H, W = cfg["x"]
+    Cout, Cw, KH, KW = cfg["w"]
+    geom = (B, Cin, Cout, Cw, H, W, KH, KW)
+    t = taps(cfg)
+    esz = 8 if cfg["dtype"] == "f64" else 4
+    if cfg["kind"] == "morpho":
+        op = 0 if cfg["op"] == "dilation" else 1
+        merge = MERGE_CODE[cfg["merge"]]
+        out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
+        idx = torch.empty(native.indices_bytes(merge, geom), dtype=torch.uint8, device=dev)
+
+        def launch():
+            native.morpho_forward(op, merge, True, 0.0, x, ws[0], 0, out, idx, geom)
+
+        what = f"{cfg['op']} forward, merge {cfg['merge']}, saving winners (mca_morpho_forward, one kernel)"
+        if cfg["bound"] == "hbm":
+            work = (B * Cin * H * W + B * Cout * H * W + ws[0].numel()) * esz + idx.numel()
+            return launch, work, "bytes", what
+        return launch, 2 * t, "flop", what
+    # smorph (C3) or the stack's smorph layer (C5): its backward.
+    merge = MERGE_CODE[cfg.get("merge", "sum")]
+    a = 1.0 if cfg["kind"] == "smorph" else 5.0
+    w = ws[0] if cfg["kind"] == "smorph" else ws[1]
+    alpha = torch.full((Cout * Cin,), a, dtype=dtype, device=dev)
+    out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
+    gx, gw, ga = torch.empty_like(x), torch.empty_like(w), torch.empty_like(alpha)
+    native.smorph_forward(merge, x, w, alpha, out, geom)
+
+    def launch():
+        native.smorph_backward(merge, x, w, alpha, out, grad, gx, gw, ga, geom)
+
+    what = f"smorph backward, merge {cfg.get('merge', 'sum')}, alpha {a:g} (mca_smorph_backward: kernel + zero-fill + slot reduction)"
+    return launch, 18 * t, "flop", what
+
+
+def time_launches(torch, launch, target_s=1.0, max_n=50):
+    """Average duration of back-to-back launches between two HIP events on the current stream."""
+    s = torch.cuda.current_stream()
+    launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    launch()
+    e1.record(s)
+    torch.cuda.synchronize()
+    n = max(1, min(max_n, int(target_s * 1000.0 / max(e0.elapsed_time(e1), 1e-3))))
+    e0.record(s)
+    for _ in range(n):
+        launch()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n, n
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f).get(f"configs[{config - 1}]")
+    if not rec:
+        return None
+    return (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024.0
+
+
 def cpu_baseline(cfg, seconds):
     threads = min(len(os.sched_getaffinity(0)), 16)
     sx = cfg["sample"]["x"]
@@ -188,7 +252,23 @@ def main():
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_launch": n * 4, "launches": args.steps}), flush=True)
+        return
     x, ws, dtype = make_inputs(cfg, torch, dev)
+    if args.kernel_only:
+        launch, _, _, what = dominant(cfg, torch, _native, x, ws, dtype, dev)
+        for _ in range(args.steps):
+            launch()
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": what, "launches": args.steps}), flush=True)
+        return
     step, n_out = build_step(cfg, torch, mca, x, ws, dtype, dev)
 
     for _ in range(args.warmup):
@@ -206,17 +286,18 @@ def main():
     bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
     ms_per_step = wall * 1000.0 / args.steps
 
-    wk = work(cfg)
-    if cfg["bound"] == "hbm":
-        achieved = wk["bwd"] / (bwd_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None}
+    # Roofline of the dominant kernel, timed after the step loop (outside the timed region).
+    launch, dwork, dunit, what = dominant(cfg, torch, _native, x.detach(), [w.detach() for w in ws], dtype, dev)
+    kms, kn = time_launches(torch, launch)
+    if dunit == "bytes":
+        achieved = dwork / (kms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS}
     else:
         peak = PEAK_FP64_TFLOPS if cfg["dtype"] == "f64" else PEAK_FP32_TFLOPS
-        achieved = wk["bwd"] / (bwd_ms * 1e-3) / 1e12
-        roof = {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None}
-    roof["kernel"] = "backward entry (mca_*_backward: dominant kernel plus its zero-fill and slot reduction)"
-    roof["fwd_achieved"] = (wk["fwd"] / (fwd_ms * 1e-3)) / (1e9 if cfg["bound"] == "hbm" else 1e12)
-
+        achieved = dwork / (kms * 1e-3) / 1e12
+        roof = {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak}
+    roof["traffic"] = measured_traffic(args.config)
+    roof.update({"kernel": what, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": dwork, "work_unit": dunit})
     line = {
         "metric": METRIC,
         "value": n_out / (ms_per_step * 1e-3),
