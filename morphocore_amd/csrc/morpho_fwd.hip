@@ -521,11 +521,12 @@ static bool has_static(const Geom& g)
 }
 
 // Rows per wave of the static kernel: the TAPS mode holds (RH + KH - 1) x KW window values in
-// registers, the VALUE modes one column of RH + KH - 1.
+// registers (4 rows from 5x5 up: fewer registers, more waves, measured faster), the VALUE modes one
+// column of RH + KH - 1.
 template <typename T, int KH, int MODE>
 constexpr int static_rows()
 {
-    return sizeof(T) == 8 ? 4 : (MODE == FWD_TAPS && KH >= 11 ? 4 : 8);
+    return sizeof(T) == 8 ? 4 : (MODE == FWD_TAPS && KH >= 5 ? 4 : 8);
 }
 
 template <typename T>
