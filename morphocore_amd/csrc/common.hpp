@@ -19,6 +19,7 @@
 
 #include <cmath>
 #include <limits>
+#include <type_traits>
 
 namespace mca
 {

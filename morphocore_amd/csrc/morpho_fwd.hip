@@ -395,10 +395,10 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             for (int rr = 0; rr < WR; ++rr)
 #pragma unroll
                 for (int kw = 0; kw < KW; ++kw) wnd[rr][kw] = tb[rr * COLS - kw];
+            int arg[OB][RH];
 #pragma unroll
             for (int ob = 0; ob < OB; ++ob)
             {
-                const int o = o0 + ob;
                 const T* wp = &wts[buf][ob * K];
 #pragma unroll
                 for (int r = 0; r < RH; ++r)
@@ -430,18 +430,28 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
                     int kcol = 0;
 #pragma unroll
                     for (int kw = KW - 1; kw >= 0; --kw) kcol = Tr::combine(xrow[-kw], wrow[kw]) == best ? kw : kcol;
-                    int arg = krow * KW + kcol;
-                    if (best == Tr::init()) arg = 0;
+                    arg[ob][r] = best == Tr::init() ? 0 : krow * KW + kcol;
                     merge_pair<T, MK>(best, i, acc[ob][r], win[ob][r]);
-                    const int h = h0 + wave * RH + r;
-                    if (o < g.Cout && h < g.H && wc < g.W)
-                    {
-                        if constexpr (K <= 256)
-                            static_cast<uint8_t*>(p.idx)[pair_tap_index(g, ident, b, o, i, h, wc)] = (uint8_t)arg;
-                        else
-                            static_cast<uint16_t*>(p.idx)[pair_tap_index(g, ident, b, o, i, h, wc)] = (uint16_t)arg;
-                    }
                 }
+            }
+            // The stores follow every pair's scan, so that the scans form one basic block in which
+            // the LDS reads of one pair overlap the arithmetic of the others; the asm uses keep the
+            // compiler from sinking each pair's column scan into its conditional store.
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                for (int r = 0; r < RH; ++r) asm volatile("" ::"v"(arg[ob][r]));
+            using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
+            const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob)
+            {
+                const int o = o0 + ob;
+                if (o >= g.Cout) continue;
+                AT* __restrict__ dst = static_cast<AT*>(p.idx) + pair_tap_index(g, ident, b, o, i, hw, w0);
+#pragma unroll
+                for (int r = 0; r < RH; ++r)
+                    if (hw + r < g.H && wc < g.W) dst[r * g.W + lane] = (AT)arg[ob][r];
             }
         }
         else

@@ -106,14 +106,15 @@ struct SmorphFwdParams
 // The same exponential for the arguments the smorph kernels pass, alpha (v - ref) with ref the
 // extremum of the window: never positive, or NaN. Bit for bit equal to exp_t on (-inf, max_input];
 // a NaN argument gives NaN, as in the reference (whose range checks let NaN through), and the upper
-// clamp is dropped since no argument reaches it.
+// clamp is dropped since no argument reaches it. `lo` is the lower clamp, min_input (a caller may
+// hold it in a register, which makes the comparison a register-only one).
 template <typename T>
-__device__ __forceinline__ T exp_ref(T x)
+__device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
 {
     using C = ExpConsts<T>;
     using Bits = typename C::Bits;
-    const bool under = x < C::min_input;
-    const T xc = under ? T(C::min_input) : x;
+    const bool under = x < lo;
+    const T xc = under ? lo : x;
     const T nm = fma(xc, C::log2e, C::magic);
     const T n = nm - C::magic;
     const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));

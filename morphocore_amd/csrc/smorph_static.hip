@@ -12,9 +12,11 @@
 //    as in the reference;
 //  * the backward keeps every tap's e in registers (up to 7x7) between the pass that forms S and W
 //    and the pass that routes the gradient, so each exponential is evaluated once per backward
-//    (11x11 re-evaluates it: 121 more registers cost more waves than the exponentials cost VALU). Every lane of a wave routes the same tap at
-//    once, so the grad_input and grad_weight LDS atomics hit consecutive or lane-striped addresses
-//    (no bank conflicts).
+//    (11x11 re-evaluates it: 121 more registers cost more waves than the exponentials cost VALU);
+//  * every lane of a wave routes the same tap at once: a row of KW taps is summed per tile column
+//    across the wave (a DPP shift per tap) before one LDS atomic per row, and the grad_weight LDS
+//    atomics hit lane-striped copies (no bank conflicts). LDS atomics cost per instruction, not per
+//    active lane (measured), so partial sums replace instructions, never lanes.
 #include "smorph_common.hpp"
 
 namespace mca
@@ -110,7 +112,10 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
 template <int KH, int KW, bool MASKED>
 __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, float a, float ref, const TapMask<KH, KW>& tm, float& S, float& Wsum)
 {
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int COLS = TILE_W + KW - 1;
+    float lo = ExpConsts<float>::min_input;
+    asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     float s = 0.0f, wsum = 0.0f;
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh)
@@ -120,17 +125,12 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
         for (int kw = 0; kw < KW; ++kw)
         {
             const float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
-            const float e = exp_ref((v - ref) * a);
-            if constexpr (MASKED)
-            {
-                s = tm.col[kw] ? s + e : s;
-                wsum = tm.col[kw] ? fmaf(e, v, wsum) : wsum;
-            }
-            else
-            {
-                s = s + e;
-                wsum = fmaf(e, v, wsum);
-            }
+            float e = exp_ref((v - ref) * a, lo);
+            // An out-of-image tap adds e = 0 (its staged x is 0, so v is finite): S + 0 and
+            // fma(0, v, W) leave both sums exactly as skipping it does.
+            if constexpr (MASKED) e = tm.col[kw] ? e : 0.0f;
+            s = s + e;  // unfused, as in the reference (e is rounded before the sum)
+            wsum = fmaf(e, v, wsum);
         }
     }
     S = s;
@@ -144,7 +144,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams
     constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, ELEMS = ROWS * COLS;
     constexpr int NS = (ELEMS + BLOCK - 1) / BLOCK;
     __shared__ float tile[2][ELEMS];
-    __shared__ float wl[2][K + 1];  // the pair's structuring element, then its alpha
+    // The pair's structuring element, then its alpha; rows padded to 16 bytes so the taps load as
+    // 128-bit broadcast reads.
+    __shared__ __align__(16) float wl[2][(K + 4) & ~3];
     const Geom g = p.g;
     const Tiling t = p.t;
     const int lane = threadIdx.x & (WAVE - 1);
@@ -275,14 +277,23 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams
 // the grad_weight bin of tap k and to grad_alpha (returned: the sum of p_k (v_k - ref)(v_k - out)
 // over the taps). gv is g * scale (0 outside the image); for MAX / MIN it is divided by the pixel's
 // winner count, and only a pair within 1e-6 of the merged output outv routes.
+// The value of the next lower lane (0 in lane 0): DPP wave_shr:1 with bound_ctrl.
+__device__ __forceinline__ float wave_shift_up(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, true));
+}
+
 template <int MK, int KH, int KW, bool MASKED>
 __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
-                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl)
+                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
 {
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
     constexpr bool KEEPV = false;  // v re-read from LDS in each pass: fewer registers, more waves (measured faster)
-    constexpr bool GATE = MASKED || MK == MK_MAX || MK == MK_MIN;
+    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN;
     const bool dil = a >= 0.0f;
+    float lo = ExpConsts<float>::min_input;
+    asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     float v[KEEPV ? K : 1], e[K <= 49 ? K : 1];
     float ref;
     if constexpr (KEEPV)
@@ -331,17 +342,11 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         {
             const int k = kh * KW + kw;
             const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
-            const float ek = exp_ref((vk - ref) * a);
-            if constexpr (MASKED)
-            {
-                s = tm.col[kw] ? s + ek : s;
-                wsum = tm.col[kw] ? fmaf(ek, vk, wsum) : wsum;
-            }
-            else
-            {
-                s = s + ek;
-                wsum = fmaf(ek, vk, wsum);
-            }
+            float ek = exp_ref((vk - ref) * a, lo);
+            // Out-of-image taps: e = 0 leaves S and W as skipping them does, and routes c = 0.
+            if constexpr (MASKED) ek = tm.col[kw] ? ek : 0.0f;
+            s = s + ek;  // unfused, as in the reference
+            wsum = fmaf(ek, vk, wsum);
             if constexpr (K <= 49) e[k] = ek;
         }
     }
@@ -354,12 +359,21 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         gv = gv / (cnt > 0.0f ? cnt : 1.0f);
         route = route && is_winner(outp, outv);
     }
-    const float scaled = gv * inv;
+    // A lane that routes nothing (outside the image, where S may be 0 and out NaN, or a MAX / MIN
+    // loser) gets g' = 0 and a finite centre, so every c it adds to the row sums is 0.
+    const float scaled = route ? gv * inv : 0.0f;
+    const float outc = route ? outp : 0.0f;
     float asum = 0.0f;
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh)
     {
         if (MASKED && !tm.row(kh)) continue;
+        // grad_input of the row's taps, summed per tile column across the wave before the LDS add:
+        // lane l's tap kw lands in column l + KW - 1 - kw, so a Horner scheme over kw with a one-lane
+        // shift (DPP wave_shr) leaves column l's total in lane l. What leaves lane 63 at step kw is
+        // the (complete) total of the right halo column 63 + KW - kw; lane KW - 1 - kw keeps it.
+        float racc = 0.0f, halo = 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
@@ -368,7 +382,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             float ekr;
             if constexpr (K > 49)
             {
-                ekr = exp_ref((vk - ref) * a);
+                ekr = exp_ref((vk - ref) * a, lo);
                 if constexpr (MASKED) ekr = tm.col[kw] ? ekr : 0.0f;
             }
             else
@@ -376,21 +390,30 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
                 ekr = e[k];
             }
             const float pg = ekr * scaled;
-            const float centered = vk - outp;
+            const float centered = vk - outc;
             float c = fmaf(a * pg, centered, pg);
-            float ad = pg * (vk - ref) * centered;
-            if constexpr (GATE)
+            if constexpr (GATE) c = route ? c : 0.0f;
+            if (kw == 0)
             {
-                const bool ok = route && (!MASKED || tm.col[kw]);
-                c = ok ? c : 0.0f;
-                ad = ok ? ad : 0.0f;
+                racc = c;
             }
-            lds_add(&gxb[-(kh * COLS + kw)], (Acc)c);
+            else
+            {
+                const int fell = __builtin_amdgcn_readlane(__float_as_int(racc), WAVE - 1);
+                asm("v_writelane_b32 %0, %1, %2" : "+v"(halo) : "s"(fell), "i"(KW - 1 - kw));
+                racc = wave_shift_up(racc) + c;
+            }
             lds_add(&bl[k * SMORPH_BIN_COPIES], (Acc)c);
-            asum = asum + ad;
+            asum = fmaf(pg * (vk - ref), centered, asum);
+            // Keeps the compiler from deferring the alpha terms to the end of the pair, which would
+            // hold every tap's factors in registers.
+            asm volatile("" : "+v"(asum));
         }
+        Acc* grow = gxb - (kh * COLS + KW - 1);  // this row's tile column `lane`
+        lds_add(grow, (Acc)racc);
+        if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
     }
-    return asum;
+    return route ? asum : 0.0f;
 }
 
 template <int MK, int KH, int KW>
@@ -402,7 +425,8 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
     __shared__ float tile[ROWS * COLS];
     __shared__ Acc gtile[ROWS * COLS];
     __shared__ __align__(32) Acc bins[(K + 1) * NC];  // grad_weight bins of the K taps, then grad_alpha; NC copies each
-    __shared__ float wl[2][K + 1];      // structuring element and alpha of the current / next pair
+    // Structuring element and alpha of the current / next pair, rows padded to 16 bytes (128-bit reads).
+    __shared__ __align__(16) float wl[2][(K + 4) & ~3];
     const Geom g = p.g;
     const Tiling t = p.t;
     const int lane = threadIdx.x & (WAVE - 1);
@@ -480,9 +504,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
             const float a = w[K];
             float asum;
             if (interior)
-                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl);
+                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
             else
-                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl);
+                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
             lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
