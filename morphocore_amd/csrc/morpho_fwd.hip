@@ -120,16 +120,45 @@ __device__ __forceinline__ void store_output(const FwdParams<T>& p, int b, int o
             int karg = 0;
             if (acc != Tr::init())
             {
-                for (int k = 0; k < K; ++k)
+                // Taps in chunks of 8 whose loads are all in flight together (the rescan is a chain of
+                // dependent global loads otherwise); the first equal tap of the first chunk holding
+                // one wins.
+                constexpr int CH = 8;
+                int kh0 = 0, kw0 = 0, found = -1;
+                T fval = T(0);
+                for (int k0 = 0; k0 < K && found < 0; k0 += CH)
                 {
-                    const int kh = k / g.KW, kw = k - kh * g.KW;
-                    const T val = Tr::combine(read_padded(xp, g.H, g.W, h + ph - kh, wc + pw - kw, p.replicate != 0, p.fill), wp[k]);
-                    if (val == acc)
+                    T val[CH];
+                    int kh = kh0, kw = kw0;
+#pragma unroll
+                    for (int j = 0; j < CH; ++j)
                     {
-                        karg = k;
-                        if (v == T(0)) v = val;
-                        break;
+                        // read_padded with an unconditional (clamped, in-bounds) load
+                        const int kk = min(k0 + j, K - 1);
+                        const int y = h + ph - kh, x = wc + pw - kw;
+                        const T raw = xp[(int64_t)clampi(y, 0, g.H - 1) * g.W + clampi(x, 0, g.W - 1)];
+                        const bool inb = y >= 0 && y < g.H && x >= 0 && x < g.W;
+                        val[j] = Tr::combine(inb || p.replicate ? raw : p.fill, wp[kk]);
+                        if (++kw == g.KW)
+                        {
+                            kw = 0;
+                            ++kh;
+                        }
                     }
+                    kh0 = kh;
+                    kw0 = kw;
+#pragma unroll
+                    for (int j = CH - 1; j >= 0; --j)
+                    {
+                        const bool hit = k0 + j < K && val[j] == acc;
+                        found = hit ? k0 + j : found;
+                        fval = hit ? val[j] : fval;
+                    }
+                }
+                if (found >= 0)
+                {
+                    karg = found;
+                    if (v == T(0)) v = fval;
                 }
             }
             packed = (int32_t)((c << 16) | karg);
@@ -561,12 +590,28 @@ static hipError_t launch_generic(FwdParams<T> p, hipStream_t stream)
     return hipGetLastError();
 }
 
+// Below this many workgroups the chip is mostly idle and every workgroup's serial latency (its channel
+// loop, the winner rescans of its pixels) is the kernel time: such launches take one row per wave and
+// one output channel per workgroup instead, for up to RH * OB times more workgroups.
+constexpr int64_t SMALL_GRID = 1024;
+
 template <typename T, int OP, int MK, int OB, int MODE, int KS>
 static hipError_t launch_static(FwdParams<T> p, hipStream_t stream)
 {
     constexpr int RH = static_rows<T, KS, MODE>();
     p.t = make_tiling(p.g, RH);
-    const int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.nog;
+    int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.nog;
+    if constexpr (RH > 1 || OB > 1)
+    {
+        if (blocks < SMALL_GRID)
+        {
+            p.t = make_tiling(p.g, 1);
+            p.nog = p.g.Cout;
+            blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.nog;
+            morpho_fwd_static<T, OP, MK, KS, KS, 1, 1, MODE><<<(unsigned)blocks, BLOCK, 0, stream>>>(p);
+            return hipGetLastError();
+        }
+    }
     morpho_fwd_static<T, OP, MK, KS, KS, OB, RH, MODE><<<(unsigned)blocks, BLOCK, 0, stream>>>(p);
     return hipGetLastError();
 }
