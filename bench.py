@@ -187,16 +187,29 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
 
 
 def time_launches(torch, launch, target_s=1.0, max_n=50):
-    """Average duration of back-to-back launches between two HIP events on the current stream."""
+    """Average duration of back-to-back launches between two HIP events on the current stream.
+
+    A spin kernel queued ahead of the first event keeps the GPU busy while the host queues the n
+    launches, so that the events bracket kernels that run back to back and not the host's launch
+    gaps (which exceed the kernel time of the smallest configurations)."""
     s = torch.cuda.current_stream()
     launch()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
     e0.record(s)
     launch()
     e1.record(s)
+    host_s = time.perf_counter() - t0
     torch.cuda.synchronize()
     n = max(1, min(max_n, int(target_s * 1000.0 / max(e0.elapsed_time(e1), 1e-3))))
+    # Spin-kernel clock rate, then a spin covering twice the host time of n launches (at most 0.5 s).
+    e0.record(s)
+    torch.cuda._sleep(1 << 20)
+    e1.record(s)
+    torch.cuda.synchronize()
+    cycles_per_ms = (1 << 20) / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(min(500.0, 2.0 * n * host_s * 1e3 + 1.0) * cycles_per_ms))
     e0.record(s)
     for _ in range(n):
         launch()

@@ -120,10 +120,10 @@ __device__ __forceinline__ void store_output(const FwdParams<T>& p, int b, int o
             int karg = 0;
             if (acc != Tr::init())
             {
-                // Taps in chunks of 8 whose loads are all in flight together (the rescan is a chain of
+                // Taps in chunks of 4 whose loads are all in flight together (the rescan is a chain of
                 // dependent global loads otherwise); the first equal tap of the first chunk holding
                 // one wins.
-                constexpr int CH = 8;
+                constexpr int CH = 4;
                 int kh0 = 0, kw0 = 0, found = -1;
                 T fval = T(0);
                 for (int k0 = 0; k0 < K && found < 0; k0 += CH)
@@ -424,6 +424,18 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             for (int rr = 0; rr < WR; ++rr)
 #pragma unroll
                 for (int kw = 0; kw < KW; ++kw) wnd[rr][kw] = tb[rr * COLS - kw];
+            // Up to 5x5 the taps are stored after every pair's scan, so that the scans form one basic
+            // block in which the LDS reads of one pair overlap the arithmetic of the others; larger
+            // elements store each pair's tap at once (the deferred form needs more registers than
+            // leave two waves per SIMD).
+            constexpr bool DEFER = K <= 25;
+            using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
+            const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
+            auto store_tap = [&](int ob, int r, int a) {
+                const int o = o0 + ob;
+                if (o < g.Cout && hw + r < g.H && wc < g.W)
+                    (static_cast<AT*>(p.idx) + pair_tap_index(g, ident, b, o, i, hw, w0))[r * g.W + lane] = (AT)a;
+            };
             int arg[OB][RH];
 #pragma unroll
             for (int ob = 0; ob < OB; ++ob)
@@ -461,26 +473,21 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
                     for (int kw = KW - 1; kw >= 0; --kw) kcol = Tr::combine(xrow[-kw], wrow[kw]) == best ? kw : kcol;
                     arg[ob][r] = best == Tr::init() ? 0 : krow * KW + kcol;
                     merge_pair<T, MK>(best, i, acc[ob][r], win[ob][r]);
+                    if constexpr (!DEFER) store_tap(ob, r, arg[ob][r]);
                 }
             }
-            // The stores follow every pair's scan, so that the scans form one basic block in which
-            // the LDS reads of one pair overlap the arithmetic of the others; the asm uses keep the
-            // compiler from sinking each pair's column scan into its conditional store.
-#pragma unroll
-            for (int ob = 0; ob < OB; ++ob)
-#pragma unroll
-                for (int r = 0; r < RH; ++r) asm volatile("" ::"v"(arg[ob][r]));
-            using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
-            const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
-#pragma unroll
-            for (int ob = 0; ob < OB; ++ob)
+            if constexpr (DEFER)
             {
-                const int o = o0 + ob;
-                if (o >= g.Cout) continue;
-                AT* __restrict__ dst = static_cast<AT*>(p.idx) + pair_tap_index(g, ident, b, o, i, hw, w0);
+                // The asm uses keep the compiler from sinking each pair's column scan into its
+                // conditional store.
 #pragma unroll
-                for (int r = 0; r < RH; ++r)
-                    if (hw + r < g.H && wc < g.W) dst[r * g.W + lane] = (AT)arg[ob][r];
+                for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                    for (int r = 0; r < RH; ++r) asm volatile("" ::"v"(arg[ob][r]));
+#pragma unroll
+                for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                    for (int r = 0; r < RH; ++r) store_tap(ob, r, arg[ob][r]);
             }
         }
         else
