@@ -412,8 +412,12 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     T* counts = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
     T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes));
     const int nslots = g.B * s.nstrips;
-    if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
-    if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
+    // The static kernels that keep their partials in LDS store every slot entry themselves.
+    if (!(smorph_static_supported<T>(g) && smorph_bwd_lds_partials(g, merge == MERGE_IDENTITY)))
+    {
+        if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
+        if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
+    }
 
     if (merge == MERGE_MAX || merge == MERGE_MIN)
     {

@@ -454,6 +454,12 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
             wl[buf][K] = p.alpha[pair_index(o)];
     };
 
+    // This workgroup's grad_weight / grad_alpha partials summed over its tiles (pair o - o_begin, tap
+    // k or K for alpha), stored once at the end, when they fit.
+    constexpr int NPART = K <= 49 ? SMORPH_LDS_PARTIALS : 1;
+    __shared__ float partials[NPART];
+    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
+    for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
     for (int j = threadIdx.x; j < (K + 1) * NC; j += BLOCK) bins[j] = Acc(0);
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
@@ -525,7 +531,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
                 if ((j & 7) == 0)
                 {
                     const int k = j >> 3;
-                    if (k < K)
+                    if (lds_partials)
+                        partials[(o - o_begin) * (K + 1) + k] += (float)v;  // one owner per entry
+                    else if (k < K)
                         global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
                     else
                         global_add(&part_a[pair_index(o)], (float)v);
@@ -542,6 +550,21 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
             if (y < 0 || y >= g.H || x < 0 || x >= g.W) continue;
             const float v = (float)gtile[idx];
             if (v != 0.0f) global_add(&gplane[(int64_t)y * g.W + x], v);
+        }
+    }
+    if (lds_partials)
+    {
+        // Every entry of this workgroup's share of the slot (zeros for a strip without tiles): the
+        // host skips the slot's zero fill.
+        __syncthreads();
+        const int n = (o_end - o_begin) * (K + 1);
+        for (int j = threadIdx.x; j < n; j += BLOCK)
+        {
+            const int ol = j / (K + 1), k = j - ol * (K + 1), o = o_begin + ol;
+            if (k < K)
+                part_w[((int64_t)o * g.Cw + wi) * K + k] = partials[j];
+            else
+                part_a[pair_index(o)] = partials[j];
         }
     }
 }
