@@ -38,6 +38,7 @@ struct FwdParams
     Geom g;
     Tiling t;
     int nog;
+    int chans;  // static kernel, IDENTITY: consecutive channels per workgroup (else 1)
     int replicate;
     int average;
     T fill;
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const FwdWork wk = decode_fwd(p.nog, p.t);
     const int b = wk.b;
-    const int h0 = wk.ty * S::TH, w0 = wk.tx * TILE_W, o0 = wk.og * OB;
+    const int h0 = wk.ty * S::TH, w0 = wk.tx * TILE_W, o0 = wk.og * (ident ? p.chans : OB);
     const int y0 = h0 + KH / 2 - (KH - 1), x0 = w0 + KW / 2 - (KW - 1);
     const int64_t plane = g.plane();
     const T* __restrict__ wb = p.w + (int64_t)b * g.wbs;
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
     {
         const int idx = min((int)threadIdx.x + j * BLOCK, SW::ELEMS - 1);
         const int ob = idx / K, k = idx - ob * K;
-        woff[j] = (min(o0 + ob, g.Cout - 1) * g.Cw) * K + k;
+        woff[j] = ident ? k : (min(o0 + ob, g.Cout - 1) * g.Cw) * K + k;
     }
     const T* __restrict__ xb = p.x + (int64_t)b * g.Cin * plane;
     T pre[NS], wpre[NW];
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
         const T* __restrict__ pl = xb + (int64_t)i * plane;
 #pragma unroll
         for (int j = 0; j < NS; ++j) pre[j] = off[j] >= 0 ? pl[off[j]] : p.fill;
-        const T* __restrict__ wi = wb + (ident ? 0 : i) * K;
+        const T* __restrict__ wi = wb + (int64_t)i * K;  // IDENTITY: channel i's own element
 #pragma unroll
         for (int j = 0; j < NW; ++j) wpre[j] = wi[woff[j]];
     };
@@ -399,8 +400,10 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             win[ob][r] = 0;
         }
 
+    // IDENTITY walks its p.chans channels as the other merges walk the input channels (next tile
+    // prefetched), storing each channel's outputs after its scan.
     const int i_begin = ident ? o0 : 0;
-    const int i_end = ident ? o0 + 1 : g.Cin;
+    const int i_end = ident ? min(o0 + p.chans, g.Cout) : g.Cin;
     load(i_begin);
     store(0);
     __syncthreads();
@@ -432,7 +435,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
             const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
             auto store_tap = [&](int ob, int r, int a) {
-                const int o = o0 + ob;
+                const int o = ident ? i : o0 + ob;
                 if (o < g.Cout && hw + r < g.H && wc < g.W)
                     (static_cast<AT*>(p.idx) + pair_tap_index(g, ident, b, o, i, hw, w0))[r * g.W + lane] = (AT)a;
             };
@@ -538,19 +541,31 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
                 }
         }
 
+        if constexpr (ident)
+        {
+#pragma unroll
+            for (int r = 0; r < RH; ++r)
+            {
+                const int h = h0 + wave * RH + r;
+                if (h < g.H && wc < g.W) store_output<T, OP, MK, MODE>(p, b, i, h, wc, 1, acc[0][r], win[0][r]);
+            }
+        }
         if (more) store(buf ^ 1);
         __syncthreads();
     }
 
+    if constexpr (!ident)
+    {
 #pragma unroll
-    for (int ob = 0; ob < OB; ++ob)
+        for (int ob = 0; ob < OB; ++ob)
 #pragma unroll
-        for (int r = 0; r < RH; ++r)
-        {
-            const int o = o0 + ob, h = h0 + wave * RH + r;
-            if (o >= g.Cout || h >= g.H || wc >= g.W) continue;
-            store_output<T, OP, MK, MODE>(p, b, o, h, wc, i_end - i_begin, acc[ob][r], win[ob][r]);
-        }
+            for (int r = 0; r < RH; ++r)
+            {
+                const int o = o0 + ob, h = h0 + wave * RH + r;
+                if (o >= g.Cout || h >= g.H || wc >= g.W) continue;
+                store_output<T, OP, MK, MODE>(p, b, o, h, wc, i_end - i_begin, acc[ob][r], win[ob][r]);
+            }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -601,12 +616,20 @@ static hipError_t launch_generic(FwdParams<T> p, hipStream_t stream)
 // loop, the winner rescans of its pixels) is the kernel time: such launches take one row per wave and
 // one output channel per workgroup instead, for up to RH * OB times more workgroups.
 constexpr int64_t SMALL_GRID = 1024;
+constexpr int IDENT_CHANS = 8;
 
 template <typename T, int OP, int MK, int OB, int MODE, int KS>
 static hipError_t launch_static(FwdParams<T> p, hipStream_t stream)
 {
     constexpr int RH = static_rows<T, KS, MODE>();
     p.t = make_tiling(p.g, RH);
+    if constexpr (MK == MK_IDENT)
+    {
+        // IDENTITY: up to IDENT_CHANS consecutive channels per workgroup, one tile load in flight
+        // behind each channel's scan (a single channel per workgroup leaves the loads unhidden).
+        p.chans = p.g.Cout < IDENT_CHANS ? p.g.Cout : IDENT_CHANS;
+        p.nog = (p.g.Cout + p.chans - 1) / p.chans;
+    }
     int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.nog;
     if constexpr (RH > 1 || OB > 1)
     {
@@ -614,6 +637,7 @@ static hipError_t launch_static(FwdParams<T> p, hipStream_t stream)
         {
             p.t = make_tiling(p.g, 1);
             p.nog = p.g.Cout;
+            p.chans = 1;
             blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.nog;
             morpho_fwd_static<T, OP, MK, KS, KS, 1, 1, MODE><<<(unsigned)blocks, BLOCK, 0, stream>>>(p);
             return hipGetLastError();
