@@ -469,74 +469,113 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const Ta
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, WR = RH + KH - 1;
+    constexpr int ELEMS = ROWS * COLS, NS = (ELEMS + BLOCK - 1) / BLOCK;
     constexpr int NC = 32;
-    __shared__ T gs[ROWS * COLS];
-    __shared__ int ts[ROWS * COLS];
-    __shared__ Acc bins[K * NC];
+    __shared__ T gs[ELEMS];
+    __shared__ int ts[ELEMS];
+    __shared__ __align__(16) Acc bins[K * NC];
     const Geom g = p.g;
     const Tiling t = p.t;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int work = xcd_work_index(blockIdx.x, gridDim.x);
-    const int c = work % g.Cin;
-    work /= g.Cin;
+    const int cgroup = work % p.nig;
+    work /= p.nig;
     const int tile = work % t.ntiles();
     const int b = work / t.ntiles();
     const int ty = tile / t.ntx, tx = tile - ty * t.ntx;
     const int h0 = ty * TH, w0 = tx * TILE_W;
     const int y0 = h0 - PH, x0 = w0 - PW;
     const int64_t plane = g.plane();
-    const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + c) * plane;
-    const uint8_t* __restrict__ tp = static_cast<const uint8_t*>(p.taps) + ((int64_t)b * g.Cout + c) * plane;
+    const int c_begin = cgroup * p.ig, c_end = min(c_begin + p.ig, g.Cin);
+    const int wc = w0 + lane;
 
-    for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
-    // Output pixels of the tile plus halo; outside the image: no gradient, a tap that matches none.
-    for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+    // Staging plan (output pixels of the tile plus halo), the same for every channel: the clamped
+    // in-image offset of each element this thread stages and whether it lies in the image (outside:
+    // no gradient, a tap that matches none).
+    int off[NS];
+    bool ok[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
     {
+        const int idx = min((int)threadIdx.x + j * BLOCK, ELEMS - 1);
         const int ly = idx / COLS, lx = idx - ly * COLS;
         const int y = y0 + ly, x = x0 + lx;
-        const bool in = y >= 0 && y < g.H && x >= 0 && x < g.W;
-        const int64_t o = in ? (int64_t)y * g.W + x : 0;
-        const T gv = gp[o];
-        const int tv = tp[o];
-        gs[idx] = in ? gv : T(0);
-        ts[idx] = in ? tv : -1;
+        ok[j] = y >= 0 && y < g.H && x >= 0 && x < g.W;
+        off[j] = clampi(y, 0, g.H - 1) * g.W + clampi(x, 0, g.W - 1);
     }
-    __syncthreads();
-
-    T gw[WR][KW];
-    int tw[WR][KW];
+    T pg[NS];
+    int pt[NS];
+    auto load = [&](int c) {
+        const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + c) * plane;
+        const uint8_t* __restrict__ tp = static_cast<const uint8_t*>(p.taps) + ((int64_t)b * g.Cout + c) * plane;
 #pragma unroll
-    for (int rr = 0; rr < WR; ++rr)
-#pragma unroll
-        for (int kw = 0; kw < KW; ++kw)
+        for (int j = 0; j < NS; ++j)
         {
-            gw[rr][kw] = gs[(wave * RH + rr) * COLS + lane + kw];
-            tw[rr][kw] = ts[(wave * RH + rr) * COLS + lane + kw];
+            pg[j] = gp[off[j]];
+            pt[j] = tp[off[j]];
         }
-    T* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + c) * plane;
-    const int wc = w0 + lane;
-    Acc* bl = bins + (lane & (NC - 1));
-#pragma unroll
-    for (int r = 0; r < RH; ++r)
+    };
+
+    for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
+    load(c_begin);
+    for (int c = c_begin; c < c_end; ++c)
     {
-        // Window rows r .. r + KH - 1 hold the pixels p of q = (row r, this lane's column).
-        Acc s = Acc(0);
 #pragma unroll
-        for (int kh = 0; kh < KH; ++kh)
+        for (int j = 0; j < NS; ++j)
+        {
+            const int idx = threadIdx.x + j * BLOCK;
+            if (j < NS - 1 || idx < ELEMS)
+            {
+                gs[idx] = ok[j] ? pg[j] : T(0);
+                ts[idx] = ok[j] ? pt[j] : -1;
+            }
+        }
+        __syncthreads();
+        if (c + 1 < c_end) load(c + 1);  // in flight while this channel computes
+
+        T gw[WR][KW];
+        int tw[WR][KW];
 #pragma unroll
-            for (int kw = 0; kw < KW; ++kw) s += tw[r + kh][kw] == kh * KW + kw ? (Acc)gw[r + kh][kw] : Acc(0);
-        const int h = h0 + wave * RH + r;
-        if (h < g.H && wc < g.W) gplane[(int64_t)h * g.W + wc] = (T)s;
-        // grad_weight: this lane's own output pixel (h, wc), staged at (row r + PH, column PW).
-        const int k = tw[r + PH][PW];
-        if (k >= 0) lds_add(&bl[k * NC], (Acc)(OP == DILATION ? gw[r + PH][PW] : -gw[r + PH][PW]));
-    }
-    __syncthreads();
-    if (threadIdx.x < K)
-    {
-        Acc s = Acc(0);
-        for (int j = 0; j < NC; ++j) s += bins[threadIdx.x * NC + j];
-        p.part[((int64_t)b * t.ntiles() + tile) * g.Cout * K + (int64_t)c * K + threadIdx.x] = (T)s;
+        for (int rr = 0; rr < WR; ++rr)
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw)
+            {
+                gw[rr][kw] = gs[(wave * RH + rr) * COLS + lane + kw];
+                tw[rr][kw] = ts[(wave * RH + rr) * COLS + lane + kw];
+            }
+        T* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + c) * plane;
+        Acc* bl = bins + (lane & (NC - 1));
+#pragma unroll
+        for (int r = 0; r < RH; ++r)
+        {
+            // Window rows r .. r + KH - 1 hold the pixels p of q = (row r, this lane's column).
+            Acc s = Acc(0);
+#pragma unroll
+            for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+                for (int kw = 0; kw < KW; ++kw) s += tw[r + kh][kw] == kh * KW + kw ? (Acc)gw[r + kh][kw] : Acc(0);
+            const int h = h0 + wave * RH + r;
+            if (h < g.H && wc < g.W) gplane[(int64_t)h * g.W + wc] = (T)s;
+            // grad_weight: this lane's own output pixel (h, wc), staged at (row r + PH, column PW).
+            const int k = tw[r + PH][PW];
+            if (k >= 0) lds_add(&bl[k * NC], (Acc)(OP == DILATION ? gw[r + PH][PW] : -gw[r + PH][PW]));
+        }
+        __syncthreads();
+        // Channel c's bins: 8 threads per tap each add 4 copies and clear them, a butterfly over the
+        // 8 finishes (K * 8 <= BLOCK: one pass; groups of 8 lanes are whole).
+        static_assert(K * 8 <= BLOCK, "one pass over the bins");
+        if (threadIdx.x < K * 8)
+        {
+            Acc* q = bins + threadIdx.x * 4;
+            Acc v = (q[0] + q[1]) + (q[2] + q[3]);
+            q[0] = q[1] = q[2] = q[3] = Acc(0);
+#pragma unroll
+            for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
+            if ((threadIdx.x & 7) == 0)
+                p.part[((int64_t)b * t.ntiles() + tile) * g.Cout * K + (int64_t)c * K + (threadIdx.x >> 3)] = (T)v;
+        }
+        // The next channel's staging overwrites gs / ts, and its adds need the cleared bins.
+        __syncthreads();
     }
 }
 
@@ -598,9 +637,11 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     if (ident && g.KH == g.KW && (g.KH == 3 || g.KH == 5))
     {
+        // Up to 8 consecutive channels per workgroup, the next channel's loads in flight behind
+        // each channel's gather.
         s.gather = true;
-        s.ig = 1;
-        s.nig = g.Cin;
+        s.ig = g.Cin < 8 ? g.Cin : 8;
+        s.nig = (g.Cin + s.ig - 1) / s.ig;
         s.oc = 1;
         s.ncopy = 32;
         s.lds = 0;  // static
