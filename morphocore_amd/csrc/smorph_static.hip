@@ -12,7 +12,8 @@
 //    as in the reference;
 //  * the backward keeps every tap's e in registers (up to 7x7) between the pass that forms S and W
 //    and the pass that routes the gradient, so each exponential is evaluated once per backward
-//    (11x11 re-evaluates it: 121 more registers cost more waves than the exponentials cost VALU);
+//    (11x11 keeps its first two rows and re-evaluates the rest: 121 registers would cost more waves
+//    than the exponentials cost VALU);
 //  * every lane of a wave routes the same tap at once: a row of KW taps is summed per tile column
 //    across the wave (a DPP shift per tap) before one LDS atomic per row, and the grad_weight LDS
 //    atomics hit lane-striped copies (no bank conflicts). LDS atomics cost per instruction, not per
@@ -294,7 +295,10 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     const bool dil = a >= 0.0f;
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
-    float v[KEEPV ? K : 1], e[K <= 49 ? K : 1];
+    // Taps whose e stays in registers between the passes: all up to 7x7; for 11x11 the first two
+    // rows (three waves per SIMD still; a third row takes 256 registers), except IDENTITY (no room).
+    constexpr int KE = K <= 49 ? K : (MK == MK_IDENT ? 0 : 2 * KW);
+    float v[KEEPV ? K : 1], e[KE > 0 ? KE : 1];
     float ref;
     if constexpr (KEEPV)
     {
@@ -347,7 +351,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             if constexpr (MASKED) ek = tm.col[kw] ? ek : 0.0f;
             s = s + ek;  // unfused, as in the reference
             wsum = fmaf(ek, vk, wsum);
-            if constexpr (K <= 49) e[k] = ek;
+            if (k < KE) e[k] = ek;  // a constant condition once unrolled
         }
     }
     if constexpr (!KEEPV) asm volatile("" ::: "memory");
@@ -380,14 +384,14 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             const int k = kh * KW + kw;
             const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
             float ekr;
-            if constexpr (K > 49)
+            if (k >= KE)
             {
                 ekr = exp_ref((vk - ref) * a, lo);
                 if constexpr (MASKED) ekr = tm.col[kw] ? ekr : 0.0f;
             }
             else
             {
-                ekr = e[k];
+                ekr = e[k < KE ? k : 0];
             }
             const float pg = ekr * scaled;
             const float centered = vk - outc;
