@@ -581,13 +581,13 @@ static bool has_static(const Geom& g)
     return g.KH == 3 || g.KH == 5 || g.KH == 7 || g.KH == 11;
 }
 
-// Rows per wave of the static kernel: the TAPS mode holds (RH + KH - 1) x KW window values in
-// registers (4 rows from 5x5 up: fewer registers, more waves, measured faster), the VALUE modes one
-// column of RH + KH - 1.
+// Rows per wave of the static kernel: 4 for every size and mode. Fewer registers and more waves beat
+// the better LDS reuse of 8 rows (measured on MI355X: 7-27% faster from 3x3 to 11x11, VALUE, PACKED
+// and TAPS alike); 2 rows is no faster.
 template <typename T, int KH, int MODE>
 constexpr int static_rows()
 {
-    return sizeof(T) == 8 ? 4 : (MODE == FWD_TAPS && KH >= 5 ? 4 : 8);
+    return 4;
 }
 
 template <typename T>
