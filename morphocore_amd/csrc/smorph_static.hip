@@ -436,10 +436,11 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     int work = xcd_work_index(blockIdx.x, gridDim.x);
-    const int strip = work % p.nstrips;
-    work /= p.nstrips;
+    // Input channel fastest: the workgroups of one XCD share their strip's output gradients in L2.
     const int i = work % g.Cin;
-    const int b = work / g.Cin;
+    work /= g.Cin;
+    const int strip = work % p.nstrips;
+    const int b = work / p.nstrips;
     const int64_t plane = g.plane();
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
     const int slot = b * p.nstrips + strip;
