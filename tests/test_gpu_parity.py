@@ -307,6 +307,26 @@ def test_smorph_parity(merge, a, dtype):
         assert normwise_error(actual, expected) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("a", [-20.0, 0.5, 20.0])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("K,H", [(3, 14), (7, 24), (11, 30)])
+def test_smorph_static_interior_and_border_tiles(K, H, merge, a):
+    """The float32 static smorph kernels at 3x3 / 7x7 / 11x11 on images wide and tall enough that
+    some 64 x 4 tiles lie inside the image (the unmasked path) next to border tiles (masked), with a
+    partial last tile in both directions."""
+    B, Cin, Cout, W = 1, 2, 3, 200
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(31, B, Cin, H, W, kind="randn")
+    w = seeded(32, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    alpha = torch.full((pairs,), a) + seeded(33, pairs, kind="randn", scale=0.1)
+    alpha = alpha.reshape((Cout,) if merge == "identity" else (Cout, Cin))
+    g = seeded(34, B, Cout, H, W, kind="randn")
+    for actual, expected in _smorph_case(merge, x, w, alpha, g):
+        assert normwise_error(actual, expected) <= 1e-6
+
+
 @pytest.mark.parametrize("merge", ["sum", "max"])
 def test_smorph_shared_alpha(merge):
     x = seeded(25, 1, 2, 11, 13, kind="randn")
