@@ -422,10 +422,12 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     return route ? asum : 0.0f;
 }
 
-// Five waves per SIMD requested: the 7x7 kernel then fits 96 registers without spills and runs ~5%
-// faster than at four (larger elements keep what they need: the request is a hint).
+// Waves per SIMD requested (measured on MI355X): up to 7x7 six (80 registers, a few spilled; 7% faster
+// than four, five fit without spills), 11x11 five (95 registers, 2 spilled; 16% faster than three,
+// with 16 bin copies so that five workgroups' LDS fits a CU).
 template <int MK, int KH, int KW>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(5, 8))) void smorph_bwd_static(const SmorphBwdParams<float> p)
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 6, 8))) void smorph_bwd_static(
+    const SmorphBwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
