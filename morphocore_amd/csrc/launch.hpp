@@ -77,6 +77,8 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);
+template <typename T>
+hipError_t round_async(const double* src, T* dst, int64_t n, hipStream_t stream);
 
 // Slots summed per group by the first stage of a long reduction.
 constexpr int REDUCE_GROUP = 32;

@@ -1,8 +1,10 @@
 // Dilation / erosion backward for gfx950: gradient routing from the winners of the forward pass.
 //
 // MAX / MIN (morpho_bwd_packed_kernel): one workgroup per (output channel, pixel chunk) scatters each
-// output gradient to its packed (channel, tap): grad_input by global float atomics (one per output
-// pixel), grad_weight into LDS bins that become this workgroup's partial slot.
+// output gradient to its packed (channel, tap): grad_input by global double atomics (one per output
+// pixel; a pixel can collect up to Cout * KH * KW of them, which float32 sums would round past the
+// 1e-6 tolerance), rounded once to float32 afterwards, grad_weight into LDS bins that become this
+// workgroup's partial slot.
 // Reference semantics: morpho_op_cpu_backward.hxx:39-88 (run_single_winner).
 //
 // ADD / AVERAGE / IDENTITY: every channel pair routes g * scale to its own first extremal tap
@@ -37,7 +39,7 @@ struct PackedParams
 {
     const int32_t* __restrict__ idx;
     const T* __restrict__ gout;
-    T* __restrict__ gin;
+    Acc* __restrict__ gin;  // double accumulator of grad_input (the output itself for float64)
     T* __restrict__ part;
     Geom g;
     int nchunks;
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
         const int c = packed >> 16, k = packed & 0xFFFF;
         const int kh = k / g.KW, kw = k - kh * g.KW;
         const int iy = h + ph - kh, ix = wc + pw - kw;
-        if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], gv);
+        if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], (Acc)gv);
         if (p.lds_bins)
             lds_add(&bins[(int64_t)c * K + k], (Acc)(sign * gv));
         else
@@ -728,6 +730,7 @@ size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
     partials<T>(merge, g, part_bytes, nslots);
     size_t bytes = align_up(part_bytes) + align_up(reduce_slots_scratch<T>(nslots, (int64_t)g.Cout * g.Cw * g.taps()));
     if (!has_indices) bytes += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(T));
+    if (packed_winners(merge) && sizeof(T) != sizeof(Acc)) bytes += align_up((size_t)g.B * g.Cin * g.plane() * sizeof(Acc));
     return bytes;
 }
 
@@ -740,8 +743,11 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     const bool packed = packed_winners(merge);
     // The gather kernel writes every grad_input pixel itself; the others accumulate onto zeros.
     const bool gather = !packed && (int64_t)g.B * g.Cout * g.plane() > 0 && plan_taps<T>(merge, g).gather;
-    if (!gather)
-        if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
+    const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
+    // float32 max / min round their double grad_input accumulator into every pixel at the end.
+    const bool rounded = packed && sizeof(T) != sizeof(Acc) && (int64_t)g.B * g.Cout * g.plane() > 0;
+    if (!gather && !rounded)
+        if ((err = fill_async<T>(grad_in, gin_n, T(0), stream)) != hipSuccess) return err;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return fill_async<T>(grad_w, wnumel, T(0), stream);
 
     size_t part_bytes;
@@ -758,6 +764,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         T* tmp_out = reinterpret_cast<T*>(ws + align_up(indices_bytes(merge, g)));
         if ((err = morpho_forward<T>(OP, merge, replicate, fill, x, w, tmp_out, idx, g, stream)) != hipSuccess) return err;
         indices = idx;
+        ws += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(T));
     }
 
     if (packed)
@@ -765,10 +772,17 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         const PackedPlan s = plan_packed<T>(g);
         if (!s.lds_bins)
             if ((err = fill_async<T>(part, (int64_t)s.nchunks * wnumel, T(0), stream)) != hipSuccess) return err;
+        // float32: grad_input summed in a double buffer of the workspace, rounded once at the end.
+        Acc* gin_acc = reinterpret_cast<Acc*>(grad_in);
+        if constexpr (sizeof(T) != sizeof(Acc))
+        {
+            gin_acc = reinterpret_cast<Acc*>(ws);
+            if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
+        }
         PackedParams<T> p{};
         p.idx = static_cast<const int32_t*>(indices);
         p.gout = grad_out;
-        p.gin = grad_in;
+        p.gin = gin_acc;
         p.part = part;
         p.g = g;
         p.nchunks = s.nchunks;
@@ -776,6 +790,8 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         p.chunk = s.chunk;
         morpho_bwd_packed_kernel<T, OP><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
         if ((err = hipGetLastError()) != hipSuccess) return err;
+        if constexpr (sizeof(T) != sizeof(Acc))
+            if ((err = round_async<T>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
         return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
     }
 

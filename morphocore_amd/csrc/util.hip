@@ -39,6 +39,13 @@ __global__ __launch_bounds__(BLOCK) void reduce_groups_kernel(const T* __restric
     }
 }
 
+// dst[j] = (T)src[j]: a double accumulator rounded once into its float32 result.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void round_kernel(const double* __restrict__ src, T* __restrict__ dst, int64_t n)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) dst[j] = (T)src[j];
+}
+
 static int grid_for(int64_t n)
 {
     const int64_t blocks = (n + BLOCK - 1) / BLOCK;
@@ -75,6 +82,15 @@ hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, T* s
     return hipGetLastError();
 }
 
+template <typename T>
+hipError_t round_async(const double* src, T* dst, int64_t n, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    round_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(src, dst, n);
+    return hipGetLastError();
+}
+
+template hipError_t round_async<float>(const double*, float*, int64_t, hipStream_t);
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
 template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
 template size_t reduce_slots_scratch<float>(int, int64_t);

@@ -116,6 +116,31 @@ def _backward_case(op, merge, padding, dtype, x, w, g, save_indices=True, pv=0.5
     return _np(out), ref, _np(xd.grad), gx, _np(wd.grad), gw
 
 
+@pytest.mark.parametrize("merge,K,dtype", [("max", 3, torch.float32), ("min", 5, torch.float32), ("sum", 3, torch.float32),
+                                           ("mean", 5, torch.float32), ("identity", 3, torch.float32),
+                                           ("identity", 3, torch.float64), ("max", 11, torch.float32)])
+def test_forward_backward_large_grid(merge, K, dtype):
+    """Launches of at least 1024 workgroups, which take the forward's full launch shape (4 rows per
+    wave, 4 or 2 output channels per workgroup, IDENTITY 8 channels per workgroup with a partial last
+    group) rather than the small-grid one that the smaller cases here use: values and winners bit
+    exact, gradients within tolerance."""
+    B, Cin, Cout, H, W = 4, 2, 16, 256, 256
+    if merge == "identity":
+        B, Cin, H, W = 6, 20, 256, 320
+        Cout = Cin
+    x = seeded(41, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(42, *_weight_shape(merge, Cin, Cout, K, K), dtype=dtype, kind="randn", scale=0.2)
+    g = seeded(43, B, Cout, H, W, dtype=dtype, kind="randn")
+    out, ref, gx, rgx, gw, rgw = _backward_case(O.DILATION, merge, "replicate", dtype, x, w, g)
+    assert np.array_equal(out, ref)
+    assert normwise_error(gx, rgx) <= TOL[dtype]
+    assert normwise_error(gw, rgw) <= TOL[dtype]
+    if merge in ("max", "min"):
+        kout, kidx = kernel_forward(O.DILATION, merge, "replicate", 0.5, x, w, save=True)
+        _, ridx = O.morpho_forward(O.DILATION, O.MERGES[merge], O.REPLICATE, 0.5, x.numpy(), w.numpy(), save_indices=True)
+        assert np.array_equal(kout, ref) and np.array_equal(kidx, ridx)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("padding", ["geodesic", "replicate", "constant"])
 @pytest.mark.parametrize("merge", MERGES)
