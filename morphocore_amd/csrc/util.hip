@@ -12,15 +12,16 @@ __global__ __launch_bounds__(BLOCK) void fill_kernel(T* __restrict__ p, int64_t 
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) p[j] = v;
 }
 
-// out[j] = sum over slots s = 0, 1, ... of part[s * n + j], always in slot order.
+// out[j] = sum over slots s = 0, 1, ... of part[s * n + j], always in slot order, accumulated in
+// double and rounded once.
 template <typename T>
 __global__ __launch_bounds__(BLOCK) void reduce_slots_kernel(const T* __restrict__ part, int nslots, int64_t n, T* __restrict__ out)
 {
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
     {
-        T s = T(0);
-        for (int slot = 0; slot < nslots; ++slot) s += part[(int64_t)slot * n + j];
-        out[j] = s;
+        Acc s = Acc(0);
+        for (int slot = 0; slot < nslots; ++slot) s += (Acc)part[(int64_t)slot * n + j];
+        out[j] = (T)s;
     }
 }
 
@@ -33,9 +34,9 @@ __global__ __launch_bounds__(BLOCK) void reduce_groups_kernel(const T* __restric
     const int s1 = min(s0 + REDUCE_GROUP, nslots);
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
     {
-        T s = T(0);
-        for (int slot = s0; slot < s1; ++slot) s += part[(int64_t)slot * n + j];
-        tmp[(int64_t)blockIdx.y * n + j] = s;
+        Acc s = Acc(0);
+        for (int slot = s0; slot < s1; ++slot) s += (Acc)part[(int64_t)slot * n + j];
+        tmp[(int64_t)blockIdx.y * n + j] = (T)s;
     }
 }
 
