@@ -177,13 +177,42 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
     gen = torch.Generator(device=dev).manual_seed(2)
     grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
     gx, gw, ga = torch.empty_like(x), torch.empty_like(w), torch.empty_like(alpha)
-    native.smorph_forward(merge, x, w, alpha, out, geom)
+    # The step's own choice: the forward saves the pair statistics when the autograd layer would.
+    from morphocore_amd.functional._autograd import _save_smorph_stats
+
+    nbytes = native.smorph_stats_bytes(merge, dtype, geom)
+    stats = torch.empty(nbytes // 4, dtype=torch.float32, device=dev) if _save_smorph_stats(nbytes, True, dev) else None
+    native.smorph_forward(merge, x, w, alpha, out, geom, stats=stats)
 
     def launch():
-        native.smorph_backward(merge, x, w, alpha, out, grad, gx, gw, ga, geom)
+        native.smorph_backward(merge, x, w, alpha, out, grad, gx, gw, ga, geom, stats=stats)
 
+    if stats is not None:
+        # Without the recomputation of S and W (8 flop per tap), a backward tap is its exponential
+        # and its routing: 10 flop.
+        what = (f"smorph backward, merge {cfg.get('merge', 'sum')}, alpha {a:g}, from the forward's saved pair statistics "
+                "(mca_smorph_backward_stats_f32: kernel + zero-fill + slot reduction)")
+        return launch, 10 * t, "flop", what
     what = f"smorph backward, merge {cfg.get('merge', 'sum')}, alpha {a:g} (mca_smorph_backward: kernel + zero-fill + slot reduction)"
     return launch, 18 * t, "flop", what
+
+
+def step_work(cfg):
+    """Algorithmic work of one whole step (forward + backward), the convention of the dominant
+    kernel's: (work, "flop" | "bytes"), or None for configs[0] (launch bound). Max-plus taps 2 flop;
+    smorph forward taps 8 flop, backward taps 18 (recomputation included, whatever the kernels do);
+    the identity config's bytes: x and out forward, x, grad_out and grad_x backward."""
+    t = taps(cfg)
+    B, Cin, H, W = cfg["x"]
+    Cout = cfg["w"][0]
+    if cfg["kind"] == "morpho" and cfg.get("bound") == "hbm":
+        esz = 8 if cfg["dtype"] == "f64" else 4
+        return 5 * B * Cin * H * W * esz, "bytes"
+    if cfg["kind"] == "morpho":
+        return (None if B * Cout * H * W < (1 << 20) else (4 * t + 2 * B * Cout * Cin * H * W, "flop"))
+    if cfg["kind"] == "smorph":
+        return 26 * t * len(cfg["alphas"]), "flop"
+    return 2 * t + 26 * t + 2 * t, "flop"  # stack: dilation, smorph, erosion (index scatters not counted)
 
 
 def time_launches(torch, launch, target_s=1.0, max_n=50):
@@ -311,6 +340,15 @@ def main():
         roof = {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak}
     roof["traffic"] = measured_traffic(args.config)
     roof.update({"kernel": what, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": dwork, "work_unit": dunit})
+    # The whole step against the same peak (the fwd+bwd figure the configs' targets are stated on).
+    sw = step_work(cfg)
+    step_roof = None
+    if sw is not None:
+        rate = sw[0] / (ms_per_step * 1e-3)
+        if sw[1] == "bytes":
+            step_roof = {"bound": "hbm", "achieved": rate / 1e9, "unit": "GB/s", "frac": rate / 1e9 / PEAK_HBM_GBS, "work_per_step": sw[0]}
+        else:
+            step_roof = {"bound": "valu", "achieved": rate / 1e12, "unit": "TFLOP/s", "frac": rate / 1e12 / roof["peak"], "work_per_step": sw[0]}
     line = {
         "metric": METRIC,
         "value": n_out / (ms_per_step * 1e-3),
@@ -328,6 +366,7 @@ def main():
         "data": "synthetic (seeded torch generators), inputs resident in HBM",
         "config": {"workload": f"configs[{args.config - 1}]: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]), "parallelism": "none (1 GPU)"},
         "roofline": roof,
+        "step_roofline": step_roof,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -118,6 +118,23 @@ int mca_smorph_backward_f64(int merge, const double* input, const double* weight
                             int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* Smorph with saved pair statistics (float32; square 3x3, 5x5, 7x7 and 11x11 elements). No reference
+ * counterpart: the reference's backward recomputes each pair's softmax statistics from the saved
+ * input (smorph.cu:63-103, smorph_cpu_kernels.hxx:387-638). The forward below also stores, for every
+ * channel pair at every output pixel, the window's extremum, 1 / S and W / S (three float32 arrays of
+ * B * Cout * P * H * W values, P = Cin, or 1 for IDENTITY; mca_smorph_stats_bytes_f32 bytes, 0 when
+ * the configuration has no such path); the backward below reads them and evaluates each tap's
+ * exponential once. Both produce bit for bit what mca_smorph_forward_f32 / mca_smorph_backward_f32
+ * produce (the same workspace). */
+size_t mca_smorph_stats_bytes_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW);
+int mca_smorph_forward_stats_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, float* stats,
+                                 int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                 void* stream);
+int mca_smorph_backward_stats_f32(int merge, const float* input, const float* weight, const float* alpha, const float* output,
+                                  const float* stats, const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha,
+                                  int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,9 @@ EXPORTS = (
     "mca_smorph_backward_workspace_size_f64",
     "mca_smorph_backward_f32",
     "mca_smorph_backward_f64",
+    "mca_smorph_stats_bytes_f32",
+    "mca_smorph_forward_stats_f32",
+    "mca_smorph_backward_stats_f32",
 )
 
 _lib = None
@@ -75,6 +78,12 @@ def lib() -> ctypes.CDLL:
         f = getattr(so, f"mca_smorph_backward_{sfx}")
         f.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
         f.restype = _I
+    so.mca_smorph_stats_bytes_f32.argtypes = [_I] + _GEOM
+    so.mca_smorph_stats_bytes_f32.restype = _SZ
+    so.mca_smorph_forward_stats_f32.argtypes = [_I, _P, _P, _P, _P, _P] + _GEOM + [_P]
+    so.mca_smorph_forward_stats_f32.restype = _I
+    so.mca_smorph_backward_stats_f32.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
+    so.mca_smorph_backward_stats_f32.restype = _I
     _lib = so
     return so
 
@@ -130,17 +139,35 @@ def morpho_backward(op, merge, replicate, fill, x, weight, weight_batch_stride, 
              _ptr(grad_w), *geom, _ptr(ws), ws.numel(), _stream(x)))
 
 
-def smorph_forward(merge, x, weight, alpha_pairs, out, geom):
-    """Enqueue the smorph forward (C ABI mca_smorph_forward_*)."""
+def smorph_stats_bytes(merge, dtype, geom) -> int:
+    """Bytes of the pair statistics the smorph forward can save for its backward (C ABI
+    mca_smorph_stats_bytes_f32); 0 when the configuration has no such path (float64, other sizes)."""
+    if dtype != torch.float32:
+        return 0
+    return int(lib().mca_smorph_stats_bytes_f32(merge, *geom))
+
+
+def smorph_forward(merge, x, weight, alpha_pairs, out, geom, stats=None):
+    """Enqueue the smorph forward (C ABI mca_smorph_forward_*); with `stats` (a float32 buffer of
+    smorph_stats_bytes bytes) the pair statistics are saved too (mca_smorph_forward_stats_f32)."""
+    if stats is not None:
+        _check(lib().mca_smorph_forward_stats_f32(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), _ptr(stats), *geom,
+                                                  _stream(x)))
+        return
     f = getattr(lib(), f"mca_smorph_forward_{_sfx(x)}")
     _check(f(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), *geom, _stream(x)))
 
 
-def smorph_backward(merge, x, weight, alpha_pairs, out, grad_out, grad_in, grad_w, grad_alpha, geom):
-    """Enqueue the smorph backward (C ABI mca_smorph_backward_*), workspace from torch."""
+def smorph_backward(merge, x, weight, alpha_pairs, out, grad_out, grad_in, grad_w, grad_alpha, geom, stats=None):
+    """Enqueue the smorph backward (C ABI mca_smorph_backward_*, or mca_smorph_backward_stats_f32 with
+    the forward's saved `stats`), workspace from torch."""
     so, sfx = lib(), _sfx(x)
     nbytes = getattr(so, f"mca_smorph_backward_workspace_size_{sfx}")(merge, *geom)
     ws = _workspace(nbytes, x.device)
+    if stats is not None:
+        _check(so.mca_smorph_backward_stats_f32(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), _ptr(stats), _ptr(grad_out),
+                                                _ptr(grad_in), _ptr(grad_w), _ptr(grad_alpha), *geom, _ptr(ws), ws.numel(), _stream(x)))
+        return
     f = getattr(so, f"mca_smorph_backward_{sfx}")
     _check(f(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w), _ptr(grad_alpha),
              *geom, _ptr(ws), ws.numel(), _stream(x)))

@@ -113,13 +113,22 @@ int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* inpu
 
 template <typename T>
 int smorph_forward_impl(int merge, const T* input, const T* weight, const T* alpha, T* output, int64_t B, int64_t Cin, int64_t Cout,
-                        int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+                        int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream, float* stats = nullptr)
 {
     mca::Geom g{};
     int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
     if (rc != MCA_OK) return rc;
     if ((rc = check_lds(mca::smorph_lds<T>(merge, g, false))) != MCA_OK) return rc;
-    return hip_status(mca::smorph_forward<T>(merge, input, weight, alpha, output, g, (hipStream_t)stream));
+    return hip_status(mca::smorph_forward<T>(merge, input, weight, alpha, output, g, (hipStream_t)stream, stats));
+}
+
+// Checks of the saved-statistics entry points: the configuration has them and a buffer is given.
+int check_stats(int merge, const mca::Geom& g, const void* stats)
+{
+    if (mca::smorph_stats_values(merge, g) == 0)
+        return fail("No saved smorph statistics for this configuration (float32, square 3x3, 5x5, 7x7 or 11x11 elements only)");
+    if (!stats) return fail("stats must not be null");
+    return MCA_OK;
 }
 
 template <typename T>
@@ -133,7 +142,7 @@ size_t smorph_workspace_impl(int merge, int64_t B, int64_t Cin, int64_t Cout, in
 template <typename T>
 int smorph_backward_impl(int merge, const T* input, const T* weight, const T* alpha, const T* output, const T* grad_output, T* grad_input,
                          T* grad_weight, T* grad_alpha, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
-                         int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+                         int64_t KW, void* workspace, size_t workspace_bytes, void* stream, const float* stats = nullptr)
 {
     mca::Geom g{};
     int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
@@ -143,7 +152,7 @@ int smorph_backward_impl(int merge, const T* input, const T* weight, const T* al
     if (workspace_bytes < need || (need > 0 && !workspace))
         return fail("Workspace too small: " + std::to_string(workspace_bytes) + " bytes given, " + std::to_string(need) + " needed");
     return hip_status(mca::smorph_backward<T>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, g,
-                                              workspace, workspace_bytes, (hipStream_t)stream));
+                                              workspace, workspace_bytes, (hipStream_t)stream, stats));
 }
 
 }  // namespace
@@ -247,6 +256,37 @@ int mca_smorph_backward_f64(int merge, const double* input, const double* weight
 {
     return smorph_backward_impl<double>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, B, Cin,
                                         Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+size_t mca_smorph_stats_bytes_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return (size_t)mca::smorph_stats_values(merge, g) * 3 * sizeof(float);
+}
+
+int mca_smorph_forward_stats_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, float* stats,
+                                 int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                 void* stream)
+{
+    mca::Geom g{};
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_stats(merge, g, stats)) != MCA_OK) return rc;
+    return smorph_forward_impl<float>(merge, input, weight, alpha, output, B, Cin, Cout, Cw, H, W, KH, KW, stream, stats);
+}
+
+int mca_smorph_backward_stats_f32(int merge, const float* input, const float* weight, const float* alpha, const float* output,
+                                  const float* stats, const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha,
+                                  int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                  void* workspace, size_t workspace_bytes, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_stats(merge, g, stats)) != MCA_OK) return rc;
+    return smorph_backward_impl<float>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, B, Cin, Cout,
+                                       Cw, H, W, KH, KW, workspace, workspace_bytes, stream, stats);
 }
 
 }  // extern "C"

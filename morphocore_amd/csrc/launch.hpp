@@ -61,8 +61,14 @@ template <typename T>
 hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
                            T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// Values in each of the three arrays of saved smorph pair statistics (float32 static kernels only;
+// 0 when the configuration has none).
+int64_t smorph_stats_values(int merge, const Geom& g);
+
+// `stats`: where to save the pair statistics (three arrays of smorph_stats_values values), or null.
 template <typename T>
-hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream);
+hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream,
+                          float* stats = nullptr);
 
 template <typename T>
 size_t smorph_lds(int merge, const Geom& g, bool backward);
@@ -70,9 +76,11 @@ size_t smorph_lds(int merge, const Geom& g, bool backward);
 template <typename T>
 size_t smorph_backward_workspace(int merge, const Geom& g);
 
+// `stats`: the pair statistics the forward saved, or null (recomputed).
 template <typename T>
 hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, const T* out, const T* grad_out, T* grad_in, T* grad_w,
-                           T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                           T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                           const float* stats = nullptr);
 
 // Shared helpers (util.hip).
 template <typename T>

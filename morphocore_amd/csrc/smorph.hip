@@ -367,9 +367,12 @@ static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t str
     return hipGetLastError();
 }
 
+int64_t smorph_stats_values(int merge, const Geom& g) { return smorph_stats_count<float>(merge, g); }
+
 template <typename T>
-hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream)
+hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream, float* stats)
 {
+    if (stats && smorph_stats_count<T>(merge, g) == 0) return hipErrorInvalidValue;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return hipSuccess;
     SmorphFwdParams<T> p{};
     p.x = x;
@@ -377,6 +380,8 @@ hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* 
     p.alpha = alpha;
     p.out = out;
     p.target = nullptr;
+    p.pstats = stats;
+    p.nstat = smorph_stats_count<T>(merge, g);
     p.g = g;
     // The static kernels (smorph_static.hip) put one output row on each wave.
     p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
@@ -394,10 +399,12 @@ hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* 
 
 template <typename T>
 hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, const T* out, const T* grad_out, T* grad_in, T* grad_w,
-                           T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
+                           T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream, const float* stats)
 {
     hipError_t err;
     if (workspace_bytes < smorph_backward_workspace<T>(merge, g)) return hipErrorInvalidValue;
+    if (stats && smorph_stats_count<T>(merge, g) == 0) return hipErrorInvalidValue;
+    const int64_t nstat = smorph_stats_count<T>(merge, g);
     const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g);
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
@@ -419,7 +426,12 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
         if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
     }
 
-    if (merge == MERGE_MAX || merge == MERGE_MIN)
+    if (stats && (merge == MERGE_MAX || merge == MERGE_MIN))
+    {
+        if constexpr (sizeof(T) == 4)
+            if ((err = launch_smorph_counts_saved(stats + 2 * nstat, out, counts, g, stream)) != hipSuccess) return err;
+    }
+    else if (merge == MERGE_MAX || merge == MERGE_MIN)
     {
         SmorphFwdParams<T> f{};
         f.x = x;
@@ -444,6 +456,8 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     p.gin = grad_in;
     p.part_w = part_w;
     p.part_a = part_a;
+    p.pstats = stats;
+    p.nstat = nstat;
     p.g = g;
     p.t = s.t;
     p.nstrips = s.nstrips;
@@ -478,11 +492,11 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
 }
 
 #define MCA_INSTANTIATE_SMORPH(T)                                                                                                   \
-    template hipError_t smorph_forward<T>(int, const T*, const T*, const T*, T*, const Geom&, hipStream_t);                        \
+    template hipError_t smorph_forward<T>(int, const T*, const T*, const T*, T*, const Geom&, hipStream_t, float*);                \
     template size_t smorph_lds<T>(int, const Geom&, bool);                                                                          \
     template size_t smorph_backward_workspace<T>(int, const Geom&);                                                                 \
     template hipError_t smorph_backward<T>(int, const T*, const T*, const T*, const T*, const T*, T*, T*, T*, const Geom&, void*, \
-                                           size_t, hipStream_t);
+                                           size_t, hipStream_t, const float*);
 
 MCA_INSTANTIATE_SMORPH(float)
 MCA_INSTANTIATE_SMORPH(double)

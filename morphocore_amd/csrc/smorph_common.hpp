@@ -98,6 +98,10 @@ struct SmorphFwdParams
     const T* __restrict__ alpha;
     T* __restrict__ out;           // forward output, or the winner counts in STATS mode
     const T* __restrict__ target;  // STATS mode: the forward output
+    // Saved pair statistics (float32 static kernels; null: none saved): ref, then 1 / S, then W / S of
+    // every (batch element, output channel, pair, pixel), `nstat` values each.
+    float* __restrict__ pstats;
+    int64_t nstat;
     Geom g;
     Tiling t;
     int average;
@@ -136,6 +140,8 @@ struct SmorphBwdParams
     T* __restrict__ gin;
     T* __restrict__ part_w;
     T* __restrict__ part_a;
+    const float* __restrict__ pstats;  // the forward's saved pair statistics, or null (recomputed)
+    int64_t nstat;
     Geom g;
     Tiling t;
     int nstrips;
@@ -167,8 +173,22 @@ __host__ __device__ inline bool smorph_bwd_lds_partials(const Geom& g, bool iden
     return K <= 25 && (identity ? 1 : g.Cout) * (K + 1) <= SMORPH_LDS_PARTIALS;
 }
 
-// Launchers of the static-size kernels (smorph_static.hip), float32.
+// Pair statistics the float32 static forward can save for the backward: ref (the window's extremum),
+// 1 / S and W / S of every channel pair at every output pixel, index
+// ((b * Cout + o) * pairs_per_output + i') * H * W + pixel (i' = i, or 0 for IDENTITY). 0 when the
+// configuration has no static kernels.
+template <typename T>
+inline int64_t smorph_stats_count(int merge, const Geom& g)
+{
+    if (!smorph_static_supported<T>(g)) return 0;
+    return (int64_t)g.B * g.Cout * (merge == MERGE_IDENTITY ? 1 : g.Cin) * g.plane();
+}
+
+// Launchers of the static-size kernels (smorph_static.hip), float32; a non-null `pstats` selects the
+// forward that saves the pair statistics and the backward that reads them.
 hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream);
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream);
+// MAX / MIN winner counts of every output pixel from the saved W / S values (`outp`).
+hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, const Geom& g, hipStream_t stream);
 
 }  // namespace mca

@@ -140,7 +140,9 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
     Wsum = wsum;
 }
 
-template <int MK, int KH, int KW, bool STATS>
+// SAVE: also store each pair's ref, 1 / S and W / S at every in-image pixel (p.pstats), which the
+// backward then reads instead of recomputing them.
+template <int MK, int KH, int KW, bool STATS, bool SAVE>
 __global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
@@ -223,18 +225,30 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams
         const float* w = wl[buf];
         const float a = w[K];
         const bool dil = a >= 0.0f;
-        float S, Wsum;
+        float ref, S, Wsum;
         if (interior)
         {
-            const float ref = smorph_ref<KH, KW, false>(xb, w, dil, tm);
+            ref = smorph_ref<KH, KW, false>(xb, w, dil, tm);
             smorph_sums<KH, KW, false>(xb, w, a, ref, tm, S, Wsum);
         }
         else
         {
-            const float ref = smorph_ref<KH, KW, true>(xb, w, dil, tm);
+            ref = smorph_ref<KH, KW, true>(xb, w, dil, tm);
             smorph_sums<KH, KW, true>(xb, w, a, ref, tm, S, Wsum);
         }
         const float inv = 1.0f / S;
+        if constexpr (SAVE)
+        {
+            // Streamed out (read back by the backward, long after this kernel): non-temporal stores.
+            if (in)
+            {
+                const int pi = MK == MK_IDENT ? 0 : i;
+                float* q = p.pstats + ((((int64_t)b * g.Cout + o) * (MK == MK_IDENT ? 1 : g.Cin) + pi) * plane + (int64_t)h * g.W + wc);
+                __builtin_nontemporal_store(ref, q);
+                __builtin_nontemporal_store(inv, q + p.nstat);
+                __builtin_nontemporal_store(Wsum * inv, q + 2 * p.nstat);
+            }
+        }
         if constexpr (STATS)
         {
             if (is_winner(Wsum * inv, tgt)) m = m + 1.0f;
@@ -275,100 +289,81 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams
 // per wave; for each tile it walks every output channel o.
 // ------------------------------------------------------------------------------------------------
 
-// One pair (o, i) at this lane's pixel: the forward's ref, S and W (every tap's e, and v up to 7x7,
-// kept), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input (the LDS tile), to
-// the grad_weight bin of tap k and to grad_alpha (returned: the sum of p_k (v_k - ref)(v_k - out)
-// over the taps). gv is g * scale (0 outside the image); for MAX / MIN it is divided by the pixel's
-// winner count, and only a pair within 1e-6 of the merged output outv routes.
 // The value of the next lower lane (0 in lane 0): DPP wave_shr:1 with bound_ctrl.
 __device__ __forceinline__ float wave_shift_up(float v)
 {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, true));
 }
 
-template <int MK, int KH, int KW, bool MASKED>
+// The forward statistics of one pair at this lane's pixel: ref (the window's extremum), 1 / S and
+// W / S (taken from the forward's saved values, or recomputed).
+struct PairStats
+{
+    float ref, inv, outp;
+};
+
+// One pair (o, i) at this lane's pixel: the forward's ref, S and W (recomputed unless SAVED, every
+// tap's e kept up to 7x7), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input
+// (the LDS tile), to the grad_weight bin of tap k and to grad_alpha (returned: the sum of
+// p_k (v_k - ref)(v_k - out) over the taps). gv is g * scale (0 outside the image); for MAX / MIN it
+// is divided by the pixel's winner count, and only a pair within 1e-6 of the merged output outv
+// routes. SAVED: `st` holds the forward's statistics and each e is evaluated once, in the routing.
+template <int MK, int KH, int KW, bool MASKED, bool SAVED>
 __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
-                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
+                                                 PairStats st, const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
-    constexpr bool KEEPV = false;  // v re-read from LDS in each pass: fewer registers, more waves (measured faster)
-    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN;
-    const bool dil = a >= 0.0f;
+    // A lane outside the image with saved statistics holds another pixel's ref, so its e may be
+    // infinite: its c is cleared like a MAX / MIN loser's.
+    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || (SAVED && MASKED);
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     // Taps whose e stays in registers between the passes: all up to 7x7; for 11x11 the first two
     // rows (three waves per SIMD still; a third row takes 256 registers), except IDENTITY (no room).
-    constexpr int KE = K <= 49 ? K : (MK == MK_IDENT ? 0 : 2 * KW);
-    float v[KEEPV ? K : 1], e[KE > 0 ? KE : 1];
-    float ref;
-    if constexpr (KEEPV)
+    constexpr int KE = SAVED ? 0 : (K <= 49 ? K : (MK == MK_IDENT ? 0 : 2 * KW));
+    float e[KE > 0 ? KE : 1];
+    if constexpr (!SAVED)
     {
-        // v of every tap, read once; the extremum over the valid ones.
-        ref = smorph_init(dil);
+        const bool dil = a >= 0.0f;
+        const float ref = smorph_ref<KH, KW, MASKED>(xb, wl, dil, tm);
+        // v is re-read from LDS in each pass: keep the compiler from holding the first pass's loads
+        // in registers across the passes.
+        asm volatile("" ::: "memory");
+        float s = 0.0f, wsum = 0.0f;
 #pragma unroll
         for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-            for (int kw = 0; kw < KW; ++kw) v[kh * KW + kw] = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
-        if (dil)
         {
+            if (MASKED && !tm.row(kh)) continue;
 #pragma unroll
-            for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw)
             {
-                if (MASKED && !tm.row(kh)) continue;
-#pragma unroll
-                for (int kw = 0; kw < KW; ++kw) ref = fmaxf(ref, (!MASKED || tm.col[kw]) ? v[kh * KW + kw] : -std::numeric_limits<float>::infinity());
+                const int k = kh * KW + kw;
+                const float vk = xb[-(kh * COLS + kw)] + wl[k];
+                float ek = exp_ref((vk - ref) * a, lo);
+                // Out-of-image taps: e = 0 leaves S and W as skipping them does, and routes c = 0.
+                if constexpr (MASKED) ek = tm.col[kw] ? ek : 0.0f;
+                s = s + ek;  // unfused, as in the reference
+                wsum = fmaf(ek, vk, wsum);
+                if (k < KE) e[k] = ek;  // a constant condition once unrolled
             }
         }
-        else
-        {
-#pragma unroll
-            for (int kh = 0; kh < KH; ++kh)
-            {
-                if (MASKED && !tm.row(kh)) continue;
-#pragma unroll
-                for (int kw = 0; kw < KW; ++kw) ref = fminf(ref, (!MASKED || tm.col[kw]) ? v[kh * KW + kw] : std::numeric_limits<float>::infinity());
-            }
-        }
-    }
-    else
-    {
-        ref = smorph_ref<KH, KW, MASKED>(xb, wl, dil, tm);
-        // Larger elements re-read v from LDS in each pass: keep the compiler from holding the first
-        // pass's loads in registers across the passes.
         asm volatile("" ::: "memory");
+        st.ref = ref;
+        st.inv = 1.0f / s;
+        st.outp = wsum * st.inv;
     }
-    float s = 0.0f, wsum = 0.0f;
-#pragma unroll
-    for (int kh = 0; kh < KH; ++kh)
-    {
-        if (MASKED && !tm.row(kh)) continue;
-#pragma unroll
-        for (int kw = 0; kw < KW; ++kw)
-        {
-            const int k = kh * KW + kw;
-            const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
-            float ek = exp_ref((vk - ref) * a, lo);
-            // Out-of-image taps: e = 0 leaves S and W as skipping them does, and routes c = 0.
-            if constexpr (MASKED) ek = tm.col[kw] ? ek : 0.0f;
-            s = s + ek;  // unfused, as in the reference
-            wsum = fmaf(ek, vk, wsum);
-            if (k < KE) e[k] = ek;  // a constant condition once unrolled
-        }
-    }
-    if constexpr (!KEEPV) asm volatile("" ::: "memory");
-    const float inv = 1.0f / s;
-    const float outp = wsum * inv;
+    const float ref = st.ref;
     bool route = in;
     if constexpr (MK == MK_MAX || MK == MK_MIN)
     {
         gv = gv / (cnt > 0.0f ? cnt : 1.0f);
-        route = route && is_winner(outp, outv);
+        route = route && is_winner(st.outp, outv);
     }
     // A lane that routes nothing (outside the image, where S may be 0 and out NaN, or a MAX / MIN
     // loser) gets g' = 0 and a finite centre, so every c it adds to the row sums is 0.
-    const float scaled = route ? gv * inv : 0.0f;
-    const float outc = route ? outp : 0.0f;
+    const float scaled = route ? gv * st.inv : 0.0f;
+    const float outc = route ? st.outp : 0.0f;
     float asum = 0.0f;
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh)
@@ -384,7 +379,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         for (int kw = 0; kw < KW; ++kw)
         {
             const int k = kh * KW + kw;
-            const float vk = KEEPV ? v[k] : xb[-(kh * COLS + kw)] + wl[k];
+            const float vk = xb[-(kh * COLS + kw)] + wl[k];
             float ekr;
             if (k >= KE)
             {
@@ -422,11 +417,15 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     return route ? asum : 0.0f;
 }
 
-// Waves per SIMD requested (measured on MI355X): up to 7x7 six (80 registers, a few spilled; 7% faster
-// than four, five fit without spills), 11x11 five (95 registers, 2 spilled; 16% faster than three,
-// with 16 bin copies so that five workgroups' LDS fits a CU).
-template <int MK, int KH, int KW>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 6, 8))) void smorph_bwd_static(
+// Waves per SIMD requested (measured on MI355X), recomputing: up to 7x7 six (80 registers, a few
+// spilled; 7% faster than four, five fit without spills), 11x11 five (95 registers, 2 spilled; 16%
+// faster than three, with 16 bin copies so that five workgroups' LDS fits a CU). With the forward's
+// saved statistics (SAVED) no e is kept: about 50 registers, as many waves as the LDS allows (seven
+// workgroups per CU at 7x7, five at 11x11).
+constexpr int smorph_bwd_waves(int K, bool saved) { return saved ? (K > 49 ? 5 : (K > 25 ? 7 : 8)) : (K > 49 ? 5 : 6); }
+
+template <int MK, int KH, int KW, bool SAVED>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bwd_waves(KH * KW, SAVED), 8))) void smorph_bwd_static(
     const SmorphBwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
@@ -500,6 +499,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         // pixel, one output channel ahead.
         const int64_t pix = (int64_t)min(h, g.H - 1) * g.W + min(wc, g.W - 1);
         float gv_n = 0.0f, cnt_n = 0.0f, out_n = 0.0f;
+        PairStats st_n{0.0f, 0.0f, 0.0f};
         auto load_g = [&](int o) {
             o = min(o, o_end - 1);
             const int64_t oi = ((int64_t)b * g.Cout + o) * plane + pix;
@@ -509,6 +509,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
                 cnt_n = p.counts[oi];
                 out_n = p.out[oi];
             }
+            if constexpr (SAVED)
+            {
+                const float* q = p.pstats + (((int64_t)b * g.Cout + o) * (MK == MK_IDENT ? 1 : g.Cin) + (MK == MK_IDENT ? 0 : i)) * plane + pix;
+                st_n.ref = __builtin_nontemporal_load(q);
+                st_n.inv = __builtin_nontemporal_load(q + p.nstat);
+                st_n.outp = __builtin_nontemporal_load(q + 2 * p.nstat);
+            }
         };
         load_g(o_begin);
         __syncthreads();
@@ -516,14 +523,15 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         {
             const int buf = (o - o_begin) & 1;
             const float gv = in ? gv_n * p.scale : 0.0f, cnt = cnt_n, outv = out_n;
+            const PairStats st = st_n;
             load_g(o + 1);
             const float* w = wl[buf];
             const float a = w[K];
             float asum;
             if (interior)
-                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, false, SAVED>(xb, w, a, gv, cnt, outv, in, st, tm, gxb, bl, lane);
             else
-                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, true, SAVED>(xb, w, a, gv, cnt, outv, in, st, tm, gxb, bl, lane);
             lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
@@ -595,62 +603,101 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
 // Launch
 // ------------------------------------------------------------------------------------------------
 
-template <int KS>
+template <int KS, bool SAVE>
 static hipError_t fwd_size(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
 {
     const unsigned blocks = (unsigned)((int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout);
     if (stats)
     {
         if (mk == MK_MAX)
-            smorph_fwd_static<MK_MAX, KS, KS, true><<<blocks, BLOCK, 0, stream>>>(p);
+            smorph_fwd_static<MK_MAX, KS, KS, true, false><<<blocks, BLOCK, 0, stream>>>(p);
         else
-            smorph_fwd_static<MK_MIN, KS, KS, true><<<blocks, BLOCK, 0, stream>>>(p);
+            smorph_fwd_static<MK_MIN, KS, KS, true, false><<<blocks, BLOCK, 0, stream>>>(p);
         return hipGetLastError();
     }
     switch (mk)
     {
-        case MK_SUM: smorph_fwd_static<MK_SUM, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MAX: smorph_fwd_static<MK_MAX, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MIN: smorph_fwd_static<MK_MIN, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
-        default: smorph_fwd_static<MK_IDENT, KS, KS, false><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SUM: smorph_fwd_static<MK_SUM, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_fwd_static<MK_MAX, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_fwd_static<MK_MIN, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_fwd_static<MK_IDENT, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
+template <bool SAVE>
+static hipError_t fwd_dispatch(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
 {
     switch (p.g.KH)
     {
-        case 3: return fwd_size<3>(mk, stats, p, stream);
-        case 5: return fwd_size<5>(mk, stats, p, stream);
-        case 7: return fwd_size<7>(mk, stats, p, stream);
-        default: return fwd_size<11>(mk, stats, p, stream);
+        case 3: return fwd_size<3, SAVE>(mk, stats, p, stream);
+        case 5: return fwd_size<5, SAVE>(mk, stats, p, stream);
+        case 7: return fwd_size<7, SAVE>(mk, stats, p, stream);
+        default: return fwd_size<11, SAVE>(mk, stats, p, stream);
     }
 }
 
-template <int KS>
+hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream)
+{
+    if (stats && p.pstats) return hipErrorInvalidValue;
+    return p.pstats ? fwd_dispatch<true>(mk, stats, p, stream) : fwd_dispatch<false>(mk, stats, p, stream);
+}
+
+template <int KS, bool SAVED>
 static hipError_t bwd_size(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
     const unsigned blocks = (unsigned)((int64_t)p.g.B * p.g.Cin * p.nstrips);
     switch (mk)
     {
-        case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
-        default: smorph_bwd_static<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_bwd_static<MK_IDENT, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
+template <bool SAVED>
+static hipError_t bwd_dispatch(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
     switch (p.g.KH)
     {
-        case 3: return bwd_size<3>(mk, p, stream);
-        case 5: return bwd_size<5>(mk, p, stream);
-        case 7: return bwd_size<7>(mk, p, stream);
-        default: return bwd_size<11>(mk, p, stream);
+        case 3: return bwd_size<3, SAVED>(mk, p, stream);
+        case 5: return bwd_size<5, SAVED>(mk, p, stream);
+        case 7: return bwd_size<7, SAVED>(mk, p, stream);
+        default: return bwd_size<11, SAVED>(mk, p, stream);
     }
+}
+
+hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
+{
+    return p.pstats ? bwd_dispatch<true>(mk, p, stream) : bwd_dispatch<false>(mk, p, stream);
+}
+
+// MAX / MIN winner counts from the saved statistics: counts[b, o, pixel] = the number of input
+// channels i whose W / S lies within 1e-6 of the merged output (what the counting forward pass
+// computes, smorph_cpu_kernels.hxx:622-627), one thread per output pixel.
+__global__ __launch_bounds__(BLOCK) void smorph_counts_saved(const float* __restrict__ outp, const float* __restrict__ out,
+                                                             float* __restrict__ counts, int64_t n_out, int cin, int64_t plane)
+{
+    const int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (j >= n_out) return;
+    const int64_t bo = j / plane, pix = j - bo * plane;
+    const float t = out[j];
+    const float* q = outp + bo * cin * plane + pix;
+    float m = 0.0f;
+    for (int i = 0; i < cin; ++i)
+        if (is_winner(q[(int64_t)i * plane], t)) m = m + 1.0f;
+    counts[j] = m;
+}
+
+hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, const Geom& g, hipStream_t stream)
+{
+    const int64_t n_out = (int64_t)g.B * g.Cout * g.plane();
+    if (n_out == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((n_out + BLOCK - 1) / BLOCK);
+    smorph_counts_saved<<<blocks, BLOCK, 0, stream>>>(outp, out, counts, n_out, g.Cin, g.plane());
+    return hipGetLastError();
 }
 
 }  // namespace mca

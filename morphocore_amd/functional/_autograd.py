@@ -37,6 +37,22 @@ def _should_save(merge: MorphoMerge, save_indices: bool, needs_grad: bool, B: in
     return nbytes <= _SAVED_TAPS_LIMIT
 
 
+def _save_smorph_stats(nbytes: int, needs_grad: bool, device) -> bool:
+    """Whether the smorph forward keeps its pair statistics (12 bytes per channel pair and output
+    pixel; float32 with a 3x3, 5x5, 7x7 or 11x11 element) so that the backward need not recompute
+    them: when they take at most half of the device memory still available (free, plus what torch's
+    allocator holds unused). MORPHOCORE_AMD_SAVED_STATS_LIMIT caps them further (bytes, 0 disables
+    saving). The result never depends on it."""
+    if not needs_grad or nbytes <= 0:
+        return False
+    limit = os.environ.get("MORPHOCORE_AMD_SAVED_STATS_LIMIT")
+    if limit is not None and nbytes > int(limit):
+        return False
+    free, _ = torch.cuda.mem_get_info(device)
+    avail = free + torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    return nbytes <= avail // 2
+
+
 def to_merge(merge: int) -> MorphoMerge:
     """bindings.cpp:16-20."""
     merge = int(merge)
@@ -235,14 +251,18 @@ class _SmorphFunction(torch.autograd.Function):
         w4c = w4.contiguous()
         alpha_pairs = smorph_pair_alphas(alpha, merge, Cin, Cout)
         out = torch.empty((B, Cout, H, W), dtype=x4c.dtype, device=x4c.device)
-        _native.smorph_forward(int(merge), x4c, w4c, alpha_pairs, out, geom)
-        ctx.save_for_backward(out, alpha, x4c, w4c)
+        stats = None
+        nbytes = _native.smorph_stats_bytes(int(merge), x4c.dtype, geom)
+        if _save_smorph_stats(nbytes, any(ctx.needs_input_grad[:3]), x4c.device):
+            stats = torch.empty(nbytes // 4, dtype=torch.float32, device=x4c.device)
+        _native.smorph_forward(int(merge), x4c, w4c, alpha_pairs, out, geom, stats=stats)
+        ctx.save_for_backward(out, alpha, x4c, w4c, stats)
         ctx.merge = merge
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
-        out, alpha, x4, w4 = ctx.saved_tensors
+        out, alpha, x4, w4, stats = ctx.saved_tensors
         geom = _geom(x4, w4)
         B, Cin, Cout, Cw, H, W, KH, KW = geom
         alpha_pairs = smorph_pair_alphas(alpha, ctx.merge, Cin, Cout)
@@ -252,7 +272,8 @@ class _SmorphFunction(torch.autograd.Function):
         grad_input = torch.empty_like(x4)
         grad_weight = torch.empty_like(w4)
         grad_alpha_pairs = torch.empty_like(alpha_pairs)
-        _native.smorph_backward(int(ctx.merge), x4, w4, alpha_pairs, out, grad_output, grad_input, grad_weight, grad_alpha_pairs, geom)
+        _native.smorph_backward(int(ctx.merge), x4, w4, alpha_pairs, out, grad_output, grad_input, grad_weight, grad_alpha_pairs, geom,
+                                stats=stats)
         # A single alpha shared by every pair receives the gradient of all of them (smorph.cpp:96-98).
         if alpha.numel() == grad_alpha_pairs.numel():
             grad_alpha = grad_alpha_pairs.view_as(alpha)

@@ -332,13 +332,16 @@ def test_smorph_parity(merge, a, dtype):
         assert normwise_error(actual, expected) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("saved", [True, False], ids=["saved-stats", "recomputed"])
 @pytest.mark.parametrize("a", [-20.0, 0.5, 20.0])
 @pytest.mark.parametrize("merge", MERGES)
 @pytest.mark.parametrize("K,H", [(3, 14), (7, 24), (11, 30)])
-def test_smorph_static_interior_and_border_tiles(K, H, merge, a):
+def test_smorph_static_interior_and_border_tiles(K, H, merge, a, saved, monkeypatch):
     """The float32 static smorph kernels at 3x3 / 7x7 / 11x11 on images wide and tall enough that
     some 64 x 4 tiles lie inside the image (the unmasked path) next to border tiles (masked), with a
-    partial last tile in both directions."""
+    partial last tile in both directions; the backward from the forward's saved pair statistics, and
+    recomputing them (saving disabled)."""
+    monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", str(1 << 40) if saved else "0")
     B, Cin, Cout, W = 1, 2, 3, 200
     if merge == "identity":
         Cout = Cin
@@ -350,6 +353,91 @@ def test_smorph_static_interior_and_border_tiles(K, H, merge, a):
     g = seeded(34, B, Cout, H, W, kind="randn")
     for actual, expected in _smorph_case(merge, x, w, alpha, g):
         assert normwise_error(actual, expected) <= 1e-6
+
+
+def _window_extremum(x, w, dilation_like):
+    """ref of every pair and pixel, (B, Cout, Cin, H, W): the extremum of x[y + KH/2 - kh, c + KW/2 - kw]
+    + w[kh, kw] over the in-image taps (one rounding per tap, so exact in float32)."""
+    B, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    PH, PW = KH // 2, KW // 2  # odd sizes: KH = 2 PH + 1
+    fill = -np.inf if dilation_like else np.inf
+    xp = np.full((B, Cin, H + 2 * PH, W + 2 * PW), fill, dtype=np.float32)
+    xp[:, :, PH:PH + H, PW:PW + W] = x
+    best = np.full((B, Cout, Cin, H, W), fill, dtype=np.float32)
+    for kh in range(KH):
+        for kw in range(KW):
+            # Input row y + PH - kh sits at padded row y + 2 PH - kh.
+            oy, ox = 2 * PH - kh, 2 * PW - kw
+            win = xp[:, None, :, oy:oy + H, ox:ox + W] + w[None, :, :, kh, kw, None, None]
+            best = np.maximum(best, win) if dilation_like else np.minimum(best, win)
+    return best
+
+
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("K", [3, 7, 11])
+def test_smorph_saved_stats_abi(K, merge):
+    """mca_smorph_forward_stats_f32 / mca_smorph_backward_stats_f32 through the C ABI: the output is
+    bit for bit the plain forward's; the saved ref is the window's extremum; W / S merges to the
+    output (MAX / MIN / IDENTITY exactly); the backward from the statistics matches the oracle and the
+    recomputing backward."""
+    _, native, _ = _mca()
+    dev = torch.device("cuda")
+    B, Cin, Cout, H, W = 2, 3, 4, 21, 70
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(41, B, Cin, H, W, kind="randn")
+    w = seeded(42, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    # Dilation-like and erosion-like pairs side by side.
+    alpha = torch.where(torch.arange(pairs) % 2 == 0, 3.0, -2.0) + seeded(43, pairs, kind="randn", scale=0.1)
+    g = seeded(44, B, Cout, H, W, kind="randn")
+    m = O.MERGES[merge]
+    geom = (B, Cin, Cout, w.shape[1], H, W, K, K)
+    nbytes = native.smorph_stats_bytes(m, torch.float32, geom)
+    P = 1 if merge == "identity" else Cin
+    assert nbytes == 12 * B * Cout * P * H * W
+    xd, wd, ad, gd = x.to(dev), w.to(dev), alpha.to(dev), g.to(dev)
+    stats = torch.full((nbytes // 4,), float("nan"), device=dev)
+    out0 = torch.empty((B, Cout, H, W), device=dev)
+    out1 = torch.empty_like(out0)
+    native.smorph_forward(m, xd, wd, ad, out0, geom)
+    native.smorph_forward(m, xd, wd, ad, out1, geom, stats=stats)
+    out = _np(out1)
+    assert np.array_equal(_np(out0), out)
+    ref, inv, outp = (a.reshape(B, Cout, P, H, W) for a in _np(stats).reshape(3, -1))
+    assert np.isfinite(ref).all() and np.isfinite(inv).all() and np.isfinite(outp).all()
+    # ref: per pair, the extremum its alpha's sign selects.
+    a_np = alpha.numpy().reshape(Cout, P)
+    w_np = w.numpy()
+    if merge == "identity":
+        ext_d = np.stack([_window_extremum(x.numpy()[:, c:c + 1], w_np[c:c + 1], True)[:, 0, 0] for c in range(Cin)], axis=1)[:, :, None]
+        ext_e = np.stack([_window_extremum(x.numpy()[:, c:c + 1], w_np[c:c + 1], False)[:, 0, 0] for c in range(Cin)], axis=1)[:, :, None]
+    else:
+        ext_d, ext_e = _window_extremum(x.numpy(), w_np, True), _window_extremum(x.numpy(), w_np, False)
+    want = np.where((a_np >= 0)[None, :, :, None, None], ext_d, ext_e)
+    assert np.array_equal(ref, want)
+    if merge == "max":
+        assert np.array_equal(outp.max(axis=2), out)
+    elif merge == "min":
+        assert np.array_equal(outp.min(axis=2), out)
+    elif merge == "identity":
+        assert np.array_equal(outp[:, :, 0], out)
+    else:
+        total = outp.astype(np.float64).sum(axis=2) / (Cin if merge == "mean" else 1)
+        assert normwise_error(out, total) <= 1e-6
+    # Backward from the statistics, against the oracle and against the recomputing backward.
+    rgx, rgw, rga = O.smorph_backward(m, x.numpy(), w_np, alpha.numpy(), g.numpy())
+    grads = []
+    for st in (stats, None):
+        gx, gw, ga = torch.empty_like(xd), torch.empty_like(wd), torch.empty_like(ad)
+        native.smorph_backward(m, xd, wd, ad, out1, gd, gx, gw, ga, geom, stats=st)
+        grads.append((_np(gx), _np(gw), _np(ga)))
+    for got in grads:
+        for actual, expected in zip(got, (rgx, rgw, rga)):
+            assert normwise_error(actual, expected) <= 1e-6
+    for a1, a0 in zip(*grads):
+        assert normwise_error(a1, a0) <= 1e-6
 
 
 @pytest.mark.parametrize("merge", ["sum", "max"])

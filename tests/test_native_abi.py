@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 15
+    assert len(symbols) == 18
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -93,3 +93,25 @@ def test_workspace_sizes_and_rejection():
     assert rc == 1 and "Workspace too small" in lib.mca_last_error().decode()
     rc = lib.mca_smorph_backward_f32(2, None, None, None, None, None, None, None, None, *GEOM, None, 16, None)
     assert rc == 1 and "Workspace too small" in lib.mca_last_error().decode()
+
+
+def test_smorph_stats_bytes_and_rejection():
+    """The saved-statistics entry points: three float32 values per channel pair and output pixel for
+    the static sizes, none otherwise; a configuration without them, or a null buffer, is an argument
+    error before any device work."""
+    lib = _native.lib()
+    B, Cin, Cout, Cw, H, W = 2, 3, 4, 3, 16, 16
+    for k in (3, 5, 7, 11):
+        assert lib.mca_smorph_stats_bytes_f32(2, B, Cin, Cout, Cw, H, W, k, k) == 12 * B * Cout * Cin * H * W
+    assert lib.mca_smorph_stats_bytes_f32(5, 2, 3, 3, 1, H, W, 7, 7) == 12 * 2 * 3 * H * W  # IDENTITY: one pair per output
+    assert lib.mca_smorph_stats_bytes_f32(2, B, Cin, Cout, Cw, H, W, 4, 4) == 0
+    assert lib.mca_smorph_stats_bytes_f32(2, B, Cin, Cout, Cw, H, W, 3, 5) == 0
+    assert lib.mca_smorph_stats_bytes_f32(9, B, Cin, Cout, Cw, H, W, 3, 3) == 0
+    rc = lib.mca_smorph_forward_stats_f32(2, None, None, None, None, None, B, Cin, Cout, Cw, H, W, 4, 4, None)
+    assert rc == 1 and "No saved smorph statistics" in lib.mca_last_error().decode()
+    rc = lib.mca_smorph_forward_stats_f32(2, None, None, None, None, None, B, Cin, Cout, Cw, H, W, 3, 3, None)
+    assert rc == 1 and "stats must not be null" in lib.mca_last_error().decode()
+    rc = lib.mca_smorph_backward_stats_f32(2, None, None, None, None, None, None, None, None, None, B, Cin, Cout, Cw, H, W, 3, 3,
+                                           None, 0, None)
+    assert rc == 1 and "stats must not be null" in lib.mca_last_error().decode()
+    assert _native.smorph_stats_bytes(2, __import__("torch").float64, (B, Cin, Cout, Cw, H, W, 3, 3)) == 0
