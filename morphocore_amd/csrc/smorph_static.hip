@@ -375,11 +375,19 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         // the (complete) total of the right halo column 63 + KW - kw; lane KW - 1 - kw keeps it.
         float racc = 0.0f, halo = 0.0f;
         __builtin_amdgcn_sched_barrier(0);
+        // x and w of the next tap are read from LDS one tap ahead, so that the read's latency
+        // overlaps this tap's arithmetic (each tap is one long dependent chain).
+        float xn = xb[-(kh * COLS)], wn = wl[kh * KW];
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
             const int k = kh * KW + kw;
-            const float vk = xb[-(kh * COLS + kw)] + wl[k];
+            const float vk = xn + wn;
+            if (kw + 1 < KW)
+            {
+                xn = xb[-(kh * COLS + kw + 1)];
+                wn = wl[k + 1];
+            }
             float ekr;
             if (k >= KE)
             {
