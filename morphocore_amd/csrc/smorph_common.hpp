@@ -107,25 +107,44 @@ struct SmorphFwdParams
     int average;
 };
 
+// Half of exp(r)'s Taylor polynomial: Horner with every coefficient halved (exact), so each step is
+// exactly half of horner<T, K>'s (scaling by a power of two commutes with rounding).
+template <typename T, int K>
+__device__ __forceinline__ T horner_half(T r)
+{
+    if constexpr (K == ExpConsts<T>::degree)
+        return InvFact<T, K>::value * T(0.5);
+    else
+        return fma(horner_half<T, K + 1>(r), r, InvFact<T, K>::value * T(0.5));
+}
+
 // The same exponential for the arguments the smorph kernels pass, alpha (v - ref) with ref the
-// extremum of the window: never positive, or NaN. Bit for bit equal to exp_t on (-inf, max_input];
-// a NaN argument gives NaN, as in the reference (whose range checks let NaN through), and the upper
-// clamp is dropped since no argument reaches it. `lo` is the lower clamp, min_input (a caller may
-// hold it in a register, which makes the comparison a register-only one).
+// extremum of the window: never positive, or NaN. Bit for bit equal to exp_t on (-inf, max_input]
+// (checked exhaustively for float32 on [-200, 0], NaN and -inf); a NaN argument gives NaN, as in the
+// reference (whose range checks let NaN through), and the upper clamp is dropped since no argument
+// reaches it. `lo` is the lower clamp, min_input (a caller may hold it in a register, which makes the
+// comparison a register-only one). Arranged for fewer instructions than exp_t:
+//  * below `lo` the result is selected to 0 at the end, so the argument needs no clamp (what the
+//    reduction computes there is discarded);
+//  * the rounding constant carries bias + 1 (even, and in the same binade, so every rounding is
+//    unchanged): the low bits of nm hold n + bias + 1, and shifting them into the exponent field is
+//    2^(n + 1) with no add; the halved polynomial compensates, and (p / 2) 2^(n + 1) is the same
+//    exact product as p 2^n, rounded once. n + bias + 1 stays in [2, bias + 1] for n in
+//    [log2(min normal), 0].
 template <typename T>
 __device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
 {
     using C = ExpConsts<T>;
     using Bits = typename C::Bits;
+    constexpr T magic = C::magic + T(C::bias + 1);
     const bool under = x < lo;
-    const T xc = under ? lo : x;
-    const T nm = fma(xc, C::log2e, C::magic);
-    const T n = nm - C::magic;
-    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));
-    const T p = horner<T, 0>(r);
-    const Bits bits = (Bits)(((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant) + ((uint64_t)C::bias << C::mant));
-    const T scale = under ? T(0) : __builtin_bit_cast(T, bits);
-    return p * scale;
+    const T nm = fma(x, C::log2e, magic);
+    const T n = nm - magic;
+    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, x));
+    const T ph = horner_half<T, 0>(r);
+    const T scale = __builtin_bit_cast(T, (Bits)((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant));
+    const T e = ph * scale;
+    return under ? T(0) : e;
 }
 
 template <typename T>
