@@ -375,18 +375,26 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         // the (complete) total of the right halo column 63 + KW - kw; lane KW - 1 - kw keeps it.
         float racc = 0.0f, halo = 0.0f;
         __builtin_amdgcn_sched_barrier(0);
-        // x and w of the next tap are read from LDS one tap ahead, so that the read's latency
-        // overlaps this tap's arithmetic (each tap is one long dependent chain).
-        float xn = xb[-(kh * COLS)], wn = wl[kh * KW];
+        // x and w read from LDS ahead of their use, so that the reads' latency overlaps arithmetic
+        // (each tap is one long dependent chain): with SAVED the whole row at once (paired reads),
+        // else one tap ahead (fewer registers, which the recomputing kernels lack).
+        constexpr int XR = SAVED ? KW : 1;
+        float xr[XR], wr[XR];
+#pragma unroll
+        for (int kw = 0; kw < XR; ++kw)
+        {
+            xr[kw] = xb[-(kh * COLS + kw)];
+            wr[kw] = wl[kh * KW + kw];
+        }
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
             const int k = kh * KW + kw;
-            const float vk = xn + wn;
-            if (kw + 1 < KW)
+            const float vk = SAVED ? xr[kw < XR ? kw : 0] + wr[kw < XR ? kw : 0] : xr[0] + wr[0];
+            if (!SAVED && kw + 1 < KW)
             {
-                xn = xb[-(kh * COLS + kw + 1)];
-                wn = wl[k + 1];
+                xr[0] = xb[-(kh * COLS + kw + 1)];
+                wr[0] = wl[k + 1];
             }
             float ekr;
             if (k >= KE)
