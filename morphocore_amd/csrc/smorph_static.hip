@@ -37,12 +37,15 @@ __device__ __forceinline__ float smorph_init(bool dilation_like)
 }
 
 // Validity of this wave's tap rows (bit kh: the input row lies in the image, uniform over the wave)
-// and of this lane's tap columns.
+// and of this lane's tap columns, as a penalty: 0 in the image, +inf outside. Masking by arithmetic
+// (v - pen never wins a max, an exponential's argument minus pen gives e = 0) keeps the masked taps
+// branch free: a select between a loaded value and a constant is turned into a branch around the
+// load by the compiler.
 template <int KH, int KW>
 struct TapMask
 {
     unsigned rows;
-    bool col[KW];
+    float pen[KW];
 
     __device__ __forceinline__ void init(const Geom& g, int h, int wc)
     {
@@ -58,7 +61,7 @@ struct TapMask
         for (int kw = 0; kw < KW; ++kw)
         {
             const int c = wc + KW / 2 - kw;
-            col[kw] = c >= 0 && c < g.W;
+            pen[kw] = c >= 0 && c < g.W ? 0.0f : std::numeric_limits<float>::infinity();
         }
     }
     __device__ __forceinline__ bool row(int kh) const { return (rows >> kh) & 1u; }
@@ -81,7 +84,7 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
             for (int kw = 0; kw < KW; ++kw)
             {
                 float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
-                if constexpr (MASKED) v = tm.col[kw] ? v : -std::numeric_limits<float>::infinity();
+                if constexpr (MASKED) v = v - tm.pen[kw];  // -inf (or NaN) outside: never wins
                 ref = fmaxf(ref, v);
             }
         }
@@ -96,7 +99,7 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
             for (int kw = 0; kw < KW; ++kw)
             {
                 float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
-                if constexpr (MASKED) v = tm.col[kw] ? v : std::numeric_limits<float>::infinity();
+                if constexpr (MASKED) v = v + tm.pen[kw];
                 ref = fminf(ref, v);
             }
         }
@@ -128,10 +131,10 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
         for (int kw = 0; kw < KW; ++kw)
         {
             const float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
-            float e = exp_ref((v - ref) * a, lo);
-            // An out-of-image tap adds e = 0 (its staged x is 0, so v is finite): S + 0 and
-            // fma(0, v, W) leave both sums exactly as skipping it does.
-            if constexpr (MASKED) e = tm.col[kw] ? e : 0.0f;
+            // An out-of-image tap adds e = 0 (its staged x is 0, so v and the argument are finite, and
+            // the argument less +inf is -inf): S + 0 and fma(0, v, W) leave both sums exactly as
+            // skipping it does.
+            const float e = exp_ref(MASKED ? (v - ref) * a - tm.pen[kw] : (v - ref) * a, lo);
             s = s + e;  // unfused, as in the reference (e is rounded before the sum)
             wsum = fmaf(e, v, wsum);
         }
@@ -142,8 +145,12 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
 
 // SAVE: also store each pair's ref, 1 / S and W / S at every in-image pixel (p.pstats), which the
 // backward then reads instead of recomputing them.
+// Waves per SIMD requested: eight up to 7x7, five at 11x11 (the occupancy the register-held element
+// and window allow; without the request the compiler takes more registers for fewer waves, measured
+// ~2% slower).
 template <int MK, int KH, int KW, bool STATS, bool SAVE>
-__global__ __launch_bounds__(BLOCK) void smorph_fwd_static(const SmorphFwdParams<float> p)
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 8, 8))) void smorph_fwd_static(
+    const SmorphFwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, ELEMS = ROWS * COLS;
@@ -314,9 +321,10 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
-    // A lane outside the image with saved statistics holds another pixel's ref, so its e may be
-    // infinite: its c is cleared like a MAX / MIN loser's.
-    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || (SAVED && MASKED);
+    // A lane outside the image may meet a non-finite e (with saved statistics it holds another
+    // pixel's ref; recomputing, a window with no tap in the image has an infinite ref): its c is
+    // cleared like a MAX / MIN loser's.
+    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || MASKED;
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     // Taps whose e stays in registers between the passes: all up to 7x7; for 11x11 the first two
@@ -340,9 +348,8 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             {
                 const int k = kh * KW + kw;
                 const float vk = xb[-(kh * COLS + kw)] + wl[k];
-                float ek = exp_ref((vk - ref) * a, lo);
                 // Out-of-image taps: e = 0 leaves S and W as skipping them does, and routes c = 0.
-                if constexpr (MASKED) ek = tm.col[kw] ? ek : 0.0f;
+                const float ek = exp_ref(MASKED ? (vk - ref) * a - tm.pen[kw] : (vk - ref) * a, lo);
                 s = s + ek;  // unfused, as in the reference
                 wsum = fmaf(ek, vk, wsum);
                 if (k < KE) e[k] = ek;  // a constant condition once unrolled
@@ -399,8 +406,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             float ekr;
             if (k >= KE)
             {
-                ekr = exp_ref((vk - ref) * a, lo);
-                if constexpr (MASKED) ekr = tm.col[kw] ? ekr : 0.0f;
+                ekr = exp_ref(MASKED ? (vk - ref) * a - tm.pen[kw] : (vk - ref) * a, lo);
             }
             else
             {
