@@ -309,13 +309,16 @@ struct SmorphBwdPlan
     size_t lds;
 };
 
+// `saved`: the backward from saved statistics, whose static kernel takes two output rows per wave
+// (fewer tiles, so no more slots than the one-row plan, which sizes the workspace).
 template <typename T>
-static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g)
+static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = false)
 {
     SmorphBwdPlan s{};
-    // The static kernels (smorph_static.hip) use one output row per wave and static LDS.
+    // The static kernels (smorph_static.hip) use one output row per wave (two from saved statistics)
+    // and static LDS.
     const bool stat = smorph_static_supported<T>(g);
-    s.t = make_tiling(g, stat ? 1 : rows_per_wave<T>());
+    s.t = make_tiling(g, stat ? (saved ? 2 : 1) : rows_per_wave<T>());
     s.ncopy = 16;
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
     const int64_t units = (int64_t)g.B * g.Cin;
@@ -405,7 +408,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     if (workspace_bytes < smorph_backward_workspace<T>(merge, g)) return hipErrorInvalidValue;
     if (stats && smorph_stats_count<T>(merge, g) == 0) return hipErrorInvalidValue;
     const int64_t nstat = smorph_stats_count<T>(merge, g);
-    const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g);
+    const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g, stats != nullptr);
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
     if ((int64_t)g.B * g.Cout * g.plane() == 0)

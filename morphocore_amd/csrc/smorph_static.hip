@@ -622,6 +622,291 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bw
 }
 
 // ------------------------------------------------------------------------------------------------
+// Backward from saved statistics, two output rows per wave: pixels A (row h) and B (row h + 1) of a
+// lane's column. Tile row j = 0 .. KH of the wave's staged input holds tap row KH - 1 - j of A and tap
+// row KH - j of B, so
+//  * both pixels' taps of a tile row share its x reads, and their c values are added before the
+//    row's DPP Horner sum and its LDS add (KH + 1 row sums for the two pixels instead of 2 KH);
+//  * a tap's bin receives A's value (kept for one tile row) plus B's in one f64 LDS add.
+// ------------------------------------------------------------------------------------------------
+
+// One pixel's routing state for a pair: its saved ref, g' / S (0 when it routes nothing) and the
+// centre W / S (0 likewise).
+struct RoutePixel
+{
+    float ref, scaled, outc;
+    bool route;
+};
+
+template <int MK, int KH, int KW, bool MASKED>
+__device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* wl, float a, const RoutePixel& A, const RoutePixel& B,
+                                                  unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, int lane)
+{
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
+    constexpr int K = KH * KW, COLS = TILE_W + KW - 1, NC = smorph_bin_copies(K);
+    // MAX / MIN losers, and lanes outside the image (another pixel's ref, so e may be infinite):
+    // c cleared.
+    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || MASKED;
+    float lo = ExpConsts<float>::min_input;
+    asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
+    float asumA = 0.0f, asumB = 0.0f;
+    float abuf[KW];  // A's c of the previous tile row's taps, added to B's in the same taps' bins
+    auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
+        const float vk = x + wl[k];
+        const float ek = exp_ref(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
+        const float pg = ek * P.scaled;
+        const float centered = vk - P.outc;
+        float c = fmaf(a * pg, centered, pg);
+        if constexpr (GATE) c = P.route ? c : 0.0f;
+        asum = fmaf(pg * (vk - P.ref), centered, asum);
+        // Keeps the compiler from deferring the alpha terms, which would hold every tap's factors
+        // in registers.
+        asm volatile("" : "+v"(asum));
+        return c;
+    };
+#pragma unroll
+    for (int j = 0; j <= KH; ++j)
+    {
+        const bool rv = !MASKED || ((rows >> j) & 1u);  // the tile row lies in the image (uniform)
+        const int khA = j < KH ? KH - 1 - j : 0, khB = j > 0 ? KH - j : 0;
+        float xr[KW];
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw) xr[kw] = xw[j * COLS - kw];
+        float racc = 0.0f, halo = 0.0f;
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            float cA = 0.0f, cB = 0.0f;
+            if (rv)
+            {
+                if (j < KH) cA = route_tap(A, xr[kw], khA * KW + kw, kw, asumA);
+                if (j > 0) cB = route_tap(B, xr[kw], khB * KW + kw, kw, asumB);
+                const float cs = j == 0 ? cA : (j == KH ? cB : cA + cB);
+                // Row sums per tile column across the wave (DPP wave_shr Horner over kw); what leaves
+                // lane 63 at step kw is the right halo column 63 + KW - kw: lane KW - 1 - kw keeps it.
+                if (kw == 0)
+                {
+                    racc = cs;
+                }
+                else
+                {
+                    const int fell = __builtin_amdgcn_readlane(__float_as_int(racc), WAVE - 1);
+                    asm("v_writelane_b32 %0, %1, %2" : "+v"(halo) : "s"(fell), "i"(KW - 1 - kw));
+                    racc = wave_shift_up(racc) + cs;
+                }
+            }
+            if (j > 0) lds_add(&bl[(khB * KW + kw) * NC], (Acc)(cB + abuf[kw]));
+            if (j < KH) abuf[kw] = cA;
+        }
+        if (rv)
+        {
+            Acc* grow = gw + j * COLS;  // tile row 2 wave + j, column `lane`
+            lds_add(grow, (Acc)racc);
+            if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
+        }
+    }
+    return (A.route ? asumA : 0.0f) + (B.route ? asumB : 0.0f);
+}
+
+template <int MK, int KH, int KW>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : (KH * KW > 25 ? 6 : 7), 8))) void
+smorph_bwd_saved2(const SmorphBwdParams<float> p)
+{
+    constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
+    constexpr int RH = 2, TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
+    constexpr int NC = smorph_bin_copies(K);
+    __shared__ float tile[ROWS * COLS];
+    __shared__ Acc gtile[ROWS * COLS];
+    __shared__ __align__(32) Acc bins[(K + 1) * NC];  // grad_weight bins of the K taps, then grad_alpha; NC copies each
+    __shared__ __align__(16) float wl[2][(K + 4) & ~3];
+    const Geom g = p.g;
+    const Tiling t = p.t;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    int work = xcd_work_index(blockIdx.x, gridDim.x);
+    const int i = work % g.Cin;  // input channel fastest: an XCD's workgroups share the strip's g in L2
+    work /= g.Cin;
+    const int strip = work % p.nstrips;
+    const int b = work / p.nstrips;
+    const int64_t plane = g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * K;
+    const int slot = b * p.nstrips + strip;
+    float* __restrict__ part_w = p.part_w + (int64_t)slot * wnumel;
+    float* __restrict__ part_a = p.part_a + (int64_t)slot * p.npairs;
+    const int wi = MK == MK_IDENT ? 0 : i;
+    const int o_begin = MK == MK_IDENT ? i : 0;
+    const int o_end = MK == MK_IDENT ? i + 1 : g.Cout;
+    const int cpair = MK == MK_IDENT ? 1 : g.Cin;
+    const float* __restrict__ xp = p.x + ((int64_t)b * g.Cin + i) * plane;
+    float* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + i) * plane;
+    auto pair_index = [&](int o) { return MK == MK_IDENT ? o : o * g.Cin + i; };
+    auto stage_weights = [&](int o, int buf) {
+        if (threadIdx.x < K)
+            wl[buf][threadIdx.x] = p.w[((int64_t)o * g.Cw + wi) * K + threadIdx.x];
+        else if (threadIdx.x == K)
+            wl[buf][K] = p.alpha[pair_index(o)];
+    };
+    constexpr int NPART = K <= 25 ? SMORPH_LDS_PARTIALS : 1;
+    __shared__ float partials[NPART];
+    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
+    for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
+    for (int j = threadIdx.x; j < (K + 1) * NC; j += BLOCK) bins[j] = Acc(0);
+    const int tile_begin = strip * p.tps;
+    const int tile_end = min(tile_begin + p.tps, t.ntiles());
+    const float* xw = tile + RH * wave * COLS + lane + KW - 1;  // tile row 2 wave, this lane's tap-0 column
+    Acc* gw = gtile + RH * wave * COLS + lane;
+    Acc* bl = bins + (lane & (NC - 1));
+    for (int tid = tile_begin; tid < tile_end; ++tid)
+    {
+        const int ty = tid / t.ntx, tx = tid - ty * t.ntx;
+        const int h0 = ty * TH, w0 = tx * TILE_W;
+        const int y0 = h0 + PH - (KH - 1), x0 = w0 + PW - (KW - 1);
+        const int hA = h0 + RH * wave, wc = w0 + lane;
+        const bool inA = hA < g.H && wc < g.W, inB = hA + 1 < g.H && wc < g.W;
+        const bool interior = y0 >= 0 && y0 + ROWS <= g.H && x0 >= 0 && x0 + COLS <= g.W;
+        unsigned rows = 0;
+#pragma unroll
+        for (int j = 0; j <= KH; ++j)
+        {
+            const int y = y0 + RH * wave + j;
+            rows |= (y >= 0 && y < g.H) ? 1u << j : 0u;
+        }
+        rows = __builtin_amdgcn_readfirstlane(rows);
+        float pen[KW];
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+        {
+            const int c = wc + PW - kw;
+            pen[kw] = c >= 0 && c < g.W ? 0.0f : std::numeric_limits<float>::infinity();
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+        {
+            const int ly = idx / COLS, lx = idx - ly * COLS;
+            const int y = y0 + ly, x = x0 + lx;
+            tile[idx] = (y >= 0 && y < g.H && x >= 0 && x < g.W) ? xp[(int64_t)y * g.W + x] : 0.0f;
+            gtile[idx] = Acc(0);
+        }
+        stage_weights(o_begin, 0);
+        // Output gradient, saved statistics (and for MAX / MIN the merged output and winner count)
+        // of both pixels, one output channel ahead.
+        const int64_t pixA = (int64_t)min(hA, g.H - 1) * g.W + min(wc, g.W - 1);
+        const int64_t pixB = (int64_t)min(hA + 1, g.H - 1) * g.W + min(wc, g.W - 1);
+        float gA_n = 0.0f, gB_n = 0.0f, cA_n = 0.0f, cB_n = 0.0f, oA_n = 0.0f, oB_n = 0.0f;
+        PairStats sA_n{0.0f, 0.0f, 0.0f}, sB_n{0.0f, 0.0f, 0.0f};
+        auto load_g = [&](int o) {
+            o = min(o, o_end - 1);
+            const int64_t ob = ((int64_t)b * g.Cout + o) * plane;
+            gA_n = p.gout[ob + pixA];
+            gB_n = p.gout[ob + pixB];
+            if constexpr (MK == MK_MAX || MK == MK_MIN)
+            {
+                cA_n = p.counts[ob + pixA];
+                cB_n = p.counts[ob + pixB];
+                oA_n = p.out[ob + pixA];
+                oB_n = p.out[ob + pixB];
+            }
+            const float* q = p.pstats + (((int64_t)b * g.Cout + o) * cpair + (MK == MK_IDENT ? 0 : i)) * plane;
+            sA_n.ref = __builtin_nontemporal_load(q + pixA);
+            sA_n.inv = __builtin_nontemporal_load(q + p.nstat + pixA);
+            sA_n.outp = __builtin_nontemporal_load(q + 2 * p.nstat + pixA);
+            sB_n.ref = __builtin_nontemporal_load(q + pixB);
+            sB_n.inv = __builtin_nontemporal_load(q + p.nstat + pixB);
+            sB_n.outp = __builtin_nontemporal_load(q + 2 * p.nstat + pixB);
+        };
+        auto route_pixel = [&](bool in, float gv, float cnt, float outv, const PairStats& st) {
+            RoutePixel r;
+            gv = in ? gv * p.scale : 0.0f;
+            bool route = in;
+            if constexpr (MK == MK_MAX || MK == MK_MIN)
+            {
+                gv = gv / (cnt > 0.0f ? cnt : 1.0f);
+                route = route && is_winner(st.outp, outv);
+            }
+            r.ref = st.ref;
+            r.scaled = route ? gv * st.inv : 0.0f;
+            r.outc = route ? st.outp : 0.0f;
+            r.route = route;
+            return r;
+        };
+        load_g(o_begin);
+        __syncthreads();
+        for (int o = o_begin; o < o_end; ++o)
+        {
+            const int buf = (o - o_begin) & 1;
+            const RoutePixel A = route_pixel(inA, gA_n, cA_n, oA_n, sA_n);
+            const RoutePixel B = route_pixel(inB, gB_n, cB_n, oB_n, sB_n);
+            load_g(o + 1);
+            const float* w = wl[buf];
+            const float a = w[K];
+            float asum;
+            if (interior)
+                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, lane);
+            else
+                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, lane);
+            lds_add(&bl[K * NC], (Acc)asum);
+            if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
+            __syncthreads();
+            // Sum the NC copies of each bin (8 threads per bin, NC / 8 adjacent copies each, a butterfly
+            // over the 8) into this workgroup's slot, as the one-row kernel does.
+            constexpr int PER = NC / 8;
+            for (int j = threadIdx.x; j < (K + 1) * 8; j += BLOCK)
+            {
+                Acc v;
+                if constexpr (PER == 4)
+                {
+                    double4* q = reinterpret_cast<double4*>(&bins[j * 4]);
+                    const double4 c4 = *q;
+                    *q = make_double4(0.0, 0.0, 0.0, 0.0);
+                    v = (c4.x + c4.y) + (c4.z + c4.w);
+                }
+                else
+                {
+                    double2* q = reinterpret_cast<double2*>(&bins[j * 2]);
+                    const double2 c2 = *q;
+                    *q = make_double2(0.0, 0.0);
+                    v = c2.x + c2.y;
+                }
+#pragma unroll
+                for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
+                if ((j & 7) == 0)
+                {
+                    const int k = j >> 3;
+                    if (lds_partials)
+                        partials[(o - o_begin) * (K + 1) + k] += (float)v;
+                    else if (k < K)
+                        global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
+                    else
+                        global_add(&part_a[pair_index(o)], (float)v);
+                }
+            }
+            __syncthreads();
+        }
+        for (int idx = threadIdx.x; idx < ROWS * COLS; idx += BLOCK)
+        {
+            const int ly = idx / COLS, lx = idx - ly * COLS;
+            const int y = y0 + ly, x = x0 + lx;
+            if (y < 0 || y >= g.H || x < 0 || x >= g.W) continue;
+            const float v = (float)gtile[idx];
+            if (v != 0.0f) global_add(&gplane[(int64_t)y * g.W + x], v);
+        }
+    }
+    if (lds_partials)
+    {
+        __syncthreads();
+        const int n = (o_end - o_begin) * (K + 1);
+        for (int j = threadIdx.x; j < n; j += BLOCK)
+        {
+            const int ol = j / (K + 1), k = j - ol * (K + 1), o = o_begin + ol;
+            if (k < K)
+                part_w[((int64_t)o * g.Cw + wi) * K + k] = partials[j];
+            else
+                part_a[pair_index(o)] = partials[j];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Launch
 // ------------------------------------------------------------------------------------------------
 
@@ -691,8 +976,33 @@ static hipError_t bwd_dispatch(int mk, const SmorphBwdParams<float>& p, hipStrea
     }
 }
 
+template <int KS>
+static hipError_t bwd2_size(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
+{
+    const unsigned blocks = (unsigned)((int64_t)p.g.B * p.g.Cin * p.nstrips);
+    switch (mk)
+    {
+        case MK_SUM: smorph_bwd_saved2<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_bwd_saved2<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_bwd_saved2<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_bwd_saved2<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
+    if (p.pstats && p.t.rh == 2)
+    {
+        switch (p.g.KH)
+        {
+            case 3: return bwd2_size<3>(mk, p, stream);
+            case 5: return bwd2_size<5>(mk, p, stream);
+            case 7: return bwd2_size<7>(mk, p, stream);
+            default: return bwd2_size<11>(mk, p, stream);
+        }
+    }
+    if (p.t.rh != 1) return hipErrorInvalidValue;
     return p.pstats ? bwd_dispatch<true>(mk, p, stream) : bwd_dispatch<false>(mk, p, stream);
 }
 
