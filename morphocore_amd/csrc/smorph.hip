@@ -127,6 +127,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
             const T inv = T(1) / S[r];
             if constexpr (STATS)
             {
+                if (i == i_begin) tgt[r] = smorph_merge_target(tgt[r], Wsum[r] * inv);
                 if (is_winner(Wsum[r] * inv, tgt[r])) m[r] = m[r] + T(1);
             }
             else if constexpr (MK == MK_MAX)
@@ -161,6 +162,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
             if (p.average) v = v / (T)g.Cin;
         }
         p.out[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = v;
+        if constexpr (STATS) p.tout[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = tgt[r];
     }
 }
 
@@ -333,7 +335,8 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     const size_t nslots = (size_t)g.B * s.nstrips;
     s.part_w_bytes = nslots * wnumel * sizeof(T);
     s.part_a_bytes = nslots * s.npairs * sizeof(T);
-    s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
+    // MAX / MIN: winner counts, then the merge target, per output pixel.
+    s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? 2 * (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
     s.lds = stat ? 0
                  : align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + ((size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(Acc);
     return s;
@@ -420,6 +423,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     T* part_w = reinterpret_cast<T*>(ws);
     T* part_a = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes));
     T* counts = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
+    T* target = counts + (int64_t)g.B * g.Cout * g.plane();
     T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes));
     const int nslots = g.B * s.nstrips;
     // The static kernels that keep their partials in LDS store every slot entry themselves.
@@ -432,7 +436,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     if (stats && (merge == MERGE_MAX || merge == MERGE_MIN))
     {
         if constexpr (sizeof(T) == 4)
-            if ((err = launch_smorph_counts_saved(stats + 2 * nstat, out, counts, g, stream)) != hipSuccess) return err;
+            if ((err = launch_smorph_counts_saved(stats + 2 * nstat, out, counts, target, g, stream)) != hipSuccess) return err;
     }
     else if (merge == MERGE_MAX || merge == MERGE_MIN)
     {
@@ -441,6 +445,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
         f.w = w;
         f.alpha = alpha;
         f.out = counts;
+        f.tout = target;
         f.target = out;
         f.g = g;
         f.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
@@ -453,7 +458,9 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     p.x = x;
     p.w = w;
     p.alpha = alpha;
-    p.out = out;
+    // MAX / MIN compare the pair outputs with the merge target (the forward's output unless channel
+    // 0's pair output is NaN).
+    p.out = (merge == MERGE_MAX || merge == MERGE_MIN) ? target : out;
     p.counts = counts;
     p.gout = grad_out;
     p.gin = grad_in;

@@ -80,6 +80,16 @@ __device__ __forceinline__ T exp_t(T x)
     return p * scale;
 }
 
+// The target the reference's MAX / MIN backward compares the pair outputs with: the extremum over the
+// channels starting from channel 0's pair output (smorph_cpu_kernels.hxx:491-503), which is the
+// forward's output (merged from lowest() / max(), where NaN never wins) unless channel 0's output is
+// NaN: then NaN, and no pair is a winner.
+template <typename T>
+__device__ __forceinline__ T smorph_merge_target(T forward_out, T channel0_out)
+{
+    return channel0_out != channel0_out ? channel0_out : forward_out;
+}
+
 // Tolerance within which a channel counts as a MAX / MIN winner (reference: smorph.cu:7-9,
 // smorph_cpu_kernels.hxx:622-627).
 template <typename T>
@@ -98,6 +108,7 @@ struct SmorphFwdParams
     const T* __restrict__ alpha;
     T* __restrict__ out;           // forward output, or the winner counts in STATS mode
     const T* __restrict__ target;  // STATS mode: the forward output
+    T* __restrict__ tout;          // STATS mode: the backward's merge target (see smorph_merge_target)
     // Saved pair statistics (float32 static kernels; null: none saved): ref, then 1 / S, then W / S of
     // every (batch element, output channel, pair, pixel), `nstat` values each.
     float* __restrict__ pstats;
@@ -207,7 +218,7 @@ inline int64_t smorph_stats_count(int merge, const Geom& g)
 // forward that saves the pair statistics and the backward that reads them.
 hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<float>& p, hipStream_t stream);
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream);
-// MAX / MIN winner counts of every output pixel from the saved W / S values (`outp`).
-hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, const Geom& g, hipStream_t stream);
+// MAX / MIN merge target and winner counts of every output pixel from the saved W / S values (`outp`).
+hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, float* target, const Geom& g, hipStream_t stream);
 
 }  // namespace mca

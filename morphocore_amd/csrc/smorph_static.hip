@@ -244,6 +244,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
             smorph_sums<KH, KW, true>(xb, w, a, ref, tm, S, Wsum);
         }
         const float inv = 1.0f / S;
+        if constexpr (STATS)
+        {
+            if (i == i_begin) tgt = smorph_merge_target(tgt, Wsum * inv);
+        }
         if constexpr (SAVE)
         {
             // Streamed out (read back by the backward, long after this kernel): non-temporal stores.
@@ -289,6 +293,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         if (p.average) v = v / (float)g.Cin;
     }
     p.out[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = v;
+    if constexpr (STATS) p.tout[((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc] = tgt;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -313,8 +318,8 @@ struct PairStats
 // tap's e kept up to 7x7), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input
 // (the LDS tile), to the grad_weight bin of tap k and to grad_alpha (returned: the sum of
 // p_k (v_k - ref)(v_k - out) over the taps). gv is g * scale (0 outside the image); for MAX / MIN it
-// is divided by the pixel's winner count, and only a pair within 1e-6 of the merged output outv
-// routes. SAVED: `st` holds the forward's statistics and each e is evaluated once, in the routing.
+// is divided by the pixel's winner count, and a pair not within 1e-6 of the merge target outv routes
+// with g' = 0. SAVED: `st` holds the forward's statistics and each e is evaluated once, in the routing.
 template <int MK, int KH, int KW, bool MASKED, bool SAVED>
 __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
                                                  PairStats st, const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
@@ -323,8 +328,8 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
     // A lane outside the image may meet a non-finite e (with saved statistics it holds another
     // pixel's ref; recomputing, a window with no tap in the image has an infinite ref): its c is
-    // cleared like a MAX / MIN loser's.
-    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || MASKED;
+    // cleared.
+    constexpr bool GATE = MASKED;
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     // Taps whose e stays in registers between the passes: all up to 7x7; for 11x11 the first two
@@ -361,16 +366,17 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         st.outp = wsum * st.inv;
     }
     const float ref = st.ref;
-    bool route = in;
     if constexpr (MK == MK_MAX || MK == MK_MIN)
     {
+        // As the reference (smorph_cpu_kernels.hxx:507-545): a pair that is not a winner routes with
+        // g' = 0, so its c are 0, or NaN where its own values are not finite.
         gv = gv / (cnt > 0.0f ? cnt : 1.0f);
-        route = route && is_winner(st.outp, outv);
+        gv = is_winner(st.outp, outv) ? gv : 0.0f;
     }
-    // A lane that routes nothing (outside the image, where S may be 0 and out NaN, or a MAX / MIN
-    // loser) gets g' = 0 and a finite centre, so every c it adds to the row sums is 0.
-    const float scaled = route ? gv * st.inv : 0.0f;
-    const float outc = route ? st.outp : 0.0f;
+    // A lane outside the image (where S may be 0 and out NaN) gets g' = 0 and a finite centre, and
+    // its c are cleared.
+    const float scaled = in ? gv * st.inv : 0.0f;
+    const float outc = in ? st.outp : 0.0f;
     float asum = 0.0f;
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh)
@@ -415,7 +421,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             const float pg = ekr * scaled;
             const float centered = vk - outc;
             float c = fmaf(a * pg, centered, pg);
-            if constexpr (GATE) c = route ? c : 0.0f;
+            if constexpr (GATE) c = in ? c : 0.0f;
             if (kw == 0)
             {
                 racc = c;
@@ -436,7 +442,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         lds_add(grow, (Acc)racc);
         if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
     }
-    return route ? asum : 0.0f;
+    return in ? asum : 0.0f;
 }
 
 // Waves per SIMD requested (measured on MI355X), recomputing: up to 7x7 six (80 registers, a few
@@ -630,12 +636,12 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bw
 //  * a tap's bin receives A's value (kept for one tile row) plus B's in one f64 LDS add.
 // ------------------------------------------------------------------------------------------------
 
-// One pixel's routing state for a pair: its saved ref, g' / S (0 when it routes nothing) and the
-// centre W / S (0 likewise).
+// One pixel's routing state for a pair: its saved ref, g' / S and the centre W / S (both 0 outside
+// the image).
 struct RoutePixel
 {
     float ref, scaled, outc;
-    bool route;
+    bool in;
 };
 
 template <int MK, int KH, int KW, bool MASKED>
@@ -644,9 +650,8 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1, NC = smorph_bin_copies(K);
-    // MAX / MIN losers, and lanes outside the image (another pixel's ref, so e may be infinite):
-    // c cleared.
-    constexpr bool GATE = MK == MK_MAX || MK == MK_MIN || MASKED;
+    // Lanes outside the image (another pixel's ref, so e may be infinite): c cleared.
+    constexpr bool GATE = MASKED;
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     float asumA = 0.0f, asumB = 0.0f;
@@ -657,7 +662,7 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
         const float pg = ek * P.scaled;
         const float centered = vk - P.outc;
         float c = fmaf(a * pg, centered, pg);
-        if constexpr (GATE) c = P.route ? c : 0.0f;
+        if constexpr (GATE) c = P.in ? c : 0.0f;
         asum = fmaf(pg * (vk - P.ref), centered, asum);
         // Keeps the compiler from deferring the alpha terms, which would hold every tap's factors
         // in registers.
@@ -705,7 +710,7 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
             if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
         }
     }
-    return (A.route ? asumA : 0.0f) + (B.route ? asumB : 0.0f);
+    return (A.in ? asumA : 0.0f) + (B.in ? asumB : 0.0f);
 }
 
 template <int MK, int KH, int KW>
@@ -817,16 +822,17 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
         auto route_pixel = [&](bool in, float gv, float cnt, float outv, const PairStats& st) {
             RoutePixel r;
             gv = in ? gv * p.scale : 0.0f;
-            bool route = in;
             if constexpr (MK == MK_MAX || MK == MK_MIN)
             {
+                // A pair that is not a winner routes with g' = 0 (its c are 0, or NaN where its own
+                // values are not finite), as the reference.
                 gv = gv / (cnt > 0.0f ? cnt : 1.0f);
-                route = route && is_winner(st.outp, outv);
+                gv = is_winner(st.outp, outv) ? gv : 0.0f;
             }
             r.ref = st.ref;
-            r.scaled = route ? gv * st.inv : 0.0f;
-            r.outc = route ? st.outp : 0.0f;
-            r.route = route;
+            r.scaled = in ? gv * st.inv : 0.0f;
+            r.outc = in ? st.outp : 0.0f;
+            r.in = in;
             return r;
         };
         load_g(o_begin);
@@ -1006,29 +1012,32 @@ hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hip
     return p.pstats ? bwd_dispatch<true>(mk, p, stream) : bwd_dispatch<false>(mk, p, stream);
 }
 
-// MAX / MIN winner counts from the saved statistics: counts[b, o, pixel] = the number of input
-// channels i whose W / S lies within 1e-6 of the merged output (what the counting forward pass
-// computes, smorph_cpu_kernels.hxx:622-627), one thread per output pixel.
+// MAX / MIN merge target and winner counts from the saved statistics: target[b, o, pixel] =
+// smorph_merge_target of the merged output, counts[b, o, pixel] = the number of input channels i
+// whose W / S lies within 1e-6 of it (what the counting forward pass computes,
+// smorph_cpu_kernels.hxx:507-518, 622-627), one thread per output pixel.
 __global__ __launch_bounds__(BLOCK) void smorph_counts_saved(const float* __restrict__ outp, const float* __restrict__ out,
-                                                             float* __restrict__ counts, int64_t n_out, int cin, int64_t plane)
+                                                             float* __restrict__ counts, float* __restrict__ target, int64_t n_out, int cin,
+                                                             int64_t plane)
 {
     const int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
     if (j >= n_out) return;
     const int64_t bo = j / plane, pix = j - bo * plane;
-    const float t = out[j];
     const float* q = outp + bo * cin * plane + pix;
+    const float t = smorph_merge_target(out[j], q[0]);
     float m = 0.0f;
     for (int i = 0; i < cin; ++i)
         if (is_winner(q[(int64_t)i * plane], t)) m = m + 1.0f;
     counts[j] = m;
+    target[j] = t;
 }
 
-hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, const Geom& g, hipStream_t stream)
+hipError_t launch_smorph_counts_saved(const float* outp, const float* out, float* counts, float* target, const Geom& g, hipStream_t stream)
 {
     const int64_t n_out = (int64_t)g.B * g.Cout * g.plane();
     if (n_out == 0) return hipSuccess;
     const unsigned blocks = (unsigned)((n_out + BLOCK - 1) / BLOCK);
-    smorph_counts_saved<<<blocks, BLOCK, 0, stream>>>(outp, out, counts, n_out, g.Cin, g.plane());
+    smorph_counts_saved<<<blocks, BLOCK, 0, stream>>>(outp, out, counts, target, n_out, g.Cin, g.plane());
     return hipGetLastError();
 }
 

@@ -355,6 +355,32 @@ def test_smorph_static_interior_and_border_tiles(K, H, merge, a, saved, monkeypa
         assert normwise_error(actual, expected) <= 1e-6
 
 
+@pytest.mark.parametrize("saved", [True, False], ids=["saved-stats", "recomputed"])
+@pytest.mark.parametrize("merge", ["sum", "max", "identity"])
+@pytest.mark.parametrize("K", [3, 7])
+def test_smorph_static_nan_input(K, merge, saved, monkeypatch):
+    """An in-image NaN in the input propagates through the float32 static smorph kernels as through
+    the reference (its window's pair outputs, and the gradients they route, are NaN; NaN never wins
+    the window's extremum, nor the MAX merge), on interior and border tiles; every finite value
+    within tolerance."""
+    monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", str(1 << 40) if saved else "0")
+    B, Cin, Cout, H, W = 1, 2, 3, 20, 200
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(51, B, Cin, H, W, kind="randn")
+    x[0, 0, 9, 100] = float("nan")  # an interior tile
+    x[0, 1, 0, 3] = float("nan")  # a border tile, next to the image corner
+    w = seeded(52, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    alpha = torch.where(torch.arange(pairs) % 2 == 0, 2.0, -3.0).reshape((Cout,) if merge == "identity" else (Cout, Cin))
+    g = seeded(53, B, Cout, H, W, kind="randn")
+    results = _smorph_case(merge, x, w, alpha, g)
+    # The oracle's output holds NaN, except under MAX, whose merge never picks a NaN channel.
+    assert np.isnan(results[0][1]).any() == (merge != "max")
+    for actual, expected in results:
+        assert normwise_error(actual, expected) <= 1e-6
+
+
 def _window_extremum(x, w, dilation_like):
     """ref of every pair and pixel, (B, Cout, Cin, H, W): the extremum of x[y + KH/2 - kh, c + KW/2 - kw]
     + w[kh, kw] over the in-image taps (one rounding per tap, so exact in float32)."""
