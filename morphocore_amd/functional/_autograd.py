@@ -244,7 +244,7 @@ class _SmorphFunction(torch.autograd.Function):
     """Smorph<merge> (smorph.cpp:20-111) on 4-D, checked arguments; `w4` is the blended w~."""
 
     @staticmethod
-    def forward(ctx, x4, w4, alpha, merge):
+    def forward(ctx, x4, w4, alpha, merge, needs_grad):
         geom = _geom(x4, w4)
         B, Cin, Cout, Cw, H, W, KH, KW = geom
         x4c = x4.contiguous()
@@ -253,7 +253,7 @@ class _SmorphFunction(torch.autograd.Function):
         out = torch.empty((B, Cout, H, W), dtype=x4c.dtype, device=x4c.device)
         stats = None
         nbytes = _native.smorph_stats_bytes(int(merge), x4c.dtype, geom)
-        if _save_smorph_stats(nbytes, any(ctx.needs_input_grad[:3]), x4c.device):
+        if _save_smorph_stats(nbytes, needs_grad, x4c.device):
             stats = torch.empty(nbytes // 4, dtype=torch.float32, device=x4c.device)
         _native.smorph_forward(int(merge), x4c, w4c, alpha_pairs, out, geom, stats=stats)
         ctx.save_for_backward(out, alpha, x4c, w4c, stats)
@@ -279,7 +279,7 @@ class _SmorphFunction(torch.autograd.Function):
             grad_alpha = grad_alpha_pairs.view_as(alpha)
         else:
             grad_alpha = grad_alpha_pairs.sum().view_as(alpha)
-        return grad_input, grad_weight, grad_alpha, None
+        return grad_input, grad_weight, grad_alpha, None, None
 
 
 def smorph_operation(input: torch.Tensor, weight: torch.Tensor, alpha: torch.Tensor, merge: int) -> torch.Tensor:
@@ -298,7 +298,9 @@ def smorph_operation(input: torch.Tensor, weight: torch.Tensor, alpha: torch.Ten
         raise RuntimeError("Input channels must match weight input channels")
     smorph_pair_alphas(alpha, merge, int(x4.shape[1]), int(w4.shape[0]))
     _check_device(x4, w4, alpha, name="smorph_forward_hip")
-    out = _SmorphFunction.apply(x4, w4, alpha, merge)
+    # Inside Function.forward autograd is off: whether a backward can follow is decided here.
+    needs_grad = torch.is_grad_enabled() and (input.requires_grad or weight.requires_grad or alpha.requires_grad)
+    out = _SmorphFunction.apply(x4, w4, alpha, merge, needs_grad)
     return output_to_original(out, input_dims)
 
 

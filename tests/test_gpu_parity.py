@@ -381,6 +381,34 @@ def test_smorph_static_nan_input(K, merge, saved, monkeypatch):
         assert normwise_error(actual, expected) <= 1e-6
 
 
+def test_smorph_saves_statistics_only_for_a_backward(monkeypatch):
+    """The forward keeps the pair statistics only when a backward can follow (grad mode on and an
+    input that requires grad), within the memory limit; the results do not depend on it."""
+    mca, native, _ = _mca()
+    dev = torch.device("cuda")
+    seen = []
+    real = native.smorph_forward
+
+    def spy(*args, stats=None, **kw):
+        seen.append(stats is not None)
+        return real(*args, stats=stats, **kw)
+
+    monkeypatch.setattr(native, "smorph_forward", spy)
+    x = seeded(61, 1, 2, 12, 70, kind="randn").to(dev)
+    w = seeded(62, 3, 2, 3, 3, kind="randn", scale=0.1).to(dev)
+    alpha = torch.full((3, 2), 2.0, device=dev)
+    with torch.no_grad():
+        y0 = mca.functional.smorph(x, w, alpha, channel_merge_mode="sum")
+    y1 = mca.functional.smorph(x, w, alpha, channel_merge_mode="sum")  # nothing requires grad
+    xr = x.clone().requires_grad_(True)
+    y2 = mca.functional.smorph(xr, w, alpha, channel_merge_mode="sum")
+    monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", "0")
+    y3 = mca.functional.smorph(xr, w, alpha, channel_merge_mode="sum")
+    assert seen == [False, False, True, False]
+    for y in (y1, y2, y3):
+        assert torch.equal(y, y0)
+
+
 def _window_extremum(x, w, dilation_like):
     """ref of every pair and pixel, (B, Cout, Cin, H, W): the extremum of x[y + KH/2 - kh, c + KW/2 - kw]
     + w[kh, kw] over the in-image taps (one rounding per tap, so exact in float32)."""
