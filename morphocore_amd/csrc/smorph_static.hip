@@ -10,10 +10,11 @@
 //    windows lie inside the image take a path without any check. Out-of-image taps are excluded by
 //    position, as in the reference (SmorphBlockMask, smorph_valid_rows); an in-image NaN propagates
 //    as in the reference;
-//  * the backward keeps every tap's e in registers (up to 7x7) between the pass that forms S and W
-//    and the pass that routes the gradient, so each exponential is evaluated once per backward
-//    (11x11 keeps its first two rows and re-evaluates the rest: 121 registers would cost more waves
-//    than the exponentials cost VALU);
+//  * the forward can save each pair's ref, 1 / S and W / S, and the backward from them (two output
+//    rows per wave) evaluates each exponential once; the backward that recomputes them keeps every
+//    tap's e in registers (up to 7x7) between the pass that forms S and W and the pass that routes
+//    the gradient (11x11 keeps its first two rows and re-evaluates the rest: 121 registers would
+//    cost more waves than the exponentials cost VALU);
 //  * every lane of a wave routes the same tap at once: a row of KW taps is summed per tile column
 //    across the wave (a DPP shift per tap) before one LDS atomic per row, and the grad_weight LDS
 //    atomics hit lane-striped copies (no bank conflicts). LDS atomics cost per instruction, not per
@@ -314,15 +315,15 @@ struct PairStats
     float ref, inv, outp;
 };
 
-// One pair (o, i) at this lane's pixel: the forward's ref, S and W (recomputed unless SAVED, every
-// tap's e kept up to 7x7), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input
+// One pair (o, i) at this lane's pixel, recomputing: the forward's ref, S and W (every tap's e kept
+// up to 7x7), then the routing of c_k = p_k (1 + alpha (v_k - out)) g' to grad_input
 // (the LDS tile), to the grad_weight bin of tap k and to grad_alpha (returned: the sum of
 // p_k (v_k - ref)(v_k - out) over the taps). gv is g * scale (0 outside the image); for MAX / MIN it
 // is divided by the pixel's winner count, and a pair not within 1e-6 of the merge target outv routes
-// with g' = 0. SAVED: `st` holds the forward's statistics and each e is evaluated once, in the routing.
-template <int MK, int KH, int KW, bool MASKED, bool SAVED>
+// with g' = 0.
+template <int MK, int KH, int KW, bool MASKED>
 __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
-                                                 PairStats st, const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
+                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
@@ -334,9 +335,9 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     // Taps whose e stays in registers between the passes: all up to 7x7; for 11x11 the first two
     // rows (three waves per SIMD still; a third row takes 256 registers), except IDENTITY (no room).
-    constexpr int KE = SAVED ? 0 : (K <= 49 ? K : (MK == MK_IDENT ? 0 : 2 * KW));
+    constexpr int KE = K <= 49 ? K : (MK == MK_IDENT ? 0 : 2 * KW);
     float e[KE > 0 ? KE : 1];
-    if constexpr (!SAVED)
+    PairStats st;
     {
         const bool dil = a >= 0.0f;
         const float ref = smorph_ref<KH, KW, MASKED>(xb, wl, dil, tm);
@@ -388,26 +389,18 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         // the (complete) total of the right halo column 63 + KW - kw; lane KW - 1 - kw keeps it.
         float racc = 0.0f, halo = 0.0f;
         __builtin_amdgcn_sched_barrier(0);
-        // x and w read from LDS ahead of their use, so that the reads' latency overlaps arithmetic
-        // (each tap is one long dependent chain): with SAVED the whole row at once (paired reads),
-        // else one tap ahead (fewer registers, which the recomputing kernels lack).
-        constexpr int XR = SAVED ? KW : 1;
-        float xr[XR], wr[XR];
-#pragma unroll
-        for (int kw = 0; kw < XR; ++kw)
-        {
-            xr[kw] = xb[-(kh * COLS + kw)];
-            wr[kw] = wl[kh * KW + kw];
-        }
+        // x and w of the next tap read from LDS one tap ahead of their use, so that the reads'
+        // latency overlaps this tap's arithmetic (each tap is one long dependent chain).
+        float xn = xb[-(kh * COLS)], wn = wl[kh * KW];
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
             const int k = kh * KW + kw;
-            const float vk = SAVED ? xr[kw < XR ? kw : 0] + wr[kw < XR ? kw : 0] : xr[0] + wr[0];
-            if (!SAVED && kw + 1 < KW)
+            const float vk = xn + wn;
+            if (kw + 1 < KW)
             {
-                xr[0] = xb[-(kh * COLS + kw + 1)];
-                wr[0] = wl[k + 1];
+                xn = xb[-(kh * COLS + kw + 1)];
+                wn = wl[k + 1];
             }
             float ekr;
             if (k >= KE)
@@ -445,15 +438,12 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
     return in ? asum : 0.0f;
 }
 
-// Waves per SIMD requested (measured on MI355X), recomputing: up to 7x7 six (80 registers, a few
-// spilled; 7% faster than four, five fit without spills), 11x11 five (95 registers, 2 spilled; 16%
-// faster than three, with 16 bin copies so that five workgroups' LDS fits a CU). With the forward's
-// saved statistics (SAVED) no e is kept: about 50 registers, as many waves as the LDS allows (seven
-// workgroups per CU at 7x7, five at 11x11).
-constexpr int smorph_bwd_waves(int K, bool saved) { return saved ? (K > 49 ? 5 : (K > 25 ? 7 : 8)) : (K > 49 ? 5 : 6); }
-
-template <int MK, int KH, int KW, bool SAVED>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bwd_waves(KH * KW, SAVED), 8))) void smorph_bwd_static(
+// The backward recomputing each pair's statistics (the saved-statistics backward is
+// smorph_bwd_saved2 below). Waves per SIMD requested (measured on MI355X): up to 7x7 six (80
+// registers, a few spilled; 7% faster than four, five fit without spills), 11x11 five (95 registers,
+// 2 spilled; 16% faster than three, with 16 bin copies so that five workgroups' LDS fits a CU).
+template <int MK, int KH, int KW>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 6, 8))) void smorph_bwd_static(
     const SmorphBwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
@@ -527,7 +517,6 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bw
         // pixel, one output channel ahead.
         const int64_t pix = (int64_t)min(h, g.H - 1) * g.W + min(wc, g.W - 1);
         float gv_n = 0.0f, cnt_n = 0.0f, out_n = 0.0f;
-        PairStats st_n{0.0f, 0.0f, 0.0f};
         auto load_g = [&](int o) {
             o = min(o, o_end - 1);
             const int64_t oi = ((int64_t)b * g.Cout + o) * plane + pix;
@@ -537,13 +526,6 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bw
                 cnt_n = p.counts[oi];
                 out_n = p.out[oi];
             }
-            if constexpr (SAVED)
-            {
-                const float* q = p.pstats + (((int64_t)b * g.Cout + o) * (MK == MK_IDENT ? 1 : g.Cin) + (MK == MK_IDENT ? 0 : i)) * plane + pix;
-                st_n.ref = __builtin_nontemporal_load(q);
-                st_n.inv = __builtin_nontemporal_load(q + p.nstat);
-                st_n.outp = __builtin_nontemporal_load(q + 2 * p.nstat);
-            }
         };
         load_g(o_begin);
         __syncthreads();
@@ -551,15 +533,14 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(smorph_bw
         {
             const int buf = (o - o_begin) & 1;
             const float gv = in ? gv_n * p.scale : 0.0f, cnt = cnt_n, outv = out_n;
-            const PairStats st = st_n;
             load_g(o + 1);
             const float* w = wl[buf];
             const float a = w[K];
             float asum;
             if (interior)
-                asum = smorph_bwd_pair<MK, KH, KW, false, SAVED>(xb, w, a, gv, cnt, outv, in, st, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
             else
-                asum = smorph_bwd_pair<MK, KH, KW, true, SAVED>(xb, w, a, gv, cnt, outv, in, st, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
             lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
@@ -956,30 +937,18 @@ hipError_t launch_smorph_fwd_static(int mk, bool stats, const SmorphFwdParams<fl
     return p.pstats ? fwd_dispatch<true>(mk, stats, p, stream) : fwd_dispatch<false>(mk, stats, p, stream);
 }
 
-template <int KS, bool SAVED>
+template <int KS>
 static hipError_t bwd_size(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
     const unsigned blocks = (unsigned)((int64_t)p.g.B * p.g.Cin * p.nstrips);
     switch (mk)
     {
-        case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
-        default: smorph_bwd_static<MK_IDENT, KS, KS, SAVED><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        default: smorph_bwd_static<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
-}
-
-template <bool SAVED>
-static hipError_t bwd_dispatch(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
-{
-    switch (p.g.KH)
-    {
-        case 3: return bwd_size<3, SAVED>(mk, p, stream);
-        case 5: return bwd_size<5, SAVED>(mk, p, stream);
-        case 7: return bwd_size<7, SAVED>(mk, p, stream);
-        default: return bwd_size<11, SAVED>(mk, p, stream);
-    }
 }
 
 template <int KS>
@@ -998,18 +967,15 @@ static hipError_t bwd2_size(int mk, const SmorphBwdParams<float>& p, hipStream_t
 
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
-    if (p.pstats && p.t.rh == 2)
+    // From saved statistics: the two-row kernel (64 x 8 tiles); recomputing: the one-row kernel.
+    if (p.t.rh != (p.pstats ? 2 : 1)) return hipErrorInvalidValue;
+    switch (p.g.KH)
     {
-        switch (p.g.KH)
-        {
-            case 3: return bwd2_size<3>(mk, p, stream);
-            case 5: return bwd2_size<5>(mk, p, stream);
-            case 7: return bwd2_size<7>(mk, p, stream);
-            default: return bwd2_size<11>(mk, p, stream);
-        }
+        case 3: return p.pstats ? bwd2_size<3>(mk, p, stream) : bwd_size<3>(mk, p, stream);
+        case 5: return p.pstats ? bwd2_size<5>(mk, p, stream) : bwd_size<5>(mk, p, stream);
+        case 7: return p.pstats ? bwd2_size<7>(mk, p, stream) : bwd_size<7>(mk, p, stream);
+        default: return p.pstats ? bwd2_size<11>(mk, p, stream) : bwd_size<11>(mk, p, stream);
     }
-    if (p.t.rh != 1) return hipErrorInvalidValue;
-    return p.pstats ? bwd_dispatch<true>(mk, p, stream) : bwd_dispatch<false>(mk, p, stream);
 }
 
 // MAX / MIN merge target and winner counts from the saved statistics: target[b, o, pixel] =
