@@ -254,7 +254,10 @@ class _SmorphFunction(torch.autograd.Function):
         stats = None
         nbytes = _native.smorph_stats_bytes(int(merge), x4c.dtype, geom)
         if _save_smorph_stats(nbytes, needs_grad, x4c.device):
-            stats = torch.empty(nbytes // 4, dtype=torch.float32, device=x4c.device)
+            try:
+                stats = torch.empty(nbytes // 4, dtype=torch.float32, device=x4c.device)
+            except torch.cuda.OutOfMemoryError:
+                stats = None  # fragmented memory: the backward recomputes them
         _native.smorph_forward(int(merge), x4c, w4c, alpha_pairs, out, geom, stats=stats)
         ctx.save_for_backward(out, alpha, x4c, w4c, stats)
         ctx.merge = merge
