@@ -633,6 +633,37 @@ def test_config2_full_size_properties():
     assert float(gx.double().sum()) <= 16 * 32 * 32 * 128 * 128
 
 
+@pytest.mark.parametrize("merge,K,a", [("mean", 7, 1.0), ("mean", 7, -20.0), ("sum", 11, 5.0), ("max", 5, 3.0), ("identity", 7, -1.0)])
+def test_smorph_large_grid_saved_matches_recomputed(merge, K, a, monkeypatch):
+    """At a size with thousands of workgroups (configs[2]-like channels, 160 x 200 images), the
+    backward from saved statistics (two rows per wave) and the recomputing backward (one row per
+    wave) are independent kernels: their forward outputs are bit for bit equal and their gradients
+    agree to the float32 tolerance; batch element 0 of the forward matches the oracle."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    B, C, H, W = 2, 16, 160, 200
+    x = seeded(71, B, C, H, W, kind="randn")
+    w = seeded(72, *_weight_shape(merge, C, C, K, K), kind="randn", scale=0.1)
+    pairs = C if merge == "identity" else C * C
+    alpha = (torch.full((pairs,), a) + seeded(73, pairs, kind="randn", scale=0.05)).reshape((C,) if merge == "identity" else (C, C))
+    g = seeded(74, B, C, H, W, kind="randn")
+    results = []
+    for limit in (str(1 << 40), "0"):
+        monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", limit)
+        xd = x.to(dev).requires_grad_(True)
+        wd = w.to(dev).requires_grad_(True)
+        ad = alpha.to(dev).requires_grad_(True)
+        out = torch.ops.morphocore.smorph(xd, wd, ad, O.MERGES[merge])
+        out.backward(g.to(dev))
+        results.append((_np(out), _np(xd.grad), _np(wd.grad), _np(ad.grad)))
+    saved, recomputed = results
+    assert np.array_equal(saved[0], recomputed[0])
+    for s_, r_ in zip(saved[1:], recomputed[1:]):
+        assert normwise_error(s_, r_) <= 1e-6
+    ref = O.smorph_forward(O.MERGES[merge], x[:1].numpy(), w.numpy(), alpha.numpy())
+    assert normwise_error(saved[0][:1], ref) <= 1e-6
+
+
 # ------------------------------------------------------------------------------------------------
 # Saved per-pair taps (sum / mean / identity) and the recompute path
 # ------------------------------------------------------------------------------------------------
