@@ -123,9 +123,10 @@ int mca_smorph_backward_f64(int merge, const double* input, const double* weight
  * input (smorph.cu:63-103, smorph_cpu_kernels.hxx:387-638). The forward below also stores, for every
  * channel pair at every output pixel, the window's extremum, 1 / S and W / S (three float32 arrays of
  * B * Cout * P * H * W values, P = Cin, or 1 for IDENTITY; mca_smorph_stats_bytes_f32 bytes, 0 when
- * the configuration has no such path); the backward below reads them and evaluates each tap's
- * exponential once. Both produce bit for bit what mca_smorph_forward_f32 / mca_smorph_backward_f32
- * produce (the same workspace). */
+ * the configuration has no such path); the backward below reads them instead of recomputing them
+ * (the same workspace as mca_smorph_backward_f32). The forward's output is bit for bit that of
+ * mca_smorph_forward_f32; the gradients agree with mca_smorph_backward_f32's within the float32
+ * tolerance (the two kernels add the same terms in different orders). */
 size_t mca_smorph_stats_bytes_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW);
 int mca_smorph_forward_stats_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, float* stats,
                                  int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
