@@ -125,9 +125,9 @@ int smorph_forward_impl(int merge, const T* input, const T* weight, const T* alp
 // Checks of the saved-statistics entry points: the configuration has them and a buffer is given.
 int check_stats(int merge, const mca::Geom& g, const void* stats)
 {
-    if (mca::smorph_stats_values(merge, g) == 0)
+    if (!mca::smorph_stats_supported(g))
         return fail("No saved smorph statistics for this configuration (float32, square 3x3, 5x5, 7x7 or 11x11 elements only)");
-    if (!stats) return fail("stats must not be null");
+    if (!stats && mca::smorph_stats_values(merge, g) > 0) return fail("stats must not be null");
     return MCA_OK;
 }
 

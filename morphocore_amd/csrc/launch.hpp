@@ -64,6 +64,8 @@ hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x
 // Values in each of the three arrays of saved smorph pair statistics (float32 static kernels only;
 // 0 when the configuration has none).
 int64_t smorph_stats_values(int merge, const Geom& g);
+// Whether the configuration has the saved-statistics path (float32 static sizes), empty or not.
+bool smorph_stats_supported(const Geom& g);
 
 // `stats`: where to save the pair statistics (three arrays of smorph_stats_values values), or null.
 template <typename T>

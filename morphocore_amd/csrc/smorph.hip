@@ -375,10 +375,12 @@ static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t str
 
 int64_t smorph_stats_values(int merge, const Geom& g) { return smorph_stats_count<float>(merge, g); }
 
+bool smorph_stats_supported(const Geom& g) { return smorph_static_supported<float>(g); }
+
 template <typename T>
 hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* out, const Geom& g, hipStream_t stream, float* stats)
 {
-    if (stats && smorph_stats_count<T>(merge, g) == 0) return hipErrorInvalidValue;
+    if (stats && !smorph_static_supported<T>(g)) return hipErrorInvalidValue;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return hipSuccess;
     SmorphFwdParams<T> p{};
     p.x = x;
@@ -409,7 +411,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
 {
     hipError_t err;
     if (workspace_bytes < smorph_backward_workspace<T>(merge, g)) return hipErrorInvalidValue;
-    if (stats && smorph_stats_count<T>(merge, g) == 0) return hipErrorInvalidValue;
+    if (stats && !smorph_static_supported<T>(g)) return hipErrorInvalidValue;
     const int64_t nstat = smorph_stats_count<T>(merge, g);
     const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g, stats != nullptr);
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();

@@ -115,3 +115,7 @@ def test_smorph_stats_bytes_and_rejection():
                                            None, 0, None)
     assert rc == 1 and "stats must not be null" in lib.mca_last_error().decode()
     assert _native.smorph_stats_bytes(2, __import__("torch").float64, (B, Cin, Cout, Cw, H, W, 3, 3)) == 0
+    # An empty batch has no statistics to save: accepted without a buffer, and nothing is launched.
+    assert lib.mca_smorph_stats_bytes_f32(2, 0, Cin, Cout, Cw, H, W, 3, 3) == 0
+    rc = lib.mca_smorph_forward_stats_f32(2, None, None, None, None, None, 0, Cin, Cout, Cw, H, W, 3, 3, None)
+    assert rc == 0, lib.mca_last_error().decode()
