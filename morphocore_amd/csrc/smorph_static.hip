@@ -617,6 +617,37 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
 //  * a tap's bin receives A's value (kept for one tile row) plus B's in one f64 LDS add.
 // ------------------------------------------------------------------------------------------------
 
+// 11x11 bins of the two-row backward, packed: four bin values of a lane summed over groups of four
+// lanes into one register (v_permlane32_swap then v_permlane16_swap, gfx950), so that one LDS add
+// with 64 distinct addresses takes all four. The 16-lane row r of the result holds value
+// smorph_pack_value(r) (0, 2, 1, 3 for rows 0-3) of the four, summed over lanes (l, l + 16, l + 32,
+// l + 48) of the inputs. Every lane of the wave takes part. (With 16 copies per bin, two lanes of a
+// half wave share each address of an unpacked add, which then costs 2.4 conflict-free adds.)
+__device__ __forceinline__ float smorph_pack4(float c0, float c1, float c2, float c3)
+{
+    const auto h01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c0), __float_as_uint(c1), false, false);
+    const auto h23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c2), __float_as_uint(c3), false, false);
+    const float s01 = __uint_as_float(h01[0]) + __uint_as_float(h01[1]);  // lanes 0-31: c0, 32-63: c1
+    const float s23 = __uint_as_float(h23[0]) + __uint_as_float(h23[1]);  // lanes 0-31: c2, 32-63: c3
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s01), __float_as_uint(s23), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+__host__ __device__ constexpr int smorph_pack_value(int row) { return ((row & 1) << 1) | (row >> 1); }
+
+// Packed bins: the K tap values in the order the two-row backward emits them (tile row j = 1 .. KH,
+// then kw: tap (KH - j) KW + kw) in groups of four, group q of 64 doubles, 16-lane row r holding
+// emission 4 q + smorph_pack_value(r), 16 copies; then the last emission (K % 4 == 1) and alpha,
+// unpacked, 16 copies each (a 32-double tail keeps the 11x11 kernel's LDS within five workgroups per
+// CU).
+template <int K>
+struct PackedBins
+{
+    static constexpr bool on = K > 49;
+    static constexpr int groups = K / 4;
+    static constexpr int size = groups * WAVE + 2 * 16;
+};
+
 // One pixel's routing state for a pair: its saved ref, g' / S and the centre W / S (both 0 outside
 // the image).
 struct RoutePixel
@@ -627,7 +658,7 @@ struct RoutePixel
 
 template <int MK, int KH, int KW, bool MASKED>
 __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* wl, float a, const RoutePixel& A, const RoutePixel& B,
-                                                  unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, int lane)
+                                                  unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, Acc* btail, int lane)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1, NC = smorph_bin_copies(K);
@@ -637,6 +668,8 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     float asumA = 0.0f, asumB = 0.0f;
     float abuf[KW];  // A's c of the previous tile row's taps, added to B's in the same taps' bins
+    constexpr bool PACK = PackedBins<K>::on;
+    float pk[4];  // PACK: the current group of four bin values
     auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
         const float vk = x + wl[k];
         const float ek = exp_ref(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
@@ -681,7 +714,19 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
                     racc = wave_shift_up(racc) + cs;
                 }
             }
-            if (j > 0) lds_add(&bl[(khB * KW + kw) * NC], (Acc)(cB + abuf[kw]));
+            if (j > 0)
+            {
+                if constexpr (PACK)
+                {
+                    const int e = (j - 1) * KW + kw;  // emission index (a constant once unrolled)
+                    pk[e & 3] = cB + abuf[kw];
+                    if ((e & 3) == 3) lds_add(&bl[(e >> 2) * WAVE], (Acc)smorph_pack4(pk[0], pk[1], pk[2], pk[3]));
+                }
+                else
+                {
+                    lds_add(&bl[(khB * KW + kw) * NC], (Acc)(cB + abuf[kw]));
+                }
+            }
             if (j < KH) abuf[kw] = cA;
         }
         if (rv)
@@ -691,7 +736,15 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
             if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
         }
     }
-    return (A.in ? asumA : 0.0f) + (B.in ? asumB : 0.0f);
+    const float asum = (A.in ? asumA : 0.0f) + (B.in ? asumB : 0.0f);
+    if constexpr (PACK)
+    {
+        // The tail: the last emission (K % 4 == 1 for odd square elements), then alpha.
+        static_assert(K % 4 == 1, "odd square elements");
+        lds_add(&btail[0], (Acc)pk[0]);
+        lds_add(&btail[16], (Acc)asum);
+    }
+    return asum;
 }
 
 template <int MK, int KH, int KW>
@@ -701,9 +754,12 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int RH = 2, TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
     constexpr int NC = smorph_bin_copies(K);
+    constexpr bool PACK = PackedBins<K>::on;
+    constexpr int NBINS = PACK ? PackedBins<K>::size : (K + 1) * NC;
     __shared__ float tile[ROWS * COLS];
     __shared__ Acc gtile[ROWS * COLS];
-    __shared__ __align__(32) Acc bins[(K + 1) * NC];  // grad_weight bins of the K taps, then grad_alpha; NC copies each
+    // grad_weight bins of the K taps, then grad_alpha: NC copies each, or PACK's groups of four.
+    __shared__ __align__(32) Acc bins[NBINS];
     __shared__ __align__(16) float wl[2][(K + 4) & ~3];
     const Geom g = p.g;
     const Tiling t = p.t;
@@ -736,12 +792,13 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
     __shared__ float partials[NPART];
     const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
     for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
-    for (int j = threadIdx.x; j < (K + 1) * NC; j += BLOCK) bins[j] = Acc(0);
+    for (int j = threadIdx.x; j < NBINS; j += BLOCK) bins[j] = Acc(0);
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
     const float* xw = tile + RH * wave * COLS + lane + KW - 1;  // tile row 2 wave, this lane's tap-0 column
     Acc* gw = gtile + RH * wave * COLS + lane;
-    Acc* bl = bins + (lane & (NC - 1));
+    Acc* bl = bins + (PACK ? lane : (lane & (NC - 1)));
+    Acc* btail = bins + (PACK ? PackedBins<K>::groups * WAVE : 0) + (lane & 15);
     for (int tid = tile_begin; tid < tile_end; ++tid)
     {
         const int ty = tid / t.ntx, tx = tid - ty * t.ntx;
@@ -828,12 +885,43 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             const float a = w[K];
             float asum;
             if (interior)
-                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, lane);
+                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, lane);
             else
-                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, lane);
-            lds_add(&bl[K * NC], (Acc)asum);
+                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, lane);
+            if constexpr (!PACK) lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
+            if constexpr (PACK)
+            {
+                // Sum the 16 copies of each value (4 threads per value, 4 adjacent copies each, a
+                // butterfly over the 4) into this workgroup's slot: the packed groups, then the tail.
+                // The thread count is a multiple of 4.
+                constexpr int NG = PackedBins<K>::groups;
+                for (int j = threadIdx.x; j < NG * 16 + 2 * 4; j += BLOCK)
+                {
+                    double4* q = reinterpret_cast<double4*>(&bins[j * 4]);
+                    const double4 c4 = *q;
+                    *q = make_double4(0.0, 0.0, 0.0, 0.0);
+                    Acc v = (c4.x + c4.y) + (c4.z + c4.w);
+                    v += __shfl_xor(v, 1, 4);
+                    v += __shfl_xor(v, 2, 4);
+                    // Emission index: in the groups, or the tail's K - 1 (the last tap) and K (alpha).
+                    const int e = j < NG * 16 ? (j >> 4) * 4 + smorph_pack_value((j >> 2) & 3) : K - 1 + ((j - NG * 16) >> 2);
+                    if ((j & 3) == 0 && e <= K)
+                    {
+                        // Emission e < K is tap (KH - 1 - e / KW) KW + e % KW; e == K is alpha.
+                        const int k = e < K ? (KH - 1 - e / KW) * KW + e % KW : K;
+                        if (lds_partials)
+                            partials[(o - o_begin) * (K + 1) + k] += (float)v;
+                        else if (k < K)
+                            global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
+                        else
+                            global_add(&part_a[pair_index(o)], (float)v);
+                    }
+                }
+                __syncthreads();
+                continue;
+            }
             // Sum the NC copies of each bin (8 threads per bin, NC / 8 adjacent copies each, a butterfly
             // over the 8) into this workgroup's slot, as the one-row kernel does.
             constexpr int PER = NC / 8;
