@@ -617,12 +617,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
 //  * a tap's bin receives A's value (kept for one tile row) plus B's in one f64 LDS add.
 // ------------------------------------------------------------------------------------------------
 
-// 11x11 bins of the two-row backward, packed: four bin values of a lane summed over groups of four
-// lanes into one register (v_permlane32_swap then v_permlane16_swap, gfx950), so that one LDS add
-// with 64 distinct addresses takes all four. The 16-lane row r of the result holds value
+// Bins of the two-row backward at 7x7 and 11x11, packed: four bin values of a lane summed over
+// groups of four lanes into one register (v_permlane32_swap then v_permlane16_swap, gfx950), so that
+// one LDS add with 64 distinct addresses takes all four. The 16-lane row r of the result holds value
 // smorph_pack_value(r) (0, 2, 1, 3 for rows 0-3) of the four, summed over lanes (l, l + 16, l + 32,
-// l + 48) of the inputs. Every lane of the wave takes part. (With 16 copies per bin, two lanes of a
-// half wave share each address of an unpacked add, which then costs 2.4 conflict-free adds.)
+// l + 48) of the inputs. Every lane of the wave takes part. Measured on MI355X: 2% faster at 7x7
+// (a quarter of the LDS adds for 0.4 VALU instructions per tap), 3% at 11x11 (whose unpacked 16-copy
+// bins share each address between two lanes of a half wave, 2.4x the cost of an add).
 __device__ __forceinline__ float smorph_pack4(float c0, float c1, float c2, float c3)
 {
     const auto h01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c0), __float_as_uint(c1), false, false);
@@ -643,7 +644,7 @@ __host__ __device__ constexpr int smorph_pack_value(int row) { return ((row & 1)
 template <int K>
 struct PackedBins
 {
-    static constexpr bool on = K > 49;
+    static constexpr bool on = K > 25;
     static constexpr int groups = K / 4;
     static constexpr int size = groups * WAVE + 2 * 16;
 };
