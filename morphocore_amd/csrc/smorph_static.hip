@@ -649,6 +649,14 @@ struct PackedBins
     static constexpr int size = groups * WAVE + 2 * 16;
 };
 
+// Rows of right-halo values (KW - 1 each) that one register holds, and the registers for NR rows.
+template <int NR, int KW>
+struct HaloRows
+{
+    static constexpr int rows = WAVE / (KW - 1);
+    static constexpr int regs = (NR + rows - 1) / rows;
+};
+
 // One pixel's routing state for a pair: its saved ref, g' / S and the centre W / S (both 0 outside
 // the image).
 struct RoutePixel
@@ -659,7 +667,8 @@ struct RoutePixel
 
 template <int MK, int KH, int KW, bool MASKED>
 __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* wl, float a, const RoutePixel& A, const RoutePixel& B,
-                                                  unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, Acc* btail, int lane)
+                                                  unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, Acc* btail,
+                                                  const int (&hcell)[HaloRows<KH + 1, KW>::regs], Acc* gtile)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1, NC = smorph_bin_copies(K);
@@ -671,6 +680,13 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     float abuf[KW];  // A's c of the previous tile row's taps, added to B's in the same taps' bins
     constexpr bool PACK = PackedBins<K>::on;
     float pk[4];  // PACK: the current group of four bin values
+    // The right-halo columns of all KH + 1 tile rows, HaloRows<>::rows rows per register: tile row j's
+    // value for halo column c in lane (j % rows) (KW - 1) + c of register j / rows; one LDS add each
+    // at the end of the pair.
+    constexpr int HRW = HaloRows<KH + 1, KW>::rows, HREGS = HaloRows<KH + 1, KW>::regs;
+    float halo[HREGS];
+#pragma unroll
+    for (int r = 0; r < HREGS; ++r) halo[r] = 0.0f;
     auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
         const float vk = x + wl[k];
         const float ek = exp_ref(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
@@ -692,7 +708,7 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
         float xr[KW];
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw) xr[kw] = xw[j * COLS - kw];
-        float racc = 0.0f, halo = 0.0f;
+        float racc = 0.0f;
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
@@ -711,7 +727,7 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
                 else
                 {
                     const int fell = __builtin_amdgcn_readlane(__float_as_int(racc), WAVE - 1);
-                    asm("v_writelane_b32 %0, %1, %2" : "+v"(halo) : "s"(fell), "i"(KW - 1 - kw));
+                    asm("v_writelane_b32 %0, %1, %2" : "+v"(halo[j / HRW]) : "s"(fell), "i"((j % HRW) * (KW - 1) + KW - 1 - kw));
                     racc = wave_shift_up(racc) + cs;
                 }
             }
@@ -732,11 +748,12 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
         }
         if (rv)
         {
-            Acc* grow = gw + j * COLS;  // tile row 2 wave + j, column `lane`
-            lds_add(grow, (Acc)racc);
-            if (lane < KW - 1) lds_add(grow + WAVE, (Acc)halo);
+            lds_add(gw + j * COLS, (Acc)racc);  // tile row 2 wave + j, column `lane`
         }
     }
+#pragma unroll
+    for (int r = 0; r < HREGS; ++r)
+        if (hcell[r] >= 0) lds_add(&gtile[hcell[r]], (Acc)halo[r]);
     const float asum = (A.in ? asumA : 0.0f) + (B.in ? asumB : 0.0f);
     if constexpr (PACK)
     {
@@ -800,6 +817,16 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
     Acc* gw = gtile + RH * wave * COLS + lane;
     Acc* bl = bins + (PACK ? lane : (lane & (NC - 1)));
     Acc* btail = bins + (PACK ? PackedBins<K>::groups * WAVE : 0) + (lane & 15);
+    // The gtile cell of this lane's value in each halo register (tile row RH wave + j, halo column c,
+    // right of the wave's 64 columns), or -1 for lanes past the last tile row.
+    constexpr int HRW = HaloRows<KH + 1, KW>::rows, HREGS = HaloRows<KH + 1, KW>::regs;
+    int hcell[HREGS];
+#pragma unroll
+    for (int r = 0; r < HREGS; ++r)
+    {
+        const int j = r * HRW + lane / (KW - 1), c = lane % (KW - 1);
+        hcell[r] = lane < HRW * (KW - 1) && j <= KH ? (RH * wave + j) * COLS + WAVE + c : -1;
+    }
     for (int tid = tile_begin; tid < tile_end; ++tid)
     {
         const int ty = tid / t.ntx, tx = tid - ty * t.ntx;
@@ -886,9 +913,9 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             const float a = w[K];
             float asum;
             if (interior)
-                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, lane);
+                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             else
-                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, lane);
+                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             if constexpr (!PACK) lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
