@@ -146,11 +146,10 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
 
 // SAVE: also store each pair's ref, 1 / S and W / S at every in-image pixel (p.pstats), which the
 // backward then reads instead of recomputing them.
-// Waves per SIMD requested: eight up to 7x7, five at 11x11 (the occupancy the register-held element
-// and window allow; without the request the compiler takes more registers for fewer waves, measured
-// ~2% slower).
+// Waves per SIMD requested: seven up to 7x7, five at 11x11 (without a request the compiler takes more
+// registers for fewer waves, ~2% slower; eight spill at 7x7 and measured 0.6% slower than seven).
 template <int MK, int KH, int KW, bool STATS, bool SAVE>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 8, 8))) void smorph_fwd_static(
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : 7, 8))) void smorph_fwd_static(
     const SmorphFwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
