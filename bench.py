@@ -2,6 +2,9 @@
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu-baseline]
 
+K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
+millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
+
 A step is one forward + backward pass of the configuration's operator(s) over one batch of synthetic,
 seeded input already resident in HBM (default configs[1], "C2"). The timed
 region is exactly K steps between device synchronisations. Prints one JSON line with the whole-job
@@ -52,8 +55,8 @@ CONFIGS = {
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
-    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default: per config, DEFAULT_STEPS)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: per config, DEFAULT_STEPS)")
     p.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -61,7 +64,21 @@ def parse():
                    help="launch only the config's dominant kernel --steps times (for rocprofv3 counter runs)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="copy a MIB-sized device buffer --steps times (scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    return p.parse_args()
+    args = p.parse_args()
+    steps, warmup = DEFAULT_STEPS[args.config]
+    if args.kernel_only or args.copy_calibration:
+        steps, warmup = 10, 0
+    if args.steps is None:
+        args.steps = steps
+    if args.warmup is None:
+        args.warmup = warmup
+    return args
+
+
+# Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
+# after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
+# millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1)}
 
 
 def taps(cfg, x_shape=None):
