@@ -432,6 +432,10 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             // elements store each pair's tap at once (the deferred form needs more registers than
             // leave two waves per SIMD).
             constexpr bool DEFER = K <= 25;
+            // Up to 5x5 the first row holding the extremum and its values are selected from the
+            // registers that computed them; larger elements read that row again from LDS (a
+            // per-lane row: bank conflicts between lanes on different rows).
+            constexpr bool SELECT = K <= 25 && sizeof(T) == 4;
             using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
             const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
             auto store_tap = [&](int ob, int r, int a) {
@@ -451,29 +455,51 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
                     // start value, then the first row holding it: rows that hold only NaN never
                     // compare equal, and a pair that never improves on the start value keeps tap 0.
                     T m[KH];
+                    T v[KH][KW];
 #pragma unroll
                     for (int kh = 0; kh < KH; ++kh)
                     {
-                        T v[KW];
 #pragma unroll
-                        for (int kw = 0; kw < KW; ++kw) v[kw] = Tr::combine(wnd[r + KH - 1 - kh][kw], wp[kh * KW + kw]);
+                        for (int kw = 0; kw < KW; ++kw) v[kh][kw] = Tr::combine(wnd[r + KH - 1 - kh][kw], wp[kh * KW + kw]);
                         // A linear chain, which the compiler folds into max3 / min3 pairs.
-                        T mm = v[0];
+                        T mm = v[kh][0];
 #pragma unroll
-                        for (int kw = 1; kw < KW; ++kw) mm = Tr::pick(mm, v[kw]);
+                        for (int kw = 1; kw < KW; ++kw) mm = Tr::pick(mm, v[kh][kw]);
                         m[kh] = mm;
                     }
                     T best = Tr::init();
 #pragma unroll
                     for (int kh = 0; kh < KH; ++kh) best = Tr::pick(best, m[kh]);
-                    int krow = 0;
+                    int krow = 0, kcol = 0;
+                    if constexpr (SELECT)
+                    {
+                        // The first row holding the extremum, and its tap values, selected from
+                        // registers (the last row stands when none holds it: then best is the start
+                        // value and the tap is 0 below).
+                        krow = KH - 1;
+                        T rv[KW];
 #pragma unroll
-                    for (int kh = KH - 1; kh >= 0; --kh) krow = m[kh] == best ? kh : krow;
-                    const T* xrow = tb + (r + KH - 1 - krow) * COLS;
-                    const T* wrow = wp + krow * KW;
-                    int kcol = 0;
+                        for (int kw = 0; kw < KW; ++kw) rv[kw] = v[KH - 1][kw];
 #pragma unroll
-                    for (int kw = KW - 1; kw >= 0; --kw) kcol = Tr::combine(xrow[-kw], wrow[kw]) == best ? kw : kcol;
+                        for (int kh = KH - 2; kh >= 0; --kh)
+                        {
+                            const bool eq = m[kh] == best;
+                            krow = eq ? kh : krow;
+#pragma unroll
+                            for (int kw = 0; kw < KW; ++kw) rv[kw] = eq ? v[kh][kw] : rv[kw];
+                        }
+#pragma unroll
+                        for (int kw = KW - 1; kw >= 0; --kw) kcol = rv[kw] == best ? kw : kcol;
+                    }
+                    else
+                    {
+#pragma unroll
+                        for (int kh = KH - 1; kh >= 0; --kh) krow = m[kh] == best ? kh : krow;
+                        const T* xrow = tb + (r + KH - 1 - krow) * COLS;
+                        const T* wrow = wp + krow * KW;
+#pragma unroll
+                        for (int kw = KW - 1; kw >= 0; --kw) kcol = Tr::combine(xrow[-kw], wrow[kw]) == best ? kw : kcol;
+                    }
                     arg[ob][r] = best == Tr::init() ? 0 : krow * KW + kcol;
                     merge_pair<T, MK>(best, i, acc[ob][r], win[ob][r]);
                     if constexpr (!DEFER) store_tap(ob, r, arg[ob][r]);
