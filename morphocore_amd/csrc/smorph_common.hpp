@@ -142,6 +142,14 @@ __device__ __forceinline__ T horner_half(T r)
 //    2^(n + 1) with no add; the halved polynomial compensates, and (p / 2) 2^(n + 1) is the same
 //    exact product as p 2^n, rounded once. n + bias + 1 stays in [2, bias + 1] for n in
 //    [log2(min normal), 0].
+// exp_ref of an argument scaled by alpha = 0, which can only be +-0, -inf or NaN ((v - ref) * 0, less
+// a masked tap's +inf): exactly what exp_ref returns for those (1, 0 and NaN), in three instructions.
+template <typename T>
+__device__ __forceinline__ T exp_ref_zero_alpha(T x, T lo)
+{
+    return x < lo ? T(0) : x + T(1);
+}
+
 template <typename T>
 __device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
 {
@@ -156,6 +164,12 @@ __device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
     const T scale = __builtin_bit_cast(T, (Bits)((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant));
     const T e = ph * scale;
     return under ? T(0) : e;
+}
+
+// Whether a wave-uniform alpha is zero (+0 or -0), as a scalar condition (a branch, not a mask).
+__device__ __forceinline__ bool alpha_is_zero(float a)
+{
+    return (__builtin_amdgcn_readfirstlane(__builtin_bit_cast(unsigned, a)) & 0x7fffffffu) == 0u;
 }
 
 template <typename T>

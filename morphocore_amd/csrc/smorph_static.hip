@@ -116,7 +116,8 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
 // ------------------------------------------------------------------------------------------------
 
 // Pass 2 of a pair: S and W in tap order (kh, then kw), W fused as in the reference's AVX2 build.
-template <int KH, int KW, bool MASKED>
+// ZA: the pair's alpha is zero (every e is 1 on an in-image tap of finite v).
+template <int KH, int KW, bool MASKED, bool ZA>
 __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, float a, float ref, const TapMask<KH, KW>& tm, float& S, float& Wsum)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
@@ -135,7 +136,8 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
             // An out-of-image tap adds e = 0 (its staged x is 0, so v and the argument are finite, and
             // the argument less +inf is -inf): S + 0 and fma(0, v, W) leave both sums exactly as
             // skipping it does.
-            const float e = exp_ref(MASKED ? (v - ref) * a - tm.pen[kw] : (v - ref) * a, lo);
+            const float arg = MASKED ? (v - ref) * a - tm.pen[kw] : (v - ref) * a;
+            const float e = ZA ? exp_ref_zero_alpha(arg, lo) : exp_ref(arg, lo);
             s = s + e;  // unfused, as in the reference (e is rounded before the sum)
             wsum = fmaf(e, v, wsum);
         }
@@ -232,16 +234,23 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         const float* w = wl[buf];
         const float a = w[K];
         const bool dil = a >= 0.0f;
+        const bool za = alpha_is_zero(a);
         float ref, S, Wsum;
         if (interior)
         {
             ref = smorph_ref<KH, KW, false>(xb, w, dil, tm);
-            smorph_sums<KH, KW, false>(xb, w, a, ref, tm, S, Wsum);
+            if (za)
+                smorph_sums<KH, KW, false, true>(xb, w, a, ref, tm, S, Wsum);
+            else
+                smorph_sums<KH, KW, false, false>(xb, w, a, ref, tm, S, Wsum);
         }
         else
         {
             ref = smorph_ref<KH, KW, true>(xb, w, dil, tm);
-            smorph_sums<KH, KW, true>(xb, w, a, ref, tm, S, Wsum);
+            if (za)
+                smorph_sums<KH, KW, true, true>(xb, w, a, ref, tm, S, Wsum);
+            else
+                smorph_sums<KH, KW, true, false>(xb, w, a, ref, tm, S, Wsum);
         }
         const float inv = 1.0f / S;
         if constexpr (STATS)
@@ -664,7 +673,7 @@ struct RoutePixel
     bool in;
 };
 
-template <int MK, int KH, int KW, bool MASKED>
+template <int MK, int KH, int KW, bool MASKED, bool ZA>
 __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* wl, float a, const RoutePixel& A, const RoutePixel& B,
                                                   unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, Acc* btail,
                                                   const int (&hcell)[HaloRows<KH + 1, KW>::regs], Acc* gtile)
@@ -688,7 +697,8 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     for (int r = 0; r < HREGS; ++r) halo[r] = 0.0f;
     auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
         const float vk = x + wl[k];
-        const float ek = exp_ref(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
+        const float arg = MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a;
+        const float ek = ZA ? exp_ref_zero_alpha(arg, lo) : exp_ref(arg, lo);
         const float pg = ek * P.scaled;
         const float centered = vk - P.outc;
         float c = fmaf(a * pg, centered, pg);
@@ -911,10 +921,13 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             const float* w = wl[buf];
             const float a = w[K];
             float asum;
+            const bool za = alpha_is_zero(a);
             if (interior)
-                asum = smorph_bwd_pair2<MK, KH, KW, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
+                asum = za ? smorph_bwd_pair2<MK, KH, KW, false, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
+                          : smorph_bwd_pair2<MK, KH, KW, false, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             else
-                asum = smorph_bwd_pair2<MK, KH, KW, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
+                asum = za ? smorph_bwd_pair2<MK, KH, KW, true, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
+                          : smorph_bwd_pair2<MK, KH, KW, true, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             if constexpr (!PACK) lds_add(&bl[K * NC], (Acc)asum);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();

@@ -355,14 +355,16 @@ def test_smorph_static_interior_and_border_tiles(K, H, merge, a, saved, monkeypa
         assert normwise_error(actual, expected) <= 1e-6
 
 
+@pytest.mark.parametrize("alphas", ["mixed", "zero"], ids=["alpha-2-3", "alpha-0-3"])
 @pytest.mark.parametrize("saved", [True, False], ids=["saved-stats", "recomputed"])
 @pytest.mark.parametrize("merge", ["sum", "max", "identity"])
 @pytest.mark.parametrize("K", [3, 7])
-def test_smorph_static_nan_input(K, merge, saved, monkeypatch):
+def test_smorph_static_nan_input(K, merge, saved, alphas, monkeypatch):
     """An in-image NaN in the input propagates through the float32 static smorph kernels as through
     the reference (its window's pair outputs, and the gradients they route, are NaN; NaN never wins
     the window's extremum, nor the MAX merge), on interior and border tiles; every finite value
-    within tolerance."""
+    within tolerance. The "zero" case gives every other pair alpha = 0, whose exponentials the
+    kernels take without evaluating the exponential."""
     monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", str(1 << 40) if saved else "0")
     B, Cin, Cout, H, W = 1, 2, 3, 20, 200
     if merge == "identity":
@@ -372,7 +374,8 @@ def test_smorph_static_nan_input(K, merge, saved, monkeypatch):
     x[0, 1, 0, 3] = float("nan")  # a border tile, next to the image corner
     w = seeded(52, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
     pairs = Cout if merge == "identity" else Cout * Cin
-    alpha = torch.where(torch.arange(pairs) % 2 == 0, 2.0, -3.0).reshape((Cout,) if merge == "identity" else (Cout, Cin))
+    alpha = torch.where(torch.arange(pairs) % 2 == 0, 2.0 if alphas == "mixed" else 0.0, -3.0)
+    alpha = alpha.reshape((Cout,) if merge == "identity" else (Cout, Cin))
     g = seeded(53, B, Cout, H, W, kind="randn")
     results = _smorph_case(merge, x, w, alpha, g)
     # The oracle's output holds NaN, except under MAX, whose merge never picks a NaN channel.
