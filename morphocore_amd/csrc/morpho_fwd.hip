@@ -435,7 +435,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<T> p)
             // Up to 5x5 the first row holding the extremum and its values are selected from the
             // registers that computed them; larger elements read that row again from LDS (a
             // per-lane row: bank conflicts between lanes on different rows).
-            constexpr bool SELECT = K <= 25 && sizeof(T) == 4;
+            constexpr bool SELECT = K <= (sizeof(T) == 4 ? 25 : 9);
             using AT = std::conditional_t<(K <= 256), uint8_t, uint16_t>;
             const int hw = h0 + __builtin_amdgcn_readfirstlane(wave) * RH;  // the wave's first row
             auto store_tap = [&](int ob, int r, int a) {
