@@ -1,18 +1,22 @@
 """Benchmark of the morphocore_amd hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu-baseline]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu-baseline] [--no-extra]
 
 K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
 millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
 
 A step is one forward + backward pass of the configuration's operator(s) over one batch of synthetic,
-seeded input already resident in HBM (default configs[1], "C2"). The timed
-region is exactly K steps between device synchronisations. Prints one JSON line with the whole-job
-throughput in output elements per second, the roofline of the config's dominant kernel (launched
-through the C ABI after the timed region and timed with HIP events on torch's current stream, the
-stream it runs on; HBM traffic from the committed rocprofv3 counter summary) and the CPU baseline
-(the reference's own CPU extension, or the C oracle, on a bounded sample on the host cores, in a
-child process).
+seeded input already resident in HBM. The default is configs[4], the
+3-layer 8x64x512x512 11x11 stack: BASELINE.json's metric names no configuration, and this is the
+largest one that fits one GPU. After it, the default run also times configs[2] (the smorph alpha
+sweep the north star's target is stated on) and reports it under "configs2_step" (--no-extra
+skips it). The timed region is exactly K steps between device synchronisations.
+
+Prints one JSON line with the whole-job throughput in output elements per second, the roofline of
+the config's dominant kernel (launched through the C ABI after the timed region and timed with HIP
+events on torch's current stream, the stream it runs on; HBM traffic and VALU instruction counts
+from the committed rocprofv3 counter summaries) and the CPU baseline (the reference's own CPU
+extension, or the C oracle, on a bounded sample on the host cores, in a child process).
 
 --kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
 rocprofv3 counter runs.
@@ -57,8 +61,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None, help="timed steps (default: per config, DEFAULT_STEPS)")
     p.add_argument("--warmup", type=int, default=None, help="untimed warmup steps (default: per config, DEFAULT_STEPS)")
-    p.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    p.add_argument("--config", type=int, default=5, choices=sorted(CONFIGS))
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true", help="do not also time configs[2] after the default configs[4]")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernel-only", action="store_true",
                    help="launch only the config's dominant kernel --steps times (for rocprofv3 counter runs)")
@@ -99,7 +104,7 @@ def make_inputs(cfg, torch, dev):
 
 
 def build_step(cfg, torch, mca, x, ws, dtype, dev):
-    """Returns step() -> (fwd_event_pair, bwd_event_pair) and the output elements per step."""
+    """Returns step(events=None), the output elements per step and the number of phases per step."""
     F = mca.functional
     xr = x.requires_grad_(True)
     wr = [w.requires_grad_(True) for w in ws]
@@ -108,16 +113,18 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
     gen = torch.Generator(device=dev).manual_seed(1)
     grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
 
+    # A step is a list of (forward, backward) phases: one per alpha of the smorph sweep (each alpha's
+    # backward runs before the next alpha's forward, so one alpha's saved state is live at a time),
+    # one for the other configs.
     if cfg["kind"] == "smorph":
         alphas = [torch.full((Cout, Cin), a, dtype=dtype, device=dev, requires_grad=True) for a in cfg["alphas"]]
 
-        def fwd():
-            return [F.smorph(xr, wr[0], a, channel_merge_mode=cfg["merge"]) for a in alphas]
+        def phase(a):
+            return (lambda: [F.smorph(xr, wr[0], a, channel_merge_mode=cfg["merge"])]), (lambda outs: torch.autograd.backward(outs, [grad]))
 
-        def bwd(outs):
-            torch.autograd.backward(outs, [grad] * len(outs))
-
+        phases = [phase(a) for a in alphas]
         n_out = B * Cout * H * W * len(alphas)
+        params = [xr] + wr + alphas
     elif cfg["kind"] == "stack":
         alpha = torch.full((Cout, Cin), 5.0, dtype=dtype, device=dev, requires_grad=True)
 
@@ -126,36 +133,32 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
             y = F.smorph(y, wr[1], alpha, channel_merge_mode="sum")
             return [F.erosion(y, wr[2], "min", "replicate")]
 
-        def bwd(outs):
-            torch.autograd.backward(outs, [grad])
-
+        phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
         n_out = 3 * B * Cout * H * W
+        params = [xr] + wr + [alpha]
     else:
         op = F.dilation if cfg["op"] == "dilation" else F.erosion
-
-        def fwd():
-            return [op(xr, wr[0], cfg["merge"], "replicate")]
-
-        def bwd(outs):
-            torch.autograd.backward(outs, [grad])
-
+        phases = [(lambda: [op(xr, wr[0], cfg["merge"], "replicate")]), (lambda outs: torch.autograd.backward(outs, [grad]))]
+        phases = [tuple(phases)]
         n_out = B * Cout * H * W
-
-    params = [xr] + wr
+        params = [xr] + wr
 
     def step(events=None):
+        """One step; `events` (3 HIP events per phase) brackets each phase's forward and backward."""
         for p in params:
             p.grad = None
-        if events is not None:
-            events[0].record()
-        outs = fwd()
-        if events is not None:
-            events[1].record()
-        bwd(outs)
-        if events is not None:
-            events[2].record()
+        for k, (fwd, bwd) in enumerate(phases):
+            if events is not None:
+                events[3 * k].record()
+            outs = fwd()
+            if events is not None:
+                events[3 * k + 1].record()
+            bwd(outs)
+            del outs
+            if events is not None:
+                events[3 * k + 2].record()
 
-    return step, n_out
+    return step, n_out, len(phases)
 
 
 MERGE_CODE = {"max": 0, "min": 1, "sum": 2, "mean": 3, "identity": 5}
@@ -264,17 +267,53 @@ def time_launches(torch, launch, target_s=1.0, max_n=50):
     return e0.elapsed_time(e1) / n, n
 
 
-def measured_traffic(config):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy), or None."""
+def profile_record(config):
+    """The committed rocprofv3 counter record of a config's dominant kernel (profiles/traffic.json),
+    or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        rec = json.load(f).get(f"configs[{config - 1}]")
+        return json.load(f).get(f"configs[{config - 1}]")
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy), or None."""
+    rec = profile_record(config)
     if not rec:
         return None
     return (rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"]) * 1024.0
+
+
+def instruction_ceiling(config, cfg, roof, dwork):
+    """The VALU instruction ceiling of a VALU-bound dominant kernel: the rate its algorithmic flop
+    would reach if every SIMD issued one of the kernel's own wave64 VALU instructions every 2 cycles
+    (the full FP32 issue rate the 157.3 TFLOP/s peak assumes, at its 2.4 GHz), from the committed
+    SQ_INSTS_VALU count per launch: peak * flop per tap / (2 * VALU lane-instructions per tap).
+    `ceiling_frac` = achieved / ceiling says how close the kernel issues to that rate."""
+    rec = profile_record(config)
+    if not rec or "valu_insts" not in rec or roof["bound"] != "valu":
+        return None
+    t = taps(cfg)
+    per_tap = rec["valu_insts"] * 64.0 / t
+    ceiling = roof["peak"] * (dwork / t) / (2.0 * per_tap)
+    return {"ceiling": ceiling, "unit": "TFLOP/s", "valu_insts_per_tap": per_tap, "ceiling_frac": roof["achieved"] / ceiling,
+            "source": rec.get("profile")}
+
+
+def host_cpu():
+    """nproc, the cores this process may run on, and the CPU model of the host."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "cpu_model": model}
 
 
 def cpu_baseline(cfg, seconds):
@@ -293,8 +332,42 @@ def cpu_baseline(cfg, seconds):
     desc = f"x {tuple(sx)}, w {tuple(cfg['w'])}, fwd+bwd, {res['steps']} steps after one warm-up"
     if cfg["kind"] == "smorph":
         desc += ", alpha = 1 (one point of the sweep)"
-    return {"value": res["output_elements"] / res["seconds_per_step"], "unit": "output-elements/s", "cores": res["threads"],
-            "kind": res["kind"], "sample": desc}
+    out = {"value": res["output_elements"] / res["seconds_per_step"], "unit": "output-elements/s", "cores": res["threads"],
+           "kind": res["kind"], "sample": desc}
+    out.update(host_cpu())
+    return out
+
+
+def run_steps(cfg, torch, mca, dev, steps, warmup):
+    """Builds a config's inputs, runs `warmup` untimed steps, then times exactly `steps` steps between
+    device synchronisations. Returns the timing and the step's state (inputs)."""
+    x, ws, dtype = make_inputs(cfg, torch, dev)
+    step, n_out, nphase = build_step(cfg, torch, mca, x, ws, dtype, dev)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3 * nphase)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(events[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = sum(e[3 * p].elapsed_time(e[3 * p + 1]) for e in events for p in range(nphase)) / steps
+    bwd_ms = sum(e[3 * p + 1].elapsed_time(e[3 * p + 2]) for e in events for p in range(nphase)) / steps
+    ms_per_step = wall * 1000.0 / steps
+    return dict(ms_per_step=ms_per_step, fwd_ms=fwd_ms, bwd_ms=bwd_ms, n_out=n_out, x=x, ws=ws, dtype=dtype)
+
+
+def step_roofline(cfg, ms_per_step, peak):
+    """The whole step's algorithmic work (step_work) over the step time, against the same peak."""
+    sw = step_work(cfg)
+    if sw is None:
+        return None
+    rate = sw[0] / (ms_per_step * 1e-3)
+    if sw[1] == "bytes":
+        return {"bound": "hbm", "achieved": rate / 1e9, "unit": "GB/s", "frac": rate / 1e9 / PEAK_HBM_GBS, "work_per_step": sw[0]}
+    return {"bound": "valu", "achieved": rate / 1e12, "unit": "TFLOP/s", "frac": rate / 1e12 / peak, "work_per_step": sw[0]}
 
 
 def main():
@@ -320,34 +393,22 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_launch": n * 4, "launches": args.steps}), flush=True)
         return
-    x, ws, dtype = make_inputs(cfg, torch, dev)
     if args.kernel_only:
+        x, ws, dtype = make_inputs(cfg, torch, dev)
         launch, _, _, what = dominant(cfg, torch, _native, x, ws, dtype, dev)
         for _ in range(args.steps):
             launch()
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": what, "launches": args.steps}), flush=True)
         return
-    step, n_out = build_step(cfg, torch, mca, x, ws, dtype, dev)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(events[k])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
-    ms_per_step = wall * 1000.0 / args.steps
+    r = run_steps(cfg, torch, mca, dev, args.steps, args.warmup)
+    ms_per_step = r["ms_per_step"]
 
     # Roofline of the dominant kernel, timed after the step loop (outside the timed region).
-    launch, dwork, dunit, what = dominant(cfg, torch, _native, x.detach(), [w.detach() for w in ws], dtype, dev)
+    x, ws, dtype = r["x"].detach(), [w.detach() for w in r["ws"]], r["dtype"]
+    launch, dwork, dunit, what = dominant(cfg, torch, _native, x, ws, dtype, dev)
     kms, kn = time_launches(torch, launch)
+    del launch
     if dunit == "bytes":
         achieved = dwork / (kms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS}
@@ -357,35 +418,43 @@ def main():
         roof = {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak}
     roof["traffic"] = measured_traffic(args.config)
     roof.update({"kernel": what, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": dwork, "work_unit": dunit})
-    # The whole step against the same peak (the fwd+bwd figure the configs' targets are stated on).
-    sw = step_work(cfg)
-    step_roof = None
-    if sw is not None:
-        rate = sw[0] / (ms_per_step * 1e-3)
-        if sw[1] == "bytes":
-            step_roof = {"bound": "hbm", "achieved": rate / 1e9, "unit": "GB/s", "frac": rate / 1e9 / PEAK_HBM_GBS, "work_per_step": sw[0]}
-        else:
-            step_roof = {"bound": "valu", "achieved": rate / 1e12, "unit": "TFLOP/s", "frac": rate / 1e12 / roof["peak"], "work_per_step": sw[0]}
+    ceiling = instruction_ceiling(args.config, cfg, roof, dwork)
+    if ceiling is not None:
+        roof["instruction_ceiling"] = ceiling
+        roof["ceiling_frac"] = ceiling["ceiling_frac"]
     line = {
         "metric": METRIC,
-        "value": n_out / (ms_per_step * 1e-3),
+        "value": r["n_out"] / (ms_per_step * 1e-3),
         "unit": "output-elements/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_per_step,
-        "fwd_ms": fwd_ms,
-        "bwd_ms": bwd_ms,
+        "fwd_ms": r["fwd_ms"],
+        "bwd_ms": r["bwd_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f64" if cfg["dtype"] == "f64" else "f32",
         "data": "synthetic (seeded torch generators), inputs resident in HBM",
-        "config": {"workload": f"configs[{args.config - 1}]: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]), "parallelism": "none (1 GPU)"},
+        "config": {"workload": f"configs[{args.config - 1}]: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]),
+                   "parallelism": "none (1 GPU)"},
         "roofline": roof,
-        "step_roofline": step_roof,
+        "step_roofline": step_roofline(cfg, ms_per_step, roof.get("peak", PEAK_FP32_TFLOPS)),
         "cpu_baseline": None,
     }
+    del r, x, ws
+    if args.config == 5 and not args.no_extra:
+        # configs[2], the smorph alpha sweep the north star's >= 60% target is stated on.
+        torch.cuda.empty_cache()
+        c3 = CONFIGS[3]
+        s3, w3 = DEFAULT_STEPS[3]
+        r3 = run_steps(c3, torch, mca, dev, s3 - 1, w3)
+        line["configs2_step"] = {"workload": f"configs[2]: {c3['name']}", "steps": s3 - 1, "warmup": w3, "ms_per_step": r3["ms_per_step"],
+                                 "fwd_ms": r3["fwd_ms"], "bwd_ms": r3["bwd_ms"], "value": r3["n_out"] / (r3["ms_per_step"] * 1e-3),
+                                 "unit": "output-elements/s", "step_roofline": step_roofline(c3, r3["ms_per_step"], PEAK_FP32_TFLOPS)}
+        del r3
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(line), flush=True)

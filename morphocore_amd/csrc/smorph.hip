@@ -311,8 +311,9 @@ struct SmorphBwdPlan
     size_t lds;
 };
 
-// `saved`: the backward from saved statistics, whose static kernel takes two output rows per wave
-// (fewer tiles, so no more slots than the one-row plan, which sizes the workspace).
+// `saved`: the backward from saved statistics, whose static kernel takes two output rows per wave.
+// Its tiles are taller, but the rounding of tiles per strip can still give it more strips (slots)
+// than the one-row plan (4 x 64 x 100 x 100: 26 against 25), so the workspace is sized for both.
 template <typename T>
 static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = false)
 {
@@ -351,14 +352,24 @@ size_t smorph_lds(int merge, const Geom& g, bool backward)
     return (size_t)t.rows * t.pitch * sizeof(T);
 }
 
+// Workspace bytes of one backward plan: slot partials, MAX / MIN counts and target, reduction scratch.
 template <typename T>
-size_t smorph_backward_workspace(int merge, const Geom& g)
+static size_t smorph_plan_workspace(const SmorphBwdPlan& s, const Geom& g)
 {
-    const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g);
     const int nslots = g.B * s.nstrips;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes) +
            align_up(reduce_slots_scratch<T>(nslots, wnumel > s.npairs ? wnumel : s.npairs));
+}
+
+// Enough for either backward (recomputing or from saved statistics): the caller sizes the workspace
+// before it knows which one runs.
+template <typename T>
+size_t smorph_backward_workspace(int merge, const Geom& g)
+{
+    const size_t a = smorph_plan_workspace<T>(plan_smorph_bwd<T>(merge, g, false), g);
+    const size_t b = smorph_static_supported<T>(g) ? smorph_plan_workspace<T>(plan_smorph_bwd<T>(merge, g, true), g) : 0;
+    return a > b ? a : b;
 }
 
 template <typename T, int MK, bool STATS>
@@ -414,6 +425,8 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     if (stats && !smorph_static_supported<T>(g)) return hipErrorInvalidValue;
     const int64_t nstat = smorph_stats_count<T>(merge, g);
     const SmorphBwdPlan s = plan_smorph_bwd<T>(merge, g, stats != nullptr);
+    // The layout below is this plan's; never lay it out past the buffer.
+    if (workspace_bytes < smorph_plan_workspace<T>(s, g)) return hipErrorInvalidValue;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
     if ((int64_t)g.B * g.Cout * g.plane() == 0)

@@ -119,3 +119,32 @@ def test_smorph_stats_bytes_and_rejection():
     assert lib.mca_smorph_stats_bytes_f32(2, 0, Cin, Cout, Cw, H, W, 3, 3) == 0
     rc = lib.mca_smorph_forward_stats_f32(2, None, None, None, None, None, 0, Cin, Cout, Cw, H, W, 3, 3, None)
     assert rc == 0, lib.mca_last_error().decode()
+
+
+def _smorph_saved_plan_bytes(merge, B, Cin, Cout, H, W, K):
+    """Workspace bytes of the float32 smorph backward from saved statistics (two output rows per
+    wave: 64 x 8 tiles), for a square static element: slot partials of grad_weight and grad_alpha,
+    MAX / MIN counts and merge target, and the two-stage slot reduction's scratch."""
+    align = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    ntiles = -(-W // 64) * -(-H // 8)
+    nstrips = min(max(-(-8192 // (B * Cin)), 1), ntiles)
+    wnumel, npairs = Cout * Cin * K * K, Cout * Cin
+    while nstrips > 1 and B * nstrips * (wnumel + npairs) * 4 > (256 << 20):
+        nstrips = (nstrips + 1) // 2
+    tps = -(-ntiles // nstrips)
+    nslots = B * -(-ntiles // tps)
+    counts = 2 * B * Cout * H * W * 4 if merge in (0, 1) else 0
+    scratch = -(-nslots // 32) * max(wnumel, npairs) * 4 if nslots > 32 else 0
+    return align(nslots * wnumel * 4) + align(nslots * npairs * 4) + align(counts) + align(scratch)
+
+
+@pytest.mark.parametrize("merge", [0, 2, 3])
+@pytest.mark.parametrize("geom", [(4, 64, 100, 100, 3), (4, 64, 100, 100, 7), (2, 16, 300, 300, 5), (1, 8, 160, 200, 11)])
+def test_smorph_workspace_covers_the_saved_statistics_plan(merge, geom):
+    """The workspace size the caller allocates must also hold the layout of the backward from saved
+    statistics, whose rounding of tiles per strip can give more slots than the recomputing plan
+    (4 x 64 x 100 x 100: 26 strips against 25). Regression test of an out-of-bounds layout."""
+    B, C, H, W, K = geom
+    lib = _native.lib()
+    have = lib.mca_smorph_backward_workspace_size_f32(merge, B, C, C, C, H, W, K, K)
+    assert have >= _smorph_saved_plan_bytes(merge, B, C, C, H, W, K)
