@@ -89,6 +89,23 @@ int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const
                             double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of device scratch each GPU holds for mca_morpho_backward_noalloc_f32 (64 MiB). */
+#define MCA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* Dilation / erosion backward (float32) that allocates nothing: mca_morpho_backward_f32 without the
+ * workspace arguments. No counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under stream capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a file-scope device array of MCA_NOALLOC_SCRATCH_BYTES that each GPU holds from the
+ * first call on it until the process ends; a problem whose workspace
+ * (mca_morpho_backward_workspace_size_f32) exceeds it is rejected with MCA_ERR_INVALID. The stream
+ * must belong to the current device. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (other streams, other host threads) race and must be serialised by the caller.
+ * Outputs and argument meaning are those of mca_morpho_backward_f32. */
+int mca_morpho_backward_noalloc_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                                    int64_t weight_batch_stride, const void* indices, const float* grad_output, float* grad_input,
+                                    float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                    int64_t KH, int64_t KW, void* stream);
+
 /* Smorph forward. `weight` is the blended structuring element w~ the Python layer builds
  * (morphocore/functional/smorph.py:56-70); `alpha` holds one value per channel pair, index
  * o * Cin + i ([Cout] for IDENTITY), as smorph_pair_alphas expands it

@@ -25,6 +25,7 @@ EXPORTS = (
     "mca_morpho_backward_workspace_size_f64",
     "mca_morpho_backward_f32",
     "mca_morpho_backward_f64",
+    "mca_morpho_backward_noalloc_f32",
     "mca_smorph_forward_f32",
     "mca_smorph_forward_f64",
     "mca_smorph_backward_workspace_size_f32",
@@ -78,6 +79,8 @@ def lib() -> ctypes.CDLL:
         f = getattr(so, f"mca_smorph_backward_{sfx}")
         f.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
         f.restype = _I
+    so.mca_morpho_backward_noalloc_f32.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P]
+    so.mca_morpho_backward_noalloc_f32.restype = _I
     so.mca_smorph_stats_bytes_f32.argtypes = [_I] + _GEOM
     so.mca_smorph_stats_bytes_f32.restype = _SZ
     so.mca_smorph_forward_stats_f32.argtypes = [_I, _P, _P, _P, _P, _P] + _GEOM + [_P]
@@ -145,6 +148,17 @@ def morpho_backward(op, merge, replicate, fill, x, weight, weight_batch_stride, 
     f = getattr(so, f"mca_morpho_backward_{sfx}")
     _check(f(op, merge, int(replicate), fill, _ptr(x), _ptr(weight), weight_batch_stride, _ptr(indices), _ptr(grad_out), _ptr(grad_in),
              _ptr(grad_w), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+# Device scratch each GPU holds for the no-allocation backward (MCA_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def morpho_backward_noalloc(op, merge, replicate, fill, x, weight, weight_batch_stride, indices, grad_out, grad_in, grad_w, geom):
+    """Enqueue the float32 dilation / erosion backward that allocates nothing (C ABI
+    mca_morpho_backward_noalloc_f32): its workspace is the library's per-GPU device scratch."""
+    _check(lib().mca_morpho_backward_noalloc_f32(op, merge, int(replicate), fill, _ptr(x), _ptr(weight), weight_batch_stride,
+                                                 _ptr(indices), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w), *geom, _stream(x)))
 
 
 def smorph_stats_bytes(merge, dtype, geom) -> int:

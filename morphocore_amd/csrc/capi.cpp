@@ -3,9 +3,17 @@
 // include/morphocore_amd.h.
 #include "../../include/morphocore_amd.h"
 
+#include <mutex>
 #include <string>
 
 #include "launch.hpp"
+
+// Device scratch of mca_morpho_backward_noalloc_f32, the backward for callers that cannot allocate
+// device memory. Each GPU holds its own copy (MCA_NOALLOC_SCRATCH_BYTES) from the first call on it
+// until the process ends. In host code `scratch` only names the symbol: its device address on the
+// current GPU comes from hipGetSymbolAddress (noalloc_scratch below), and only that address is
+// handed to kernels and fills.
+static __device__ __align__(256) unsigned char scratch[MCA_NOALLOC_SCRATCH_BYTES];
 
 namespace
 {
@@ -155,6 +163,28 @@ int smorph_backward_impl(int merge, const T* input, const T* weight, const T* al
                                               workspace, workspace_bytes, (hipStream_t)stream, stats));
 }
 
+// Device address of `scratch` on `device` (which must be the current device), looked up once per
+// device and kept.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mutex;
+void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+
+int noalloc_scratch(int device, void** out)
+{
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail("Device index out of range for the no-allocation scratch");
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (!g_noalloc_ptr[device])
+    {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return hip_status(err);
+        if (!p) return fail("hipGetSymbolAddress returned a null address for the no-allocation scratch");
+        g_noalloc_ptr[device] = p;
+    }
+    *out = g_noalloc_ptr[device];
+    return MCA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -214,6 +244,36 @@ int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const
 {
     return morpho_backward_impl<double>(op, merge, replicate, fill, input, weight, weight_batch_stride, indices, grad_output, grad_input,
                                         grad_weight, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_backward_noalloc_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,
+                                    int64_t weight_batch_stride, const void* indices, const float* grad_output, float* grad_input,
+                                    float* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                    int64_t KH, int64_t KW, void* stream)
+{
+    mca::Geom g{};
+    if (op != mca::DILATION && op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(op));
+    int rc = make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, weight_batch_stride, g);
+    if (rc != MCA_OK) return rc;
+    if (mca::packed_winners(merge) && !(KH * KW < (1 << 16) && Cin < (1 << 15)))
+        return fail("Structuring element or channel count too large to save indices");
+    const size_t need = mca::morpho_backward_workspace<float>(merge, indices != nullptr, g);
+    if (need > (size_t)MCA_NOALLOC_SCRATCH_BYTES)
+        return fail("Problem too large for the no-allocation backward: it needs " + std::to_string(need) + " bytes of scratch, the limit is " +
+                    std::to_string((size_t)MCA_NOALLOC_SCRATCH_BYTES) + " (use mca_morpho_backward_f32 with a workspace)");
+    // The scratch belongs to the current device: the stream must run there.
+    int device = -1;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return hip_status(err);
+    hipDevice_t stream_device = device;
+    if ((err = hipStreamGetDevice((hipStream_t)stream, &stream_device)) != hipSuccess) return hip_status(err);
+    if ((int)stream_device != device)
+        return fail("The stream belongs to device " + std::to_string((int)stream_device) + " but device " + std::to_string(device) +
+                    " is current");
+    void* ptr = nullptr;
+    if ((rc = noalloc_scratch(device, &ptr)) != MCA_OK) return rc;
+    return morpho_backward_impl<float>(op, merge, replicate, fill, input, weight, weight_batch_stride, indices, grad_output, grad_input,
+                                       grad_weight, B, Cin, Cout, Cw, H, W, KH, KW, ptr, (size_t)MCA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int mca_smorph_forward_f32(int merge, const float* input, const float* weight, const float* alpha, float* output, int64_t B, int64_t Cin,

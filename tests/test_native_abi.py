@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 18
+    assert len(symbols) == 19
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -148,3 +148,16 @@ def test_smorph_workspace_covers_the_saved_statistics_plan(merge, geom):
     lib = _native.lib()
     have = lib.mca_smorph_backward_workspace_size_f32(merge, B, C, C, C, H, W, K, K)
     assert have >= _smorph_saved_plan_bytes(merge, B, C, C, H, W, K)
+
+
+def test_noalloc_backward_rejects_problems_beyond_its_scratch():
+    """The no-allocation backward refuses, before any device work, a problem whose workspace exceeds
+    the library's per-GPU scratch (here: configs[4]'s first layer without saved winners)."""
+    lib = _native.lib()
+    geom = (8, 64, 64, 64, 512, 512, 11, 11)
+    assert lib.mca_morpho_backward_workspace_size_f32(0, 0, *geom) > _native.NOALLOC_SCRATCH_BYTES
+    rc = lib.mca_morpho_backward_noalloc_f32(0, 0, 1, 0.0, None, None, 0, None, None, None, None, *geom, None)
+    assert rc == 1
+    assert "Problem too large for the no-allocation backward" in lib.mca_last_error().decode()
+    rc = lib.mca_morpho_backward_noalloc_f32(0, 9, 1, 0.0, None, None, 0, None, None, None, None, *GEOM, None)
+    assert rc == 1 and lib.mca_last_error().decode() == "Unknown merge mode 9"
