@@ -197,11 +197,11 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
     gen = torch.Generator(device=dev).manual_seed(2)
     grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
     gx, gw, ga = torch.empty_like(x), torch.empty_like(w), torch.empty_like(alpha)
-    # The step's own choice: the forward saves the pair statistics when the autograd layer would.
-    from morphocore_amd.functional._autograd import _save_smorph_stats
+    # The step's own choice: the forward saves the pair statistics when the operator would.
+    from morphocore_amd import _C
 
     nbytes = native.smorph_stats_bytes(merge, dtype, geom)
-    stats = torch.empty(nbytes // 4, dtype=torch.float32, device=dev) if _save_smorph_stats(nbytes, True, dev) else None
+    stats = torch.empty(nbytes // 4, dtype=torch.float32, device=dev) if _C.saved_stats_admit(nbytes, dev.index or 0) else None
     native.smorph_forward(merge, x, w, alpha, out, geom, stats=stats)
 
     def launch():

@@ -1,0 +1,637 @@
+// PyTorch-ROCm extension morphocore_amd._C: registers torch.ops.morphocore.{dilation, erosion, smorph,
+// smorph_scm} with the reference's schemas and dispatch key, and implements them as C++ autograd
+// Functions whose device work is the C ABI of libmorphocore_amd.so (include/morphocore_amd.h).
+//
+// This is the MI355X counterpart of the reference's host layer: bindings.cpp:15-156 (int checks,
+// registration, empty Python module), morpho_op_wrap.hxx:24-211 (MorphoOperation forward / backward:
+// rank handling, weight noise, the save-indices rule, saved state), smorph.cpp:20-111 and
+// smorph_scm.cpp:13-96 (Smorph / SmorphSCM forward / backward, alpha pairs, the shared-alpha gradient
+// sum), reshaper.cpp:3-151 (2-D / 3-D / 4-D ranks). Checks run in the reference's order with its
+// messages. Tensors on another device than a HIP GPU are refused: there is no CPU path.
+//
+// Two extensions of the reference's saved state, neither of which changes a result:
+//   * dilation / erosion with merge sum / mean / identity keep each channel pair's first extremal tap
+//     (one byte per pair and output pixel) up to MORPHOCORE_AMD_SAVED_TAPS_LIMIT bytes per call
+//     (default 8 GiB), so that the backward only routes;
+//   * float32 smorph with a 3x3 / 5x5 / 7x7 / 11x11 element keeps each pair's window extremum, 1 / S
+//     and W / S (12 bytes per pair and output pixel) under a budget shared by every live saved buffer
+//     of the process (SavedStats below), so that the backward need not recompute them.
+#include <Python.h>
+#include <torch/all.h>
+#include <torch/library.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPCachingAllocator.h>
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdlib>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/morphocore_amd.h"
+
+namespace
+{
+
+using torch::Tensor;
+using torch::autograd::AutogradContext;
+using torch::autograd::tensor_list;
+
+// Same integer values as the reference (morpho_op_enum.hpp:17-35, merge_enum.py:4-19).
+enum Op : int64_t
+{
+    DILATION = 0,
+    EROSION = 1
+};
+enum Merge : int64_t
+{
+    MAX = 0,
+    MIN = 1,
+    ADD = 2,
+    AVERAGE = 3,
+    SMOOTH = 4,
+    IDENTITY = 5
+};
+enum Padding : int64_t
+{
+    ZERO = 0,
+    GEODESIC = 1,
+    CONSTANT = 2,
+    REPLICATE = 3
+};
+
+// Max / min winners are saved only while the reference's CUDA grid could address every (batch,
+// output channel) pair (morpho_op_wrap.hxx:65-66).
+constexpr int64_t MAX_GRID_DIM = 65535;
+
+int64_t env_bytes(const char* name, int64_t fallback)
+{
+    const char* v = std::getenv(name);
+    if (!v || !*v) return fallback;
+    return std::strtoll(v, nullptr, 10);
+}
+
+// bindings.cpp:16-20.
+int64_t to_merge(int64_t merge)
+{
+    TORCH_CHECK(merge >= 0 && merge <= IDENTITY, "Unknown merge mode ", merge);
+    return merge;
+}
+
+// bindings.cpp:23-27.
+int64_t to_padding(int64_t padding)
+{
+    TORCH_CHECK(padding >= 0 && padding <= REPLICATE, "Unknown padding mode ", padding);
+    return padding;
+}
+
+// Border value of the fill paddings (morpho_padding_policy.hpp:22-33): ZERO 0, CONSTANT the value,
+// GEODESIC the identity element of the operation. REPLICATE reads the clamped edge pixel instead.
+double fill_value(int64_t op, int64_t padding, double padding_value)
+{
+    switch (padding)
+    {
+        case CONSTANT: return padding_value;
+        case GEODESIC: return op == DILATION ? -std::numeric_limits<double>::infinity() : std::numeric_limits<double>::infinity();
+        default: return 0.0;
+    }
+}
+
+// TensorInputDim::To4DTensor (reshaper.cpp:3-55): [H, W] and [C, H, W] gain leading unit axes.
+Tensor input_to_4d(const Tensor& t)
+{
+    const int64_t d = t.dim();
+    if (d == 4) return t;
+    if (d == 3) return t.unsqueeze(0);
+    if (d == 2) return t.unsqueeze(0).unsqueeze(0);
+    TORCH_CHECK(false, "Invalid input tensor: please give a 2D, 3D or 4D input tensor, received: ", d, " dimensions !");
+    return t;
+}
+
+// TensorInputDim::ToOriginalTensor (reshaper.cpp:57-81).
+Tensor output_to_original(const Tensor& out, int64_t input_dims)
+{
+    if (input_dims == 3) return out.squeeze(0);
+    if (input_dims == 2) return out.squeeze(0).squeeze(0);
+    return out;
+}
+
+// TensorWeightDim::To4DTensor (reshaper.cpp:84-130): a [KH, KW] weight is one channel pair.
+Tensor weight_to_4d(const Tensor& t)
+{
+    const int64_t d = t.dim();
+    if (d == 4) return t;
+    if (d == 2) return t.unsqueeze(0).unsqueeze(0);
+    TORCH_CHECK(false, "Invalid weight tensor dimensions: expected 2D, 3D, 4D or 5D tensor, received ", d, "D tensor");
+    return t;
+}
+
+void check_4d(const Tensor& x4, const Tensor& w4)
+{
+    TORCH_CHECK(x4.dim() == 4, "Input must be a 4d tensor (batch_size, in_channels, height, width)");
+    TORCH_CHECK(w4.dim() == 4, "Weight must be a 4d tensor (out_channels, in_channels, kernel_height, kernel_width)");
+}
+
+void check_identity(const Tensor& x4, const Tensor& w4, bool smorph)
+{
+    TORCH_CHECK(w4.size(0) == x4.size(1), "Identity mode requires weight.shape[0] == input.shape[1]");
+    if (smorph)
+    {
+        TORCH_CHECK(w4.size(1) == 1, "Identity mode requires weight.shape[1] == 1, got ", w4.size(1));
+    }
+    else
+    {
+        TORCH_CHECK(w4.size(1) == 1, "Identity mode requires weight.shape[1] == 1");
+    }
+}
+
+const char* scalar_name(c10::ScalarType t)
+{
+    switch (t)
+    {
+        case c10::kFloat: return "Float";
+        case c10::kDouble: return "Double";
+        case c10::kHalf: return "Half";
+        case c10::kBFloat16: return "BFloat16";
+        default: return c10::toString(t);
+    }
+}
+
+// The operators run only on a HIP device, in float32 or float64; everything else is an error, never
+// a fallback.
+void check_device(const char* name, const Tensor& x4, std::initializer_list<Tensor> others)
+{
+    TORCH_CHECK(x4.is_cuda(), "morphocore_amd: ", name, " runs on AMD GPUs (HIP devices); got an input on ", x4.device());
+    TORCH_CHECK(x4.scalar_type() == c10::kFloat || x4.scalar_type() == c10::kDouble, "\"", name, "\" not implemented for '",
+                scalar_name(x4.scalar_type()), "'");
+    for (const Tensor& t : others)
+    {
+        TORCH_CHECK(t.device() == x4.device(), "morphocore_amd: ", name, " expects every tensor on ", x4.device(), ", got one on ", t.device());
+        TORCH_CHECK(t.scalar_type() == x4.scalar_type(), "expected scalar type ", scalar_name(x4.scalar_type()), " but found ",
+                    scalar_name(t.scalar_type()));
+    }
+}
+
+void check_rc(int rc)
+{
+    TORCH_CHECK(rc == MCA_OK, mca_last_error());
+}
+
+// torch's current HIP stream of the tensor's device: the C ABI only enqueues work on it.
+void* stream_of(const Tensor& t) { return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+
+struct Geom
+{
+    int64_t B, Cin, Cout, Cw, H, W, KH, KW;
+};
+
+Geom geom_of(const Tensor& x4, const Tensor& w4)
+{
+    return Geom{x4.size(0), x4.size(1), w4.size(0), w4.size(1), x4.size(2), x4.size(3), w4.size(2), w4.size(3)};
+}
+
+Tensor byte_buffer(int64_t nbytes, const Tensor& like) { return torch::empty({nbytes > 0 ? nbytes : 1}, like.options().dtype(torch::kUInt8)); }
+
+// ------------------------------------------------------------------------------------------------
+// Saved smorph statistics: one budget for every live buffer of the process.
+// ------------------------------------------------------------------------------------------------
+
+// A buffer is admitted when the per-call cap allows it (MORPHOCORE_AMD_SAVED_STATS_LIMIT bytes; 0
+// disables saving), when the buffers still alive plus this one stay within the process budget
+// (MORPHOCORE_AMD_SAVED_STATS_BUDGET bytes, default 40% of the device's memory), and when it takes at
+// most half of the memory still available to torch (free plus cached but unused), which leaves the
+// other half to the activations of the layers that follow.
+bool stats_policy(int64_t nbytes, int64_t live, int64_t budget, int64_t avail, int64_t limit)
+{
+    if (nbytes <= 0) return false;
+    if (limit >= 0 && nbytes > limit) return false;
+    if (live + nbytes > budget) return false;
+    return nbytes <= avail / 2;
+}
+
+class SavedStats
+{
+public:
+    static SavedStats& get()
+    {
+        static SavedStats s;
+        return s;
+    }
+
+    // Bytes of saved-statistics buffers still alive on `device`.
+    int64_t live_bytes(c10::DeviceIndex device)
+    {
+        std::lock_guard<std::mutex> lock(m_);
+        return prune_and_sum(device);
+    }
+
+    bool admit(int64_t nbytes, c10::DeviceIndex device)
+    {
+        if (nbytes <= 0) return false;
+        size_t free_b = 0, total_b = 0;
+        {
+            const c10::DeviceGuard guard(c10::Device(c10::kCUDA, device));
+            if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
+        }
+        const auto stats = c10::hip::HIPCachingAllocator::getDeviceStats(device);
+        const int64_t agg = static_cast<int64_t>(c10::CachingAllocator::StatType::AGGREGATE);
+        const int64_t cached_unused = stats.reserved_bytes[agg].current - stats.allocated_bytes[agg].current;
+        const int64_t avail = static_cast<int64_t>(free_b) + (cached_unused > 0 ? cached_unused : 0);
+        const int64_t budget = env_bytes("MORPHOCORE_AMD_SAVED_STATS_BUDGET", static_cast<int64_t>(total_b) / 10 * 4);
+        const int64_t limit = env_bytes("MORPHOCORE_AMD_SAVED_STATS_LIMIT", -1);
+        std::lock_guard<std::mutex> lock(m_);
+        return stats_policy(nbytes, prune_and_sum(device), budget, avail, limit);
+    }
+
+    void track(const Tensor& t)
+    {
+        std::lock_guard<std::mutex> lock(m_);
+        live_.push_back(Entry{t.storage().getWeakStorageImpl(), static_cast<int64_t>(t.nbytes()), t.device().index()});
+    }
+
+private:
+    struct Entry
+    {
+        c10::weak_intrusive_ptr<c10::StorageImpl> storage;
+        int64_t nbytes;
+        c10::DeviceIndex device;
+    };
+
+    int64_t prune_and_sum(c10::DeviceIndex device)
+    {
+        int64_t sum = 0;
+        std::vector<Entry> keep;
+        keep.reserve(live_.size());
+        for (Entry& e : live_)
+        {
+            if (e.storage.expired()) continue;
+            if (e.device == device) sum += e.nbytes;
+            keep.push_back(std::move(e));
+        }
+        live_.swap(keep);
+        return sum;
+    }
+
+    std::mutex m_;
+    std::vector<Entry> live_;
+};
+
+// ------------------------------------------------------------------------------------------------
+// Dilation and erosion: MorphoOperation<op, merge, kind> (morpho_op_wrap.hxx:24-211).
+// ------------------------------------------------------------------------------------------------
+
+class MorphoFunction : public torch::autograd::Function<MorphoFunction>
+{
+public:
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, const Tensor& w4, int64_t op, int64_t merge, int64_t padding,
+                          double padding_value, bool save_indices, double noise_scale, bool needs_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const Tensor w = w4.contiguous();
+        const Geom g = geom_of(x, w);
+        // Weight noise: one structuring element per batch element, drawn on the weight's device from
+        // its generator as morpho_op_wrap.hxx:55-64 draws it.
+        Tensor sample_weight;
+        if (noise_scale > 0.0)
+        {
+            const Tensor noise = (torch::rand({g.B, g.Cout, g.Cw, g.KH, g.KW}, w.options()) * 2.0 - 1.0) * noise_scale;
+            sample_weight = (w.unsqueeze(0) + noise).contiguous();
+        }
+        const Tensor& kw = sample_weight.defined() ? sample_weight : w;
+        const int64_t wbs = sample_weight.defined() ? g.Cout * g.Cw * g.KH * g.KW : 0;
+        const int64_t nbytes = (int64_t)mca_morpho_indices_bytes((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+        bool save = save_indices && needs_grad;
+        if (save)
+            save = (merge == MAX || merge == MIN) ? g.Cout * g.B < MAX_GRID_DIM
+                                                  : nbytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30);
+        Tensor out = torch::empty({g.B, g.Cout, g.H, g.W}, x.options());
+        // Layout per mca_morpho_indices_bytes: packed int32 winners (max / min) or per-pair taps.
+        Tensor indices = save ? byte_buffer(nbytes, x) : Tensor();
+        const bool replicate = padding == REPLICATE;
+        const double fill = fill_value(op, padding, padding_value);
+        void* idx = indices.defined() ? indices.data_ptr() : nullptr;
+        if (x.scalar_type() == c10::kFloat)
+            check_rc(mca_morpho_forward_f32((int)op, (int)merge, replicate, (float)fill, x.data_ptr<float>(), kw.data_ptr<float>(), wbs,
+                                            out.data_ptr<float>(), idx, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        else
+            check_rc(mca_morpho_forward_f64((int)op, (int)merge, replicate, fill, x.data_ptr<double>(), kw.data_ptr<double>(), wbs,
+                                            out.data_ptr<double>(), idx, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        ctx->save_for_backward({x, w, indices, sample_weight});
+        ctx->saved_data["op"] = op;
+        ctx->saved_data["merge"] = merge;
+        ctx->saved_data["padding"] = padding;
+        ctx->saved_data["padding_value"] = padding_value;
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor& x = saved[0];
+        const Tensor& w = saved[1];
+        const Tensor& indices = saved[2];
+        const Tensor& sample_weight = saved[3];
+        const int64_t op = ctx->saved_data["op"].toInt();
+        const int64_t merge = ctx->saved_data["merge"].toInt();
+        const int64_t padding = ctx->saved_data["padding"].toInt();
+        const double padding_value = ctx->saved_data["padding_value"].toDouble();
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        std::vector<int64_t> expected = x.sizes().vec();
+        expected[1] = w.size(0);
+        TORCH_CHECK(grad_output.sizes() == expected, "grad_output shape mismatch: expected [", expected, "] but got [", grad_output.sizes(),
+                    "]");
+        TORCH_CHECK(grad_output.device() == x.device(), "grad_output must be on the same device as input");
+        TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(x.device());
+        const Geom g = geom_of(x, w);
+        // The noisy weights chose the winning taps; the weight gradient keeps the shared weight's shape.
+        const Tensor& kw = sample_weight.defined() ? sample_weight : w;
+        const int64_t wbs = sample_weight.defined() ? g.Cout * g.Cw * g.KH * g.KW : 0;
+        Tensor grad_input = torch::empty_like(x);
+        Tensor grad_weight = torch::empty_like(w);
+        const bool replicate = padding == REPLICATE;
+        const double fill = fill_value(op, padding, padding_value);
+        const void* idx = indices.defined() ? indices.data_ptr() : nullptr;
+        const int has = idx != nullptr;
+        if (x.scalar_type() == c10::kFloat)
+        {
+            const size_t n = mca_morpho_backward_workspace_size_f32((int)merge, has, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc(mca_morpho_backward_f32((int)op, (int)merge, replicate, (float)fill, x.data_ptr<float>(), kw.data_ptr<float>(), wbs, idx,
+                                             grad_output.data_ptr<float>(), grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(), g.B,
+                                             g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        }
+        else
+        {
+            const size_t n = mca_morpho_backward_workspace_size_f64((int)merge, has, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc(mca_morpho_backward_f64((int)op, (int)merge, replicate, fill, x.data_ptr<double>(), kw.data_ptr<double>(), wbs, idx,
+                                             grad_output.data_ptr<double>(), grad_input.data_ptr<double>(), grad_weight.data_ptr<double>(),
+                                             g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(),
+                                             stream_of(x)));
+        }
+        return {grad_input, grad_weight, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// Body of the dilation / erosion operators: bindings.cpp:59-101, then MorphoOperation::forward's
+// checks (morpho_op_wrap.hxx:24-77).
+Tensor morpho_operation(int64_t op, const Tensor& input, const Tensor& weight, int64_t merge, int64_t padding, double padding_value,
+                        bool save_indices, double noise_scale)
+{
+    padding = to_padding(padding);
+    merge = to_merge(merge);
+    TORCH_CHECK(merge != SMOOTH, "Unsupported merge operation");
+    TORCH_CHECK(noise_scale >= 0.0, "noise_scale must be non negative");
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    const Tensor w4 = weight_to_4d(weight);
+    check_4d(x4, w4);
+    TORCH_CHECK(x4.size(1) == w4.size(1) || merge == IDENTITY, "Input channels must match weight input channels");
+    if (merge == IDENTITY) check_identity(x4, w4, false);
+    check_device(op == DILATION ? "morpho_dilation_forward_hip" : "morpho_erosion_forward_hip", x4, {w4});
+    const bool needs_grad = torch::GradMode::is_enabled() && (input.requires_grad() || weight.requires_grad());
+    const Tensor out = MorphoFunction::apply(x4, w4, op, merge, padding, padding_value, save_indices, noise_scale, needs_grad);
+    return output_to_original(out, input_dims);
+}
+
+Tensor morpho_dilation(const Tensor& input, const Tensor& weight, int64_t merge, int64_t padding, double padding_value, bool save_indices,
+                       double noise_scale)
+{
+    return morpho_operation(DILATION, input, weight, merge, padding, padding_value, save_indices, noise_scale);
+}
+
+Tensor morpho_erosion(const Tensor& input, const Tensor& weight, int64_t merge, int64_t padding, double padding_value, bool save_indices,
+                      double noise_scale)
+{
+    return morpho_operation(EROSION, input, weight, merge, padding, padding_value, save_indices, noise_scale);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Smorph: Smorph<merge> (smorph.cpp:20-111).
+// ------------------------------------------------------------------------------------------------
+
+// One alpha per channel pair, index o * Cin + i ([Cout] for IDENTITY), or one value shared by every
+// pair (smorph_cpu_kernels.hxx:642-649).
+Tensor pair_alphas(const Tensor& alpha, int64_t merge, int64_t Cin, int64_t Cout)
+{
+    const int64_t pairs = merge == IDENTITY ? Cout : Cout * Cin;
+    TORCH_CHECK(alpha.numel() == pairs || alpha.numel() == 1, "Alpha must have one value, or shape ",
+                merge == IDENTITY ? "[channels]" : "[out_channels, in_channels]");
+    return alpha.numel() == pairs ? alpha.contiguous().reshape({pairs}) : alpha.reshape({1}).expand({pairs}).contiguous();
+}
+
+// A single alpha shared by every pair receives the gradient of all of them (smorph.cpp:96-98).
+Tensor alpha_grad(const Tensor& alpha, const Tensor& grad_pairs)
+{
+    return alpha.numel() == grad_pairs.numel() ? grad_pairs.view_as(alpha) : grad_pairs.sum().view_as(alpha);
+}
+
+class SmorphFunction : public torch::autograd::Function<SmorphFunction>
+{
+public:
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, const Tensor& w4, const Tensor& alpha, int64_t merge, bool needs_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const Tensor w = w4.contiguous();
+        const Geom g = geom_of(x, w);
+        const Tensor ap = pair_alphas(alpha, merge, g.Cin, g.Cout);
+        Tensor out = torch::empty({g.B, g.Cout, g.H, g.W}, x.options());
+        Tensor stats;
+        if (x.scalar_type() == c10::kFloat)
+        {
+            const int64_t nbytes = needs_grad ? (int64_t)mca_smorph_stats_bytes_f32((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW) : 0;
+            if (nbytes > 0 && SavedStats::get().admit(nbytes, x.device().index()))
+            {
+                try
+                {
+                    stats = torch::empty({nbytes / 4}, x.options().dtype(torch::kFloat32));
+                    SavedStats::get().track(stats);
+                }
+                catch (const c10::OutOfMemoryError&)
+                {
+                    stats = Tensor();  // fragmented memory: the backward recomputes them
+                }
+            }
+            if (stats.defined())
+                check_rc(mca_smorph_forward_stats_f32((int)merge, x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(),
+                                                      out.data_ptr<float>(), stats.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH,
+                                                      g.KW, stream_of(x)));
+            else
+                check_rc(mca_smorph_forward_f32((int)merge, x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), out.data_ptr<float>(),
+                                                g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        }
+        else
+        {
+            check_rc(mca_smorph_forward_f64((int)merge, x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), out.data_ptr<double>(),
+                                            g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        }
+        // The backward reads the output: the merge target of MAX and MIN.
+        ctx->save_for_backward({out, alpha, x, w, stats});
+        ctx->saved_data["merge"] = merge;
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor& out = saved[0];
+        const Tensor& alpha = saved[1];
+        const Tensor& x = saved[2];
+        const Tensor& w = saved[3];
+        const Tensor& stats = saved[4];
+        const int64_t merge = ctx->saved_data["merge"].toInt();
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(x.device());
+        const Geom g = geom_of(x, w);
+        const Tensor ap = pair_alphas(alpha, merge, g.Cin, g.Cout);
+        Tensor grad_input = torch::empty_like(x);
+        Tensor grad_weight = torch::empty_like(w);
+        Tensor grad_pairs = torch::empty_like(ap);
+        if (x.scalar_type() == c10::kFloat)
+        {
+            const size_t n = mca_smorph_backward_workspace_size_f32((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            if (stats.defined())
+                check_rc(mca_smorph_backward_stats_f32((int)merge, x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(),
+                                                       out.data_ptr<float>(), stats.data_ptr<float>(), grad_output.data_ptr<float>(),
+                                                       grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(), grad_pairs.data_ptr<float>(),
+                                                       g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(),
+                                                       stream_of(x)));
+            else
+                check_rc(mca_smorph_backward_f32((int)merge, x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), out.data_ptr<float>(),
+                                                 grad_output.data_ptr<float>(), grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(),
+                                                 grad_pairs.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(),
+                                                 (size_t)ws.numel(), stream_of(x)));
+        }
+        else
+        {
+            const size_t n = mca_smorph_backward_workspace_size_f64((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc(mca_smorph_backward_f64((int)merge, x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), out.data_ptr<double>(),
+                                             grad_output.data_ptr<double>(), grad_input.data_ptr<double>(), grad_weight.data_ptr<double>(),
+                                             grad_pairs.data_ptr<double>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(),
+                                             (size_t)ws.numel(), stream_of(x)));
+        }
+        return {grad_input, grad_weight, alpha_grad(alpha, grad_pairs), Tensor(), Tensor()};
+    }
+};
+
+// Body of the smorph operator: bindings.cpp:109-120, then Smorph::forward's checks (smorph.cpp:20-47,
+// smorph_cpu_kernels.hxx:642-649).
+Tensor smorph(const Tensor& input, const Tensor& weight, const Tensor& alpha, int64_t merge)
+{
+    merge = to_merge(merge);
+    TORCH_CHECK(merge != SMOOTH, "Unsupported merge operation for smorph");
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    const Tensor w4 = weight_to_4d(weight);
+    check_4d(x4, w4);
+    if (merge == IDENTITY)
+    {
+        check_identity(x4, w4, true);
+    }
+    else
+    {
+        TORCH_CHECK(x4.size(1) == w4.size(1), "Input channels must match weight input channels");
+    }
+    pair_alphas(alpha, merge, x4.size(1), w4.size(0));
+    check_device("smorph_forward_hip", x4, {w4, alpha});
+    // Inside the Function's forward autograd is off: whether a backward can follow is decided here.
+    const bool needs_grad = torch::GradMode::is_enabled() && (input.requires_grad() || weight.requires_grad() || alpha.requires_grad());
+    return output_to_original(SmorphFunction::apply(x4, w4, alpha, merge, needs_grad), input_dims);
+}
+
+// Body of the smorph_scm operator, smorph with the SMOOTH channel merge: bindings.cpp:122-125, then
+// SmorphSCM::forward's checks (smorph_scm.cpp:13-34, smorph_cpu_kernels.hxx:642-649, 668-672).
+Tensor smorph_scm(const Tensor& input, const Tensor& weight, const Tensor& alpha, const Tensor& beta)
+{
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    const Tensor w4 = weight_to_4d(weight);
+    check_4d(x4, w4);
+    TORCH_CHECK(x4.size(1) == w4.size(1), "Input channels must match weight input channels");
+    pair_alphas(alpha, SMOOTH, x4.size(1), w4.size(0));
+    TORCH_CHECK(beta.numel() == w4.size(0), "Beta must have shape [out_channels]");
+    check_device("smorph_scm_forward_hip", x4, {w4, alpha, beta});
+    TORCH_CHECK(false, "morphocore_amd: smorph_scm kernels are not built in this library");
+    return output_to_original(x4, input_dims);
+}
+
+// Module-level helpers for tests and the benchmark (no reference counterpart).
+PyObject* py_saved_stats_live_bytes(PyObject*, PyObject* args)
+{
+    int device = 0;
+    if (!PyArg_ParseTuple(args, "i", &device)) return nullptr;
+    return PyLong_FromLongLong(SavedStats::get().live_bytes((c10::DeviceIndex)device));
+}
+
+PyObject* py_saved_stats_admit(PyObject*, PyObject* args)
+{
+    long long nbytes = 0;
+    int device = 0;
+    if (!PyArg_ParseTuple(args, "Li", &nbytes, &device)) return nullptr;
+    bool ok = false;
+    try
+    {
+        ok = SavedStats::get().admit(nbytes, (c10::DeviceIndex)device);
+    }
+    catch (const std::exception& e)
+    {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    return PyBool_FromLong(ok);
+}
+
+PyObject* py_saved_stats_policy(PyObject*, PyObject* args)
+{
+    long long nbytes = 0, live = 0, budget = 0, avail = 0, limit = -1;
+    if (!PyArg_ParseTuple(args, "LLLL|L", &nbytes, &live, &budget, &avail, &limit)) return nullptr;
+    return PyBool_FromLong(stats_policy(nbytes, live, budget, avail, limit));
+}
+
+PyMethodDef g_methods[] = {
+    {"saved_stats_live_bytes", py_saved_stats_live_bytes, METH_VARARGS,
+     "saved_stats_live_bytes(device) -> bytes of saved smorph statistics still alive on the device"},
+    {"saved_stats_admit", py_saved_stats_admit, METH_VARARGS,
+     "saved_stats_admit(nbytes, device) -> whether a smorph forward would save nbytes of statistics now"},
+    {"saved_stats_policy", py_saved_stats_policy, METH_VARARGS,
+     "saved_stats_policy(nbytes, live, budget, avail[, limit]) -> the admission rule on given numbers"},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+}  // namespace
+
+// Same namespace, names and schemas as the reference (bindings.cpp:130-138).
+TORCH_LIBRARY(morphocore, m)
+{
+    m.def("dilation(Tensor input, Tensor weight, int merge, int padding, float padding_value=0., bool save_indices=True, "
+          "float noise_scale=0.) -> Tensor");
+    m.def("erosion(Tensor input, Tensor weight, int merge, int padding, float padding_value=0., bool save_indices=True, "
+          "float noise_scale=0.) -> Tensor");
+    m.def("smorph(Tensor input, Tensor weight, Tensor alpha, int merge) -> Tensor");
+    m.def("smorph_scm(Tensor input, Tensor weight, Tensor alpha, Tensor beta) -> Tensor");
+}
+
+// CompositeImplicitAutograd, as the reference (bindings.cpp:142-148): the kernels run above autograd
+// and the autograd Functions above record the backward themselves.
+TORCH_LIBRARY_IMPL(morphocore, CompositeImplicitAutograd, m)
+{
+    m.impl("dilation", &morpho_dilation);
+    m.impl("erosion", &morpho_erosion);
+    m.impl("smorph", &smorph);
+    m.impl("smorph_scm", &smorph_scm);
+}
+
+// Importing morphocore_amd._C loads this library, which runs the registrations above.
+PyMODINIT_FUNC PyInit__C(void)
+{
+    static struct PyModuleDef module_def = {PyModuleDef_HEAD_INIT, "_C", "morphocore_amd operators (torch.ops.morphocore.*)", -1, g_methods};
+    return PyModule_Create(&module_def);
+}

@@ -23,8 +23,7 @@ DTYPES = [torch.float32, torch.float64]
 def _mca():
     import morphocore_amd
     from morphocore_amd import _native
-    from morphocore_amd.functional import _autograd
-    return morphocore_amd, _native, _autograd
+    return morphocore_amd, _native, None
 
 
 def _np(t):
@@ -37,7 +36,7 @@ def _weight_shape(merge, cin, cout, kh, kw):
 
 def kernel_forward(op, merge, padding, pv, x, w, save=False, sample_weight=None):
     """One call of the C ABI forward on the GPU (kernel-facing weight)."""
-    _, native, A = _mca()
+    _, native, _ = _mca()
     dev = torch.device("cuda")
     xd = x.to(dev).contiguous()
     wd = (w if sample_weight is None else sample_weight).to(dev).contiguous()
@@ -46,7 +45,7 @@ def kernel_forward(op, merge, padding, pv, x, w, save=False, sample_weight=None)
     out = torch.empty((B, Cout, H, W), dtype=x.dtype, device=dev)
     idx = torch.empty((B, Cout, H, W), dtype=torch.int32, device=dev) if save else None
     wbs = Cout * Cw * KH * KW if sample_weight is not None else 0
-    native.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding] == O.REPLICATE, A.fill_value(op, O.PADDINGS[padding], pv), xd, wd, wbs,
+    native.morpho_forward(op, O.MERGES[merge], O.PADDINGS[padding] == O.REPLICATE, O.fill_value(op, O.PADDINGS[padding], pv, x.numpy().dtype), xd, wd, wbs,
                           out, idx, (B, Cin, Cout, Cw, H, W, KH, KW))
     torch.cuda.synchronize()
     return _np(out), (None if idx is None else _np(idx))
@@ -386,30 +385,73 @@ def test_smorph_static_nan_input(K, merge, saved, alphas, monkeypatch):
 
 def test_smorph_saves_statistics_only_for_a_backward(monkeypatch):
     """The forward keeps the pair statistics only when a backward can follow (grad mode on and an
-    input that requires grad), within the memory limit; the results do not depend on it."""
+    input that requires grad), within the per-call cap; they live as long as the autograd graph that
+    holds them; the results do not depend on them."""
     mca, native, _ = _mca()
+    from morphocore_amd import _C
+
     dev = torch.device("cuda")
-    seen = []
-    real = native.smorph_forward
-
-    def spy(*args, stats=None, **kw):
-        seen.append(stats is not None)
-        return real(*args, stats=stats, **kw)
-
-    monkeypatch.setattr(native, "smorph_forward", spy)
+    live = lambda: _C.saved_stats_live_bytes(torch.cuda.current_device())  # noqa: E731
+    base = live()
     x = seeded(61, 1, 2, 12, 70, kind="randn").to(dev)
     w = seeded(62, 3, 2, 3, 3, kind="randn", scale=0.1).to(dev)
     alpha = torch.full((3, 2), 2.0, device=dev)
+    nbytes = native.smorph_stats_bytes(2, torch.float32, (1, 2, 3, 2, 12, 70, 3, 3))
+    assert nbytes == 12 * 3 * 2 * 12 * 70
     with torch.no_grad():
         y0 = mca.functional.smorph(x, w, alpha, channel_merge_mode="sum")
+    assert live() == base
     y1 = mca.functional.smorph(x, w, alpha, channel_merge_mode="sum")  # nothing requires grad
+    assert live() == base
     xr = x.clone().requires_grad_(True)
     y2 = mca.functional.smorph(xr, w, alpha, channel_merge_mode="sum")
+    assert live() == base + nbytes
     monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", "0")
     y3 = mca.functional.smorph(xr, w, alpha, channel_merge_mode="sum")
-    assert seen == [False, False, True, False]
+    assert live() == base + nbytes
     for y in (y1, y2, y3):
         assert torch.equal(y, y0)
+    del y2
+    assert live() == base
+
+
+def test_smorph_stack_saved_statistics_budget(monkeypatch):
+    """One budget for every live saved-statistics buffer of the process: in a 3-layer smorph stack
+    whose budget holds two layers' statistics, the third layer's backward recomputes them, and the
+    outputs and gradients are those of a run that saves every layer's (within the tolerance: the two
+    backwards add the same terms in different orders)."""
+    mca, native, _ = _mca()
+    from morphocore_amd import _C
+
+    dev = torch.device("cuda")
+    live = lambda: _C.saved_stats_live_bytes(torch.cuda.current_device())  # noqa: E731
+    C, H, W, K = 4, 24, 70, 5
+    nbytes = native.smorph_stats_bytes(2, torch.float32, (2, C, C, C, H, W, K, K))
+    x = seeded(71, 2, C, H, W, kind="randn").to(dev)
+    ws = [seeded(72 + l, C, C, K, K, kind="randn", scale=0.1).to(dev) for l in range(3)]
+    alphas = [torch.full((C, C), a, device=dev) for a in (1.5, -2.0, 3.0)]
+    g = seeded(79, 2, C, H, W, kind="randn").to(dev)
+
+    def run():
+        xr = x.clone().requires_grad_(True)
+        wr = [w.clone().requires_grad_(True) for w in ws]
+        base = live()
+        y = xr
+        saved = []
+        for wl, al in zip(wr, alphas):
+            y = mca.functional.smorph(y, wl, al, channel_merge_mode="sum")
+            saved.append(live() - base)
+        y.backward(g)
+        return y.detach(), [xr.grad] + [wl.grad for wl in wr], saved
+
+    y_all, g_all, saved_all = run()
+    assert saved_all == [nbytes, 2 * nbytes, 3 * nbytes]
+    monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_BUDGET", str(live() + 2 * nbytes + nbytes // 2))
+    y_two, g_two, saved_two = run()
+    assert saved_two == [nbytes, 2 * nbytes, 2 * nbytes]
+    assert torch.equal(y_two, y_all)
+    for a, b in zip(g_two, g_all):
+        assert normwise_error(a.cpu().numpy(), b.cpu().numpy()) <= 1e-6
 
 
 def _window_extremum(x, w, dilation_like):
@@ -679,7 +721,7 @@ def test_smorph_large_grid_saved_matches_recomputed(merge, K, a, monkeypatch):
 def test_saved_pair_taps_are_first_extremal_taps(op, merge, dtype, shape):
     """The taps the forward saves for the per-pair merges are each pair's first extremal tap (the
     strict scan of morpho_op_cpu_kernels.hxx:211-252), on quantised inputs full of ties."""
-    _, native, A = _mca()
+    _, native, _ = _mca()
     B, Cin, Cout, H, W, KH, KW = shape
     if merge == "identity":
         Cout = Cin

@@ -66,8 +66,14 @@ def test_smorph_argument_errors():
         ops.smorph(x, torch.zeros(3, 3, 3, 3), torch.zeros(3), 5)
     with pytest.raises(RuntimeError, match="Unsupported merge operation for smorph"):
         ops.smorph(x, w, torch.zeros(4, 3), 4)
-    with pytest.raises(NotImplementedError, match="smorph_scm"):
+    # smorph with beta: the SMOOTH channel merge (smorph_scm), one beta per output channel
+    # (smorph_scm.cpp:33).
+    with pytest.raises(RuntimeError, match="Beta must have shape \\[out_channels\\]"):
         mca.functional.smorph(x, w, torch.zeros(4, 3), beta=torch.zeros(4, 3))
+    with pytest.raises(RuntimeError, match="Alpha must have one value, or shape \\[out_channels, in_channels\\]"):
+        ops.smorph_scm(x, w, torch.zeros(4), torch.zeros(4))
+    with pytest.raises(RuntimeError, match="runs on AMD GPUs"):
+        ops.smorph_scm(x, w, torch.zeros(4, 3), torch.zeros(4))
 
 
 def test_cpu_tensors_are_refused_not_computed():
@@ -92,3 +98,29 @@ def test_module_parameters():
     s2 = mca.nn.SMorph(3, 3, 3, channel_merge_mode="identity", init_beta=1.0)
     assert s2.alpha.shape == (3, 1) and s2.beta.shape == (3, 3)
     assert set(dict(d.named_parameters())) == {"weight"} and set(dict(s.named_parameters())) == {"weight", "alpha"}
+
+
+def test_saved_statistics_admission_rule():
+    """The rule the smorph forward applies before it keeps its pair statistics: within the per-call
+    cap, within the process budget together with every buffer still alive, and at most half of the
+    memory still available (so later layers keep room for their activations)."""
+    from morphocore_amd import _C
+
+    GB = 1 << 30
+    policy = _C.saved_stats_policy
+    assert policy(10 * GB, 0, 100 * GB, 200 * GB)
+    assert not policy(0, 0, 100 * GB, 200 * GB)  # nothing to save
+    assert not policy(10 * GB, 95 * GB, 100 * GB, 200 * GB)  # over the process budget
+    assert not policy(10 * GB, 0, 100 * GB, 19 * GB)  # more than half of what is available
+    assert not policy(10 * GB, 0, 100 * GB, 200 * GB, 5 * GB)  # over the per-call cap
+    assert not policy(1, 0, 100 * GB, 200 * GB, 0)  # cap 0 disables saving
+    # A 3-layer stack of 30 GB layers under a 80 GB budget: the third layer recomputes.
+    live, avail, admitted = 0, 250 * GB, []
+    for _ in range(3):
+        ok = policy(30 * GB, live, 80 * GB, avail)
+        admitted.append(ok)
+        if ok:
+            live += 30 * GB
+            avail -= 30 * GB
+        avail -= 10 * GB  # the layer's output
+    assert admitted == [True, True, False]
