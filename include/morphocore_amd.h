@@ -116,8 +116,10 @@ int mca_smorph_forward_f32(int merge, const float* input, const float* weight, c
 int mca_smorph_forward_f64(int merge, const double* input, const double* weight, const double* alpha, double* output, int64_t B,
                            int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
 
-/* Workspace bytes mca_smorph_backward_* needs. No reference counterpart (the reference allocates
- * inside smorph_backward_cuda, smorph.cu:63-103). */
+/* Workspace bytes mca_smorph_backward_* needs; 0 for an invalid geometry or a structuring element
+ * too large for the backward kernels' shared memory (a caller that trains can check this before the
+ * forward). No reference counterpart (the reference allocates inside smorph_backward_cuda,
+ * smorph.cu:63-103). */
 size_t mca_smorph_backward_workspace_size_f32(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
                                               int64_t KH, int64_t KW);
 size_t mca_smorph_backward_workspace_size_f64(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
@@ -152,6 +154,42 @@ int mca_smorph_backward_stats_f32(int merge, const float* input, const float* we
                                   const float* stats, const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha,
                                   int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Smorph with the SMOOTH channel merge (the smorph_scm operator, selected by a `beta` in
+ * morphocore/functional/smorph.py:72-73), float32 and float64, any structuring-element size.
+ * Replaces smorph_forward_cuda / smorph_backward_cuda with merge SMOOTH and a beta
+ * (morphocore/functional/csrc/cuda/smorph.cuh:15-25, smorph_kernels.cuh:247-298,512-523; the host
+ * side is smorph_scm.cpp:13-96). For every output channel o and pixel, the pair outputs c_i of the
+ * input channels (each as mca_smorph_forward computes it) are merged softly with beta[o]:
+ * ref = the extremum of the c_i (max for beta >= 0, min otherwise), q_i = exp(beta[o] (c_i - ref)),
+ * out = sum q_i c_i / sum q_i. alpha holds one value per pair (index o * Cin + i); Cw == Cin >= 1.
+ * `merge_stats` receives (forward) and provides (backward) 2 * B * Cout * H * W values: ref, then
+ * 1 / sum q_i, per output pixel; the forward may pass NULL when no backward follows. Both directions
+ * take a caller-owned workspace of the size the matching function returns (0: invalid geometry, or,
+ * for the backward, an element too large for the kernels' shared memory). The backward overwrites
+ * grad_input, grad_weight (of w~), grad_alpha (per pair) and grad_beta [Cout]. */
+size_t mca_smorph_scm_forward_workspace_size_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                 int64_t KW);
+size_t mca_smorph_scm_forward_workspace_size_f64(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                 int64_t KW);
+int mca_smorph_scm_forward_f32(const float* input, const float* weight, const float* alpha, const float* beta, float* output,
+                               float* merge_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                               int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_smorph_scm_forward_f64(const double* input, const double* weight, const double* alpha, const double* beta, double* output,
+                               double* merge_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                               int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+size_t mca_smorph_scm_backward_workspace_size_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                  int64_t KW);
+size_t mca_smorph_scm_backward_workspace_size_f64(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                  int64_t KW);
+int mca_smorph_scm_backward_f32(const float* input, const float* weight, const float* alpha, const float* beta, const float* output,
+                                const float* merge_stats, const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha,
+                                float* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_smorph_scm_backward_f64(const double* input, const double* weight, const double* alpha, const double* beta, const double* output,
+                                const double* merge_stats, const double* grad_output, double* grad_input, double* grad_weight,
+                                double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,14 @@ EXPORTS = (
     "mca_smorph_stats_bytes_f32",
     "mca_smorph_forward_stats_f32",
     "mca_smorph_backward_stats_f32",
+    "mca_smorph_scm_forward_workspace_size_f32",
+    "mca_smorph_scm_forward_workspace_size_f64",
+    "mca_smorph_scm_forward_f32",
+    "mca_smorph_scm_forward_f64",
+    "mca_smorph_scm_backward_workspace_size_f32",
+    "mca_smorph_scm_backward_workspace_size_f64",
+    "mca_smorph_scm_backward_f32",
+    "mca_smorph_scm_backward_f64",
 )
 
 _lib = None
@@ -78,6 +86,16 @@ def lib() -> ctypes.CDLL:
         f.restype = _SZ
         f = getattr(so, f"mca_smorph_backward_{sfx}")
         f.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+        for d in ("forward", "backward"):
+            f = getattr(so, f"mca_smorph_scm_{d}_workspace_size_{sfx}")
+            f.argtypes = list(_GEOM)
+            f.restype = _SZ
+        f = getattr(so, f"mca_smorph_scm_forward_{sfx}")
+        f.argtypes = [_P] * 6 + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+        f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
+        f.argtypes = [_P] * 11 + _GEOM + [_P, _SZ, _P]
         f.restype = _I
     so.mca_morpho_backward_noalloc_f32.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P]
     so.mca_morpho_backward_noalloc_f32.restype = _I
@@ -193,3 +211,21 @@ def smorph_backward(merge, x, weight, alpha_pairs, out, grad_out, grad_in, grad_
     f = getattr(so, f"mca_smorph_backward_{sfx}")
     _check(f(merge, _ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(out), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w), _ptr(grad_alpha),
              *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def smorph_scm_forward(x, weight, alpha_pairs, beta, out, merge_stats, geom):
+    """Enqueue smorph with the SMOOTH merge (C ABI mca_smorph_scm_forward_*), workspace from torch;
+    `merge_stats` (2 * B * Cout * H * W values, or None) receives the soft merge's ref and 1 / sum."""
+    so, sfx = lib(), _sfx(x)
+    ws = _workspace(getattr(so, f"mca_smorph_scm_forward_workspace_size_{sfx}")(*geom), x.device)
+    f = getattr(so, f"mca_smorph_scm_forward_{sfx}")
+    _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out, grad_in, grad_w, grad_alpha, grad_beta, geom):
+    """Enqueue the smorph_scm backward (C ABI mca_smorph_scm_backward_*), workspace from torch."""
+    so, sfx = lib(), _sfx(x)
+    ws = _workspace(getattr(so, f"mca_smorph_scm_backward_workspace_size_{sfx}")(*geom), x.device)
+    f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
+    _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w),
+             _ptr(grad_alpha), _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))

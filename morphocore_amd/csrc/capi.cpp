@@ -144,6 +144,7 @@ size_t smorph_workspace_impl(int merge, int64_t B, int64_t Cin, int64_t Cout, in
 {
     mca::Geom g{};
     if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    if (mca::smorph_lds<T>(merge, g, true) > mca::LDS_LIMIT) return 0;  // no backward for this element
     return mca::smorph_backward_workspace<T>(merge, g);
 }
 
@@ -161,6 +162,69 @@ int smorph_backward_impl(int merge, const T* input, const T* weight, const T* al
         return fail("Workspace too small: " + std::to_string(workspace_bytes) + " bytes given, " + std::to_string(need) + " needed");
     return hip_status(mca::smorph_backward<T>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, g,
                                               workspace, workspace_bytes, (hipStream_t)stream, stats));
+}
+
+// Geometry of the SMOOTH merge entry points: the checks of every smorph entry point with a per-pair
+// alpha (Cw == Cin), and at least one input channel to merge.
+int make_scm_geom(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, mca::Geom& g)
+{
+    const int rc = make_geom(mca::MERGE_ADD, B, Cin, Cout, Cw, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if (Cin < 1) return fail("smorph_scm needs at least one input channel");
+    return MCA_OK;
+}
+
+template <typename T>
+size_t scm_forward_workspace_impl(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g) != MCA_OK) return 0;
+    return mca::smorph_scm_forward_workspace<T>(g);
+}
+
+template <typename T>
+size_t scm_backward_workspace_impl(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g) != MCA_OK) return 0;
+    if (mca::smorph_scm_lds<T>(g, true) > mca::LDS_LIMIT) return 0;
+    return mca::smorph_scm_backward_workspace<T>(g);
+}
+
+int check_workspace(size_t given, size_t need, const void* workspace)
+{
+    if (given < need || (need > 0 && !workspace))
+        return fail("Workspace too small: " + std::to_string(given) + " bytes given, " + std::to_string(need) + " needed");
+    return MCA_OK;
+}
+
+template <typename T>
+int scm_forward_impl(const T* input, const T* weight, const T* alpha, const T* beta, T* output, T* merge_stats, int64_t B, int64_t Cin,
+                     int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes,
+                     void* stream)
+{
+    mca::Geom g{};
+    int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_lds(mca::smorph_scm_lds<T>(g, false))) != MCA_OK) return rc;
+    if ((rc = check_workspace(workspace_bytes, mca::smorph_scm_forward_workspace<T>(g), workspace)) != MCA_OK) return rc;
+    return hip_status(
+        mca::smorph_scm_forward<T>(input, weight, alpha, beta, output, merge_stats, g, workspace, workspace_bytes, (hipStream_t)stream));
+}
+
+template <typename T>
+int scm_backward_impl(const T* input, const T* weight, const T* alpha, const T* beta, const T* output, const T* merge_stats,
+                      const T* grad_output, T* grad_input, T* grad_weight, T* grad_alpha, T* grad_beta, int64_t B, int64_t Cin, int64_t Cout,
+                      int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_lds(mca::smorph_scm_lds<T>(g, true))) != MCA_OK) return rc;
+    if (!merge_stats && (int64_t)g.B * g.Cout * g.plane() > 0) return fail("merge_stats must not be null");
+    if ((rc = check_workspace(workspace_bytes, mca::smorph_scm_backward_workspace<T>(g), workspace)) != MCA_OK) return rc;
+    return hip_status(mca::smorph_scm_backward<T>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight,
+                                                  grad_alpha, grad_beta, g, workspace, workspace_bytes, (hipStream_t)stream));
 }
 
 // Device address of `scratch` on `device` (which must be the current device), looked up once per
@@ -347,6 +411,64 @@ int mca_smorph_backward_stats_f32(int merge, const float* input, const float* we
     if ((rc = check_stats(merge, g, stats)) != MCA_OK) return rc;
     return smorph_backward_impl<float>(merge, input, weight, alpha, output, grad_output, grad_input, grad_weight, grad_alpha, B, Cin, Cout,
                                        Cw, H, W, KH, KW, workspace, workspace_bytes, stream, stats);
+}
+
+size_t mca_smorph_scm_forward_workspace_size_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                 int64_t KW)
+{
+    return scm_forward_workspace_impl<float>(B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+size_t mca_smorph_scm_forward_workspace_size_f64(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                 int64_t KW)
+{
+    return scm_forward_workspace_impl<double>(B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+int mca_smorph_scm_forward_f32(const float* input, const float* weight, const float* alpha, const float* beta, float* output,
+                               float* merge_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                               int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return scm_forward_impl<float>(input, weight, alpha, beta, output, merge_stats, B, Cin, Cout, Cw, H, W, KH, KW, workspace,
+                                   workspace_bytes, stream);
+}
+
+int mca_smorph_scm_forward_f64(const double* input, const double* weight, const double* alpha, const double* beta, double* output,
+                               double* merge_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                               int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return scm_forward_impl<double>(input, weight, alpha, beta, output, merge_stats, B, Cin, Cout, Cw, H, W, KH, KW, workspace,
+                                    workspace_bytes, stream);
+}
+
+size_t mca_smorph_scm_backward_workspace_size_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                  int64_t KW)
+{
+    return scm_backward_workspace_impl<float>(B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+size_t mca_smorph_scm_backward_workspace_size_f64(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                                  int64_t KW)
+{
+    return scm_backward_workspace_impl<double>(B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+int mca_smorph_scm_backward_f32(const float* input, const float* weight, const float* alpha, const float* beta, const float* output,
+                                const float* merge_stats, const float* grad_output, float* grad_input, float* grad_weight, float* grad_alpha,
+                                float* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                                int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return scm_backward_impl<float>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight, grad_alpha,
+                                    grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_smorph_scm_backward_f64(const double* input, const double* weight, const double* alpha, const double* beta, const double* output,
+                                const double* merge_stats, const double* grad_output, double* grad_input, double* grad_weight,
+                                double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return scm_backward_impl<double>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight, grad_alpha,
+                                     grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -47,7 +47,8 @@ enum MergeKind : int
     MK_SUM = 0,  // ADD and AVERAGE (AVERAGE divides once at the end)
     MK_MAX = 1,
     MK_MIN = 2,
-    MK_IDENT = 3  // output channel c reads input channel c only
+    MK_IDENT = 3,  // output channel c reads input channel c only
+    MK_SMOOTH = 4  // smorph's SMOOTH merge (smorph_scm): a soft extremum over the pair outputs
 };
 
 constexpr int WAVE = 64;

@@ -84,6 +84,23 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
                            T* grad_alpha, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream,
                            const float* stats = nullptr);
 
+// Smorph with the SMOOTH channel merge (smorph_scm; generic kernels, float32 and float64).
+// Forward workspace: every pair output, [B, Cout, Cin, H, W]. `sstats` (2 * B * Cout * H * W values:
+// the soft merge's ref, then 1 / sum), written by the forward (may be null) and read by the backward.
+template <typename T>
+size_t smorph_scm_forward_workspace(const Geom& g);
+template <typename T>
+size_t smorph_scm_backward_workspace(const Geom& g);
+template <typename T>
+size_t smorph_scm_lds(const Geom& g, bool backward);
+template <typename T>
+hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* beta, T* out, T* sstats, const Geom& g, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+template <typename T>
+hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* beta, const T* out, const T* sstats, const T* grad_out,
+                               T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);

@@ -4,8 +4,15 @@
 // Per channel pair (o, i) and output pixel, over the taps that read an in-image pixel:
 //   v_k = x_k + w_k, ref = max v (alpha >= 0) or min v, e_k = exp(alpha (v_k - ref)),
 //   S = sum e_k, W = sum e_k v_k, out_pair = W * (1 / S), merged over input channels.
-// Out-of-image pixels are staged in LDS as NaN: they never win the ref scan, and the exp pass
-// selects them away.
+// A tap is in the image by its position (the staged tile holds 0 outside), so an in-image NaN takes
+// part as in the reference: it never wins the ref scan (strict comparison), and its exponential is
+// NaN, which reaches S, W and the gradients.
+//
+// SMOOTH merge (smorph_scm, smorph_cpu_kernels.hxx:231-266): the forward writes every pair output
+// c_i; smorph_soft_merge_kernel then takes ref = the extremum of the c_i (channel 0 first, strict),
+// q_i = exp(beta (c_i - ref)), out = (sum q_i c_i) * (1 / sum q_i). The backward routes, per pair,
+// g_i = g (p_i + beta p_i (c_i - out)) with p_i = q_i / sum q_i, recomputed from the forward's ref and
+// 1 / sum, and sums grad_beta = sum p_i (c_i - ref)(c_i - out) g.
 //
 // Forward (smorph_fwd_kernel): one workgroup per (batch element, output channel, tile) walks the
 // input channels with the tile staged in LDS. The same kernel in STATS mode counts, for MAX / MIN
@@ -22,50 +29,53 @@
 namespace mca
 {
 
-// ref, S and W of one pair for the RH pixels of this lane, from the staged tile.
-template <typename T, int RH>
-__device__ __forceinline__ void smorph_pair_stats(const T* tbase, int pitch, const T* __restrict__ wp, T a, int KH, int KW, T (&ref)[RH],
-                                                  T (&S)[RH], T (&Wsum)[RH])
+// Whether tap (kh, kw) of the output pixel whose first tap reads input row `iy` and column `ix`
+// (iy = h + KH / 2, ix = w + KW / 2) reads an in-image pixel.
+__device__ __forceinline__ bool tap_in_image(int iy, int ix, int kh, int kw, const Geom& g)
 {
+    return (unsigned)(iy - kh) < (unsigned)g.H && (unsigned)(ix - kw) < (unsigned)g.W;
+}
+
+// ref, S and W of one pair for the RH pixels of this lane (rows iy0 + r, column ix in input
+// coordinates of the first tap), from the staged tile.
+template <typename T, int RH>
+__device__ __forceinline__ void smorph_pair_stats(const T* tbase, int pitch, const T* __restrict__ wp, T a, const Geom& g, int iy0, int ix,
+                                                  T (&ref)[RH], T (&S)[RH], T (&Wsum)[RH])
+{
+#pragma clang fp contract(off)  // S = S + e and W fused as the reference rounds them (written as fma)
     const bool dilation_like = a >= T(0);
+    const T lo = ExpConsts<T>::min_input;
 #pragma unroll
     for (int r = 0; r < RH; ++r) ref[r] = dilation_like ? -std::numeric_limits<T>::infinity() : std::numeric_limits<T>::infinity();
-    if (dilation_like)
-    {
-        for (int kh = 0; kh < KH; ++kh)
-            for (int kw = 0; kw < KW; ++kw)
-            {
-                const T wk = wp[kh * KW + kw];
+    for (int kh = 0; kh < g.KH; ++kh)
+        for (int kw = 0; kw < g.KW; ++kw)
+        {
+            const T wk = wp[kh * g.KW + kw];
 #pragma unroll
-                for (int r = 0; r < RH; ++r) ref[r] = fmax(ref[r], tbase[(r - kh) * pitch - kw] + wk);
-            }
-    }
-    else
-    {
-        for (int kh = 0; kh < KH; ++kh)
-            for (int kw = 0; kw < KW; ++kw)
+            for (int r = 0; r < RH; ++r)
             {
-                const T wk = wp[kh * KW + kw];
-#pragma unroll
-                for (int r = 0; r < RH; ++r) ref[r] = fmin(ref[r], tbase[(r - kh) * pitch - kw] + wk);
+                const T v = tbase[(r - kh) * pitch - kw] + wk;
+                // Strict replacement: a NaN never wins, as in the reference.
+                const bool better = dilation_like ? v > ref[r] : v < ref[r];
+                if (better && tap_in_image(iy0 + r, ix, kh, kw, g)) ref[r] = v;
             }
-    }
+        }
 #pragma unroll
     for (int r = 0; r < RH; ++r)
     {
         S[r] = T(0);
         Wsum[r] = T(0);
     }
-    for (int kh = 0; kh < KH; ++kh)
-        for (int kw = 0; kw < KW; ++kw)
+    for (int kh = 0; kh < g.KH; ++kh)
+        for (int kw = 0; kw < g.KW; ++kw)
         {
-            const T wk = wp[kh * KW + kw];
+            const T wk = wp[kh * g.KW + kw];
 #pragma unroll
             for (int r = 0; r < RH; ++r)
             {
                 const T v = tbase[(r - kh) * pitch - kw] + wk;
-                const bool valid = v == v;
-                const T e = valid ? exp_t((v - ref[r]) * a) : T(0);
+                const bool valid = tap_in_image(iy0 + r, ix, kh, kw, g);
+                const T e = valid ? exp_ref((v - ref[r]) * a, lo) : T(0);
                 S[r] = S[r] + e;
                 Wsum[r] = fma(e, valid ? v : T(0), Wsum[r]);
             }
@@ -91,8 +101,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
     const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
     const int y0 = h0 + ph - (g.KH - 1), x0 = w0 + pw - (g.KW - 1);
     const int64_t plane = g.plane();
-    const T nan = std::numeric_limits<T>::quiet_NaN();
     const int wc = w0 + lane;
+    // Input coordinates read by tap (0, 0) of this lane's first output row.
+    const int iy0 = h0 + wave * RH + ph, ix = wc + pw;
 
     T m[RH], tgt[RH];
 #pragma unroll
@@ -114,13 +125,13 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
     for (int i = i_begin; i < i_end; ++i)
     {
         __syncthreads();
-        stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, nan);
+        stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, T(0));
         __syncthreads();
         const int pair = MK == MK_IDENT ? o : o * g.Cin + i;
         const T a = p.alpha[pair];
         const T* __restrict__ wp = p.w + ((int64_t)o * g.Cw + (MK == MK_IDENT ? 0 : i)) * K;
         T ref[RH], S[RH], Wsum[RH];
-        smorph_pair_stats<T, RH>(tbase, t.pitch, wp, a, g.KH, g.KW, ref, S, Wsum);
+        smorph_pair_stats<T, RH>(tbase, t.pitch, wp, a, g, iy0, ix, ref, S, Wsum);
 #pragma unroll
         for (int r = 0; r < RH; ++r)
         {
@@ -144,6 +155,11 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
             {
                 m[r] = fma(Wsum[r], inv, m[r]);
             }
+            else if constexpr (MK == MK_SMOOTH)
+            {
+                const int h = h0 + wave * RH + r;
+                if (h < g.H && wc < g.W) p.pout[(((int64_t)b * g.Cout + o) * g.Cin + i) * plane + (int64_t)h * g.W + wc] = Wsum[r] * inv;
+            }
             else
             {
                 m[r] = Wsum[r] * inv;
@@ -151,6 +167,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
         }
     }
 
+    if constexpr (MK == MK_SMOOTH) return;  // merged by smorph_soft_merge_kernel
 #pragma unroll
     for (int r = 0; r < RH; ++r)
     {
@@ -174,10 +191,13 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
     const Tiling t = p.t;
     const int tile_elems = t.rows * t.pitch;
     const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
+    // Bins per copy: the K taps of grad_weight, grad_alpha, and grad_beta for the SMOOTH merge.
+    const int nb = K + (MK == MK_SMOOTH ? 2 : 1);
     T* tile = reinterpret_cast<T*>(smem_raw);
     Acc* gtile = reinterpret_cast<Acc*>(smem_raw + align16((size_t)tile_elems * sizeof(T)));
     Acc* bins = gtile + tile_elems;
     Acc* abins = bins + K * p.ncopy;
+    Acc* bbins = abins + p.ncopy;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int work = xcd_work_index(blockIdx.x, gridDim.x);
     const int strip = work % p.nstrips;
@@ -190,9 +210,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
     T* part_w = p.part_w + (int64_t)slot * wnumel;
     T* part_a = p.part_a + (int64_t)slot * p.npairs;
     const int copy = lane & (p.ncopy - 1);
-    const T nan = std::numeric_limits<T>::quiet_NaN();
+    const T lo = ExpConsts<T>::min_input;
 
-    for (int j = threadIdx.x; j < (K + 1) * p.ncopy; j += BLOCK) bins[j] = Acc(0);
+    for (int j = threadIdx.x; j < nb * p.ncopy; j += BLOCK) bins[j] = Acc(0);
 
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
@@ -203,8 +223,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
         const int h0 = ty * t.th, w0 = tx * TILE_W;
         const int y0 = h0 + ph - (g.KH - 1), x0 = w0 + pw - (g.KW - 1);
         const int wc = w0 + lane;
+        const int iy0 = h0 + wave * RH + ph, ix = wc + pw;
         __syncthreads();
-        stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, nan);
+        stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, T(0));
         for (int j = threadIdx.x; j < tile_elems; j += BLOCK) gtile[j] = Acc(0);
         __syncthreads();
 
@@ -217,23 +238,38 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
             const T a = p.alpha[pair];
             const T* __restrict__ wp = p.w + ((int64_t)o * g.Cw + wi) * K;
             T ref[RH], S[RH], Wsum[RH], outp[RH], scaled[RH], asum[RH];
-            smorph_pair_stats<T, RH>(tbase, t.pitch, wp, a, g.KH, g.KW, ref, S, Wsum);
+            bool in[RH];
+            T bsum = T(0);
+            smorph_pair_stats<T, RH>(tbase, t.pitch, wp, a, g, iy0, ix, ref, S, Wsum);
 #pragma unroll
             for (int r = 0; r < RH; ++r)
             {
                 const int h = h0 + wave * RH + r;
-                const bool in = h < g.H && wc < g.W;
+                in[r] = h < g.H && wc < g.W;
                 const int64_t oi = ((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc;
-                T gv = in ? p.gout[oi] * p.scale : T(0);
+                T gv = in[r] ? p.gout[oi] * p.scale : T(0);
                 const T inv = T(1) / S[r];
                 outp[r] = Wsum[r] * inv;
                 if constexpr (MK == MK_MAX || MK == MK_MIN)
                 {
-                    if (in)
+                    if (in[r])
                     {
                         const T cnt = p.counts[oi];
                         gv = gv / (cnt > T(0) ? cnt : T(1));
                         if (!is_winner(outp[r], p.out[oi])) gv = T(0);
+                    }
+                }
+                if constexpr (MK == MK_SMOOTH)
+                {
+                    // Channel i's share of the soft merge, from the forward's ref and 1 / sum.
+                    if (in[r])
+                    {
+                        const T bt = p.beta[o];
+                        const T sref = p.sstats[oi], sinv = p.sstats[(int64_t)g.B * g.Cout * plane + oi], fin = p.out[oi];
+                        const T c = outp[r];
+                        const T pp = exp_ref((c - sref) * bt, lo) * sinv;
+                        bsum = bsum + pp * (c - sref) * (c - fin) * gv;
+                        gv = gv * fma(bt * pp, c - fin, pp);
                     }
                 }
                 scaled[r] = gv * inv;
@@ -247,10 +283,11 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
 #pragma unroll
                     for (int r = 0; r < RH; ++r)
                     {
-                        if (scaled[r] == T(0)) continue;
+                        // Every in-image tap of an in-image pixel routes, also with a zero gradient
+                        // (so that a NaN of the pair reaches the gradients, as in the reference).
+                        if (!in[r] || !tap_in_image(iy0 + r, ix, kh, kw, g)) continue;
                         const T v = tbase[(r - kh) * t.pitch - kw] + wk;
-                        if (!(v == v)) continue;
-                        const T e = exp_t((v - ref[r]) * a);
+                        const T e = exp_ref((v - ref[r]) * a, lo);
                         const T pg = e * scaled[r];
                         const T centered = v - outp[r];
                         const T c = fma(a * pg, centered, pg);
@@ -263,8 +300,10 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
 #pragma unroll
             for (int r = 0; r < RH; ++r) as += asum[r];
             if (as != T(0)) lds_add(&abins[copy], (Acc)as);
+            if constexpr (MK == MK_SMOOTH)
+                if (bsum != T(0)) lds_add(&bbins[copy], (Acc)bsum);
             __syncthreads();
-            for (int j = threadIdx.x; j <= K; j += BLOCK)
+            for (int j = threadIdx.x; j < nb; j += BLOCK)
             {
                 Acc s = Acc(0);
                 for (int c = 0; c < p.ncopy; ++c)
@@ -274,8 +313,10 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
                 }
                 if (j < K)
                     part_w[((int64_t)o * g.Cw + wi) * K + j] += (T)s;
-                else
+                else if (j == K)
                     part_a[pair] += (T)s;
+                else
+                    p.part_b[((int64_t)slot * g.Cin + i) * g.Cout + o] += (T)s;
             }
             __syncthreads();
         }
@@ -287,11 +328,66 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
             if (iy < 0 || iy >= g.H) continue;
             for (int lx = lane; lx < t.cols; lx += WAVE)
             {
-                const int ix = x0 + lx;
-                if (ix < 0 || ix >= g.W) continue;
+                const int gx = x0 + lx;
+                if (gx < 0 || gx >= g.W) continue;
                 const T v = (T)gtile[ly * t.pitch + lx];
-                if (v != T(0)) global_add(&gplane[(int64_t)iy * g.W + ix], v);
+                if (v != T(0)) global_add(&gplane[(int64_t)iy * g.W + gx], v);
             }
+        }
+    }
+}
+
+// SMOOTH merge of the pair outputs c_i of one (batch element, output channel, pixel) per thread
+// (smorph_soft_merge, smorph_cpu_kernels.hxx:231-266): ref = c_0, replaced by each later channel that
+// is strictly greater (beta >= 0) or smaller; q_i = exp((c_i - ref) beta); sum = sum q_i and
+// weighted = sum q_i c_i (fused) in channel order; out = weighted * (1 / sum). `sstats` (or null)
+// receives ref, then 1 / sum, [B, Cout, H, W] each, for the backward. The c_i of one output channel
+// are Cin planes apart, so consecutive threads read consecutive pixels of each plane.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void smorph_soft_merge_kernel(const T* __restrict__ pout, const T* __restrict__ beta, T* __restrict__ out,
+                                                                  T* __restrict__ sstats, Geom g)
+{
+#pragma clang fp contract(off)
+    const int64_t plane = g.plane();
+    const int64_t n = (int64_t)g.B * g.Cout * plane;
+    const T lo = ExpConsts<T>::min_input;
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
+    {
+        const int64_t bo = j / plane;
+        const int64_t pix = j - bo * plane;
+        const T bt = beta[bo % g.Cout];
+        const T* __restrict__ c = pout + bo * g.Cin * plane + pix;
+        T ref = c[0];
+        if (bt >= T(0))
+        {
+            for (int i = 1; i < g.Cin; ++i)
+            {
+                const T ci = c[(int64_t)i * plane];
+                ref = ci > ref ? ci : ref;
+            }
+        }
+        else
+        {
+            for (int i = 1; i < g.Cin; ++i)
+            {
+                const T ci = c[(int64_t)i * plane];
+                ref = ci < ref ? ci : ref;
+            }
+        }
+        T sum = T(0), weighted = T(0);
+        for (int i = 0; i < g.Cin; ++i)
+        {
+            const T ci = c[(int64_t)i * plane];
+            const T q = exp_ref((ci - ref) * bt, lo);
+            sum = sum + q;
+            weighted = fma(q, ci, weighted);
+        }
+        const T inv = T(1) / sum;
+        out[j] = weighted * inv;
+        if (sstats)
+        {
+            sstats[j] = ref;
+            sstats[n + j] = inv;
         }
     }
 }
@@ -307,7 +403,7 @@ struct SmorphBwdPlan
     int tps;
     int ncopy;
     int npairs;
-    size_t part_w_bytes, part_a_bytes, counts_bytes;
+    size_t part_w_bytes, part_a_bytes, part_b_bytes, counts_bytes;
     size_t lds;
 };
 
@@ -320,7 +416,7 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     SmorphBwdPlan s{};
     // The static kernels (smorph_static.hip) use one output row per wave (two from saved statistics)
     // and static LDS.
-    const bool stat = smorph_static_supported<T>(g);
+    const bool stat = merge != MERGE_SMOOTH && smorph_static_supported<T>(g);
     s.t = make_tiling(g, stat ? (saved ? 2 : 1) : rows_per_wave<T>());
     s.ncopy = 16;
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
@@ -336,10 +432,22 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     const size_t nslots = (size_t)g.B * s.nstrips;
     s.part_w_bytes = nslots * wnumel * sizeof(T);
     s.part_a_bytes = nslots * s.npairs * sizeof(T);
+    // SMOOTH: grad_beta partials [slot][Cin][Cout], as many values as the grad_alpha ones.
+    s.part_b_bytes = merge == MERGE_SMOOTH ? s.part_a_bytes : 0;
     // MAX / MIN: winner counts, then the merge target, per output pixel.
     s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? 2 * (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
-    s.lds = stat ? 0
-                 : align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + ((size_t)s.t.rows * s.t.pitch + (size_t)(g.taps() + 1) * s.ncopy) * sizeof(Acc);
+    if (stat)
+    {
+        s.lds = 0;  // static LDS
+        return s;
+    }
+    // The generic kernel: tile, its double grad_input copy, and ncopy copies of the bins (K taps,
+    // alpha, beta for SMOOTH); fewer copies (more same-address LDS adds) when a large element would
+    // not fit otherwise.
+    const size_t fixed = align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + (size_t)s.t.rows * s.t.pitch * sizeof(Acc);
+    const size_t nbins = (size_t)g.taps() + (merge == MERGE_SMOOTH ? 2 : 1);
+    while (s.ncopy > 1 && fixed + nbins * s.ncopy * sizeof(Acc) > LDS_LIMIT) s.ncopy /= 2;
+    s.lds = fixed + nbins * s.ncopy * sizeof(Acc);
     return s;
 }
 
@@ -358,8 +466,11 @@ static size_t smorph_plan_workspace(const SmorphBwdPlan& s, const Geom& g)
 {
     const int nslots = g.B * s.nstrips;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
-    return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes) +
-           align_up(reduce_slots_scratch<T>(nslots, wnumel > s.npairs ? wnumel : s.npairs));
+    const size_t red = reduce_slots_scratch<T>(nslots, wnumel > s.npairs ? wnumel : s.npairs);
+    // SMOOTH: grad_beta sums nslots * Cin partial rows of Cout values.
+    const size_t red_b = s.part_b_bytes ? reduce_slots_scratch<T>(nslots * g.Cin, g.Cout) : 0;
+    return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes) + align_up(s.counts_bytes) +
+           align_up(red > red_b ? red : red_b);
 }
 
 // Enough for either backward (recomputing or from saved statistics): the caller sizes the workspace
@@ -375,7 +486,7 @@ size_t smorph_backward_workspace(int merge, const Geom& g)
 template <typename T, int MK, bool STATS>
 static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t stream)
 {
-    if constexpr (sizeof(T) == 4)
+    if constexpr (sizeof(T) == 4 && MK != MK_SMOOTH)
         if (smorph_static_supported<T>(p.g)) return launch_smorph_fwd_static(MK, STATS, p, stream);
     constexpr int RH = rows_per_wave<T>();
     const int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout;
@@ -515,6 +626,122 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
     return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
 }
+
+// ------------------------------------------------------------------------------------------------
+// SMOOTH merge (smorph_scm): the generic kernels for every size and both types.
+// ------------------------------------------------------------------------------------------------
+
+template <typename T>
+size_t smorph_scm_forward_workspace(const Geom& g)
+{
+    return align_up((size_t)g.B * g.Cout * g.Cin * g.plane() * sizeof(T));
+}
+
+template <typename T>
+size_t smorph_scm_backward_workspace(const Geom& g)
+{
+    return smorph_plan_workspace<T>(plan_smorph_bwd<T>(MERGE_SMOOTH, g), g);
+}
+
+template <typename T>
+size_t smorph_scm_lds(const Geom& g, bool backward)
+{
+    if (backward) return plan_smorph_bwd<T>(MERGE_SMOOTH, g).lds;
+    const Tiling t = make_tiling(g, rows_per_wave<T>());
+    return (size_t)t.rows * t.pitch * sizeof(T);
+}
+
+static unsigned elementwise_grid(int64_t n)
+{
+    const int64_t blocks = (n + BLOCK - 1) / BLOCK;
+    return (unsigned)(blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks));
+}
+
+template <typename T>
+hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* beta, T* out, T* sstats, const Geom& g, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream)
+{
+    if (workspace_bytes < smorph_scm_forward_workspace<T>(g)) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)g.B * g.Cout * g.plane();
+    if (n == 0) return hipSuccess;
+    SmorphFwdParams<T> p{};
+    p.x = x;
+    p.w = w;
+    p.alpha = alpha;
+    p.pout = reinterpret_cast<T*>(workspace);
+    p.g = g;
+    p.t = make_tiling(g, rows_per_wave<T>());
+    hipError_t err = launch_smorph_fwd<T, MK_SMOOTH, false>(p, stream);
+    if (err != hipSuccess) return err;
+    smorph_soft_merge_kernel<T><<<elementwise_grid(n), BLOCK, 0, stream>>>(p.pout, beta, out, sstats, g);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* beta, const T* out, const T* sstats, const T* grad_out,
+                               T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream)
+{
+    hipError_t err;
+    const SmorphBwdPlan s = plan_smorph_bwd<T>(MERGE_SMOOTH, g);
+    if (workspace_bytes < smorph_plan_workspace<T>(s, g)) return hipErrorInvalidValue;
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
+    if ((int64_t)g.B * g.Cout * g.plane() == 0)
+    {
+        if ((err = fill_async<T>(grad_w, wnumel, T(0), stream)) != hipSuccess) return err;
+        if ((err = fill_async<T>(grad_alpha, s.npairs, T(0), stream)) != hipSuccess) return err;
+        return fill_async<T>(grad_beta, g.Cout, T(0), stream);
+    }
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    T* part_w = reinterpret_cast<T*>(ws);
+    T* part_a = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes));
+    T* part_b = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
+    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes));
+    const int nslots = g.B * s.nstrips;
+    if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
+    if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
+    if ((err = fill_async<T>(part_b, (int64_t)nslots * g.Cin * g.Cout, T(0), stream)) != hipSuccess) return err;
+
+    SmorphBwdParams<T> p{};
+    p.x = x;
+    p.w = w;
+    p.alpha = alpha;
+    p.out = out;
+    p.gout = grad_out;
+    p.gin = grad_in;
+    p.part_w = part_w;
+    p.part_a = part_a;
+    p.beta = beta;
+    p.sstats = sstats;
+    p.part_b = part_b;
+    p.g = g;
+    p.t = s.t;
+    p.nstrips = s.nstrips;
+    p.tps = s.tps;
+    p.ncopy = s.ncopy;
+    p.npairs = s.npairs;
+    p.scale = T(1);
+    constexpr int RH = rows_per_wave<T>();
+    const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
+    smorph_bwd_kernel<T, MK_SMOOTH, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
+    if ((err = reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream)) != hipSuccess) return err;
+    // grad_beta[o]: the partial rows [slot][i] summed in (slot, i) order.
+    return reduce_slots_async<T>(part_b, nslots * g.Cin, g.Cout, grad_beta, scratch, stream);
+}
+
+#define MCA_INSTANTIATE_SCM(T)                                                                                                           \
+    template size_t smorph_scm_forward_workspace<T>(const Geom&);                                                                        \
+    template size_t smorph_scm_backward_workspace<T>(const Geom&);                                                                       \
+    template size_t smorph_scm_lds<T>(const Geom&, bool);                                                                                \
+    template hipError_t smorph_scm_forward<T>(const T*, const T*, const T*, const T*, T*, T*, const Geom&, void*, size_t, hipStream_t); \
+    template hipError_t smorph_scm_backward<T>(const T*, const T*, const T*, const T*, const T*, const T*, const T*, T*, T*, T*, T*,   \
+                                               const Geom&, void*, size_t, hipStream_t);
+
+MCA_INSTANTIATE_SCM(float)
+MCA_INSTANTIATE_SCM(double)
 
 #define MCA_INSTANTIATE_SMORPH(T)                                                                                                   \
     template hipError_t smorph_forward<T>(int, const T*, const T*, const T*, T*, const Geom&, hipStream_t, float*);                \

@@ -113,6 +113,9 @@ struct SmorphFwdParams
     // every (batch element, output channel, pair, pixel), `nstat` values each.
     float* __restrict__ pstats;
     int64_t nstat;
+    // SMOOTH merge: every pair's output c, [B, Cout, Cin, H, W], merged afterwards by
+    // smorph_soft_merge_kernel.
+    T* __restrict__ pout;
     Geom g;
     Tiling t;
     int average;
@@ -186,6 +189,12 @@ struct SmorphBwdParams
     T* __restrict__ part_a;
     const float* __restrict__ pstats;  // the forward's saved pair statistics, or null (recomputed)
     int64_t nstat;
+    // SMOOTH merge (smorph_scm): beta per output channel, the forward's soft-merge statistics (ref,
+    // then 1 / sum, [B, Cout, H, W] each; `out` holds the merged output), and the grad_beta partials
+    // [slot][Cin][Cout].
+    const T* __restrict__ beta;
+    const T* __restrict__ sstats;
+    T* __restrict__ part_b;
     Geom g;
     Tiling t;
     int nstrips;

@@ -440,6 +440,14 @@ public:
         const Tensor w = w4.contiguous();
         const Geom g = geom_of(x, w);
         const Tensor ap = pair_alphas(alpha, merge, g.Cin, g.Cout);
+        if (needs_grad && g.B * g.Cout * g.H * g.W > 0)
+        {
+            const size_t ws = x.scalar_type() == c10::kFloat
+                                  ? mca_smorph_backward_workspace_size_f32((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)
+                                  : mca_smorph_backward_workspace_size_f64((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            TORCH_CHECK(ws > 0, "Structuring element too large for the smorph backward kernels' shared memory (", g.KH, "x", g.KW,
+                        "); run it without gradients");
+        }
         Tensor out = torch::empty({g.B, g.Cout, g.H, g.W}, x.options());
         Tensor stats;
         if (x.scalar_type() == c10::kFloat)
@@ -547,6 +555,88 @@ Tensor smorph(const Tensor& input, const Tensor& weight, const Tensor& alpha, in
     return output_to_original(SmorphFunction::apply(x4, w4, alpha, merge, needs_grad), input_dims);
 }
 
+// SmorphSCM (smorph_scm.cpp:13-96): smorph with the SMOOTH channel merge, one beta per output channel.
+// The forward keeps the soft merge's ref and 1 / sum per output pixel for the backward.
+class SmorphScmFunction : public torch::autograd::Function<SmorphScmFunction>
+{
+public:
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, const Tensor& w4, const Tensor& alpha, const Tensor& beta, bool needs_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const Tensor w = w4.contiguous();
+        const Tensor bt = beta.contiguous().reshape({-1});
+        const Geom g = geom_of(x, w);
+        const Tensor ap = pair_alphas(alpha, SMOOTH, g.Cin, g.Cout);
+        const bool f32 = x.scalar_type() == c10::kFloat;
+        if (needs_grad && g.B * g.Cout * g.H * g.W > 0)
+        {
+            const size_t ws = f32 ? mca_smorph_scm_backward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)
+                                  : mca_smorph_scm_backward_workspace_size_f64(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            TORCH_CHECK(ws > 0, "Structuring element too large for the smorph backward kernels' shared memory (", g.KH, "x", g.KW,
+                        "); run it without gradients");
+        }
+        Tensor out = torch::empty({g.B, g.Cout, g.H, g.W}, x.options());
+        Tensor mstats = needs_grad ? torch::empty({2, g.B, g.Cout, g.H, g.W}, x.options()) : Tensor();
+        const size_t n = f32 ? mca_smorph_scm_forward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)
+                             : mca_smorph_scm_forward_workspace_size_f64(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+        Tensor ws = byte_buffer((int64_t)n, x);
+        if (f32)
+            check_rc(mca_smorph_scm_forward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                out.data_ptr<float>(), mstats.defined() ? mstats.data_ptr<float>() : nullptr, g.B, g.Cin, g.Cout,
+                                                g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        else
+            check_rc(mca_smorph_scm_forward_f64(x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), bt.data_ptr<double>(),
+                                                out.data_ptr<double>(), mstats.defined() ? mstats.data_ptr<double>() : nullptr, g.B, g.Cin,
+                                                g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        ctx->save_for_backward({out, alpha, beta, x, w, mstats});
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor& out = saved[0];
+        const Tensor& alpha = saved[1];
+        const Tensor& beta = saved[2];
+        const Tensor& x = saved[3];
+        const Tensor& w = saved[4];
+        const Tensor& mstats = saved[5];
+        TORCH_CHECK(mstats.defined(), "smorph_scm: the forward ran without gradients and kept no merge statistics");
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(x.device());
+        const Geom g = geom_of(x, w);
+        const Tensor ap = pair_alphas(alpha, SMOOTH, g.Cin, g.Cout);
+        const Tensor bt = beta.contiguous().reshape({-1});
+        Tensor grad_input = torch::empty_like(x);
+        Tensor grad_weight = torch::empty_like(w);
+        Tensor grad_pairs = torch::empty_like(ap);
+        Tensor grad_beta = torch::empty_like(bt);
+        if (x.scalar_type() == c10::kFloat)
+        {
+            const size_t n = mca_smorph_scm_backward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc(mca_smorph_scm_backward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                 out.data_ptr<float>(), mstats.data_ptr<float>(), grad_output.data_ptr<float>(),
+                                                 grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(), grad_pairs.data_ptr<float>(),
+                                                 grad_beta.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(),
+                                                 (size_t)ws.numel(), stream_of(x)));
+        }
+        else
+        {
+            const size_t n = mca_smorph_scm_backward_workspace_size_f64(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc(mca_smorph_scm_backward_f64(x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), bt.data_ptr<double>(),
+                                                 out.data_ptr<double>(), mstats.data_ptr<double>(), grad_output.data_ptr<double>(),
+                                                 grad_input.data_ptr<double>(), grad_weight.data_ptr<double>(), grad_pairs.data_ptr<double>(),
+                                                 grad_beta.data_ptr<double>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(),
+                                                 (size_t)ws.numel(), stream_of(x)));
+        }
+        return {grad_input, grad_weight, alpha_grad(alpha, grad_pairs), grad_beta.view_as(beta), Tensor()};
+    }
+};
+
 // Body of the smorph_scm operator, smorph with the SMOOTH channel merge: bindings.cpp:122-125, then
 // SmorphSCM::forward's checks (smorph_scm.cpp:13-34, smorph_cpu_kernels.hxx:642-649, 668-672).
 Tensor smorph_scm(const Tensor& input, const Tensor& weight, const Tensor& alpha, const Tensor& beta)
@@ -559,8 +649,9 @@ Tensor smorph_scm(const Tensor& input, const Tensor& weight, const Tensor& alpha
     pair_alphas(alpha, SMOOTH, x4.size(1), w4.size(0));
     TORCH_CHECK(beta.numel() == w4.size(0), "Beta must have shape [out_channels]");
     check_device("smorph_scm_forward_hip", x4, {w4, alpha, beta});
-    TORCH_CHECK(false, "morphocore_amd: smorph_scm kernels are not built in this library");
-    return output_to_original(x4, input_dims);
+    const bool needs_grad = torch::GradMode::is_enabled() &&
+                            (input.requires_grad() || weight.requires_grad() || alpha.requires_grad() || beta.requires_grad());
+    return output_to_original(SmorphScmFunction::apply(x4, w4, alpha, beta, needs_grad), input_dims);
 }
 
 // Module-level helpers for tests and the benchmark (no reference counterpart).

@@ -458,6 +458,192 @@ int FN(oracle_smorph_backward)(int merge, const T* x, const T* wt, const T* alph
     return 0;
 }
 
+/* Soft extremum over the channels of one pixel, the SMOOTH merge: smorph_soft_merge
+ * (smorph_cpu_kernels.hxx:231-266). ref starts at channel 0 and takes each later channel that is
+ * strictly greater (beta >= 0) or smaller (beta < 0); q_i = exp((c_i - ref) * beta) with the
+ * reference's vector exponential; sum = sum q_i and weighted = sum q_i c_i (fused) in channel order;
+ * merged = weighted * (1 / sum). */
+static inline T FN(soft_merge)(const T* c, int64_t n, T beta, T* ref_out, T* inv_out)
+{
+    const int max_like = beta >= (T)0;
+    T ref = c[0];
+    for (int64_t i = 1; i < n; i++)
+        if (max_like ? (c[i] > ref) : (c[i] < ref)) ref = c[i];
+    T sum = (T)0, weighted = (T)0;
+    for (int64_t i = 0; i < n; i++)
+    {
+        const T q = EXP_T((c[i] - ref) * beta);
+        sum = sum + q;
+        weighted = FMA_T(q, c[i], weighted);
+    }
+    const T inv = (T)1 / sum;
+    *ref_out = ref;
+    *inv_out = inv;
+    return weighted * inv;
+}
+
+/* Forward of smorph with the SMOOTH channel merge (the smorph_scm operator): SmorphForwardBands::run
+ * (smorph_cpu_kernels.hxx:308-380) stores the pair output c_i of every input channel, then
+ * smorph_soft_merge merges them with the output channel's beta (no AVERAGE division). alpha holds one
+ * value per pair, index o * Cin + i (smorph_pair_alphas<SMOOTH>, :642-649); beta one per output
+ * channel. */
+int FN(oracle_smorph_scm_forward)(const T* x, const T* wt, const T* alpha, const T* beta, T* out, int64_t B, int64_t Cin, int64_t Cout,
+                                  int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    oracle_geom g = {B, Cin, Cout, Cw, H, W, KH, KW};
+    const int64_t taps = KH * KW, plane = H * W;
+    if (Cw != Cin || Cin < 1) return 1;
+
+#pragma omp parallel
+    {
+        T* outs = (T*)malloc((size_t)Cin * sizeof(T));
+#pragma omp for collapse(2) schedule(dynamic)
+        for (int64_t b = 0; b < B; b++)
+        {
+            for (int64_t o = 0; o < Cout; o++)
+            {
+                for (int64_t h = 0; h < H; h++)
+                {
+                    for (int64_t w = 0; w < W; w++)
+                    {
+                        T ref, inv;
+                        for (int64_t i = 0; i < Cin; i++)
+                            outs[i] = FN(smorph_pair)(x + (b * Cin + i) * plane, wt + (o * Cin + i) * taps, alpha[o * Cin + i], &g, h, w, &ref, &inv,
+                                                      NULL, NULL);
+                        out[((b * Cout + o) * H + h) * W + w] = FN(soft_merge)(outs, Cin, beta[o], &ref, &inv);
+                    }
+                }
+            }
+        }
+        free(outs);
+    }
+    return 0;
+}
+
+/* Backward of smorph_scm: SmorphBackwardBands::run with soft_merge (smorph_cpu_kernels.hxx:420-603).
+ * For each pixel (g = grad, no scaling): recompute every channel's pair output c_i and the soft merge
+ * (ref, 1 / sum, final); channel i receives
+ *   p_i = exp((c_i - ref) * beta) * (1 / sum),  g_i = g * (p_i + beta * p_i * (c_i - final)) (fused),
+ * and routes g_i through its pair exactly as the ADD merge routes g (oracle_smorph_backward), while
+ *   grad_beta[o] += p_i * (c_i - ref) * (c_i - final) * g.
+ * grad_alpha has one value per pair, grad_beta one per output channel. All outputs overwritten. */
+int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, const T* beta, const T* grad_out, T* grad_in, T* grad_w,
+                                   T* grad_alpha, T* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W,
+                                   int64_t KH, int64_t KW)
+{
+    oracle_geom g = {B, Cin, Cout, Cw, H, W, KH, KW};
+    const int64_t taps = KH * KW, plane = H * W, pad_h = KH / 2, pad_w = KW / 2;
+    if (Cw != Cin || Cin < 1) return 1;
+    const int64_t wnumel = Cout * Cw * taps;
+    const int64_t anumel = Cout * Cin;
+
+    ACC* gx_acc = (ACC*)calloc((size_t)(B * Cin * plane), sizeof(ACC));
+    ACC* gw_part = (ACC*)calloc((size_t)(B * wnumel), sizeof(ACC));
+    ACC* ga_part = (ACC*)calloc((size_t)(B * anumel), sizeof(ACC));
+    ACC* gb_part = (ACC*)calloc((size_t)(B * Cout), sizeof(ACC));
+    if (!gx_acc || !gw_part || !ga_part || !gb_part) return 2;
+
+#pragma omp parallel
+    {
+        T* exps = (T*)malloc((size_t)taps * sizeof(T));
+        T* outs = (T*)malloc((size_t)Cin * sizeof(T));
+#pragma omp for schedule(dynamic)
+        for (int64_t b = 0; b < B; b++)
+        {
+            ACC* gw = gw_part + b * wnumel;
+            ACC* ga = ga_part + b * anumel;
+            ACC* gb = gb_part + b * Cout;
+            for (int64_t o = 0; o < Cout; o++)
+            {
+                const T bt = beta[o];
+                for (int64_t h = 0; h < H; h++)
+                {
+                    int64_t kh_begin = h + pad_h - (H - 1);
+                    if (kh_begin < 0) kh_begin = 0;
+                    int64_t kh_end = h + pad_h + 1;
+                    if (kh_end > KH) kh_end = KH;
+                    for (int64_t w = 0; w < W; w++)
+                    {
+                        const T grad = grad_out[((b * Cout + o) * H + h) * W + w];
+                        for (int64_t i = 0; i < Cin; i++)
+                        {
+                            T ref, inv;
+                            outs[i] = FN(smorph_pair)(x + (b * Cin + i) * plane, wt + (o * Cin + i) * taps, alpha[o * Cin + i], &g, h, w, &ref, &inv,
+                                                      NULL, NULL);
+                        }
+                        T sref, sinv;
+                        const T fin = FN(soft_merge)(outs, Cin, bt, &sref, &sinv);
+                        for (int64_t i = 0; i < Cin; i++)
+                        {
+                            const T c = outs[i];
+                            const T p = EXP_T((c - sref) * bt) * sinv;
+                            gb[o] += (ACC)(p * (c - sref) * (c - fin) * grad);
+                        }
+                        for (int64_t i = 0; i < Cin; i++)
+                        {
+                            const T c = outs[i];
+                            const T p = EXP_T((c - sref) * bt) * sinv;
+                            const T pair_grad = grad * FMA_T(bt * p, c - fin, p); /* g * (p + beta * p * (c - final)), fused */
+                            const int64_t ai = o * Cin + i;
+                            const T a = alpha[ai];
+                            const T* pl = x + (b * Cin + i) * plane;
+                            const T* wp = wt + (o * Cw + i) * taps;
+                            T ref, pinv;
+                            const T out = FN(smorph_pair)(pl, wp, a, &g, h, w, &ref, &pinv, exps, NULL);
+                            const T scaled = pair_grad * pinv;
+                            ACC alpha_sum = 0;
+                            for (int64_t kw = 0; kw < KW; kw++)
+                            {
+                                for (int64_t kh = kh_begin; kh < kh_end; kh++)
+                                {
+                                    const int64_t k = kh * KW + kw;
+                                    const int64_t ih = h + pad_h - kh, iw = w + pad_w - kw;
+                                    if (iw < 0 || iw >= W) continue;
+                                    const T v = pl[ih * W + iw] + wp[k];
+                                    const T pg = exps[k] * scaled;
+                                    const T centered = v - out;
+                                    const T cc = FMA_T(a * pg, centered, pg);
+                                    gx_acc[(b * Cin + i) * plane + ih * W + iw] += (ACC)cc;
+                                    gw[(o * Cw + i) * taps + k] += (ACC)cc;
+                                    alpha_sum += (ACC)(pg * (v - ref) * centered);
+                                }
+                            }
+                            ga[ai] += alpha_sum;
+                        }
+                    }
+                }
+            }
+        }
+        free(exps);
+        free(outs);
+    }
+
+    for (int64_t j = 0; j < B * Cin * plane; j++) grad_in[j] = (T)gx_acc[j];
+    for (int64_t j = 0; j < wnumel; j++)
+    {
+        ACC s = 0;
+        for (int64_t b = 0; b < B; b++) s += gw_part[b * wnumel + j];
+        grad_w[j] = (T)s;
+    }
+    for (int64_t j = 0; j < anumel; j++)
+    {
+        ACC s = 0;
+        for (int64_t b = 0; b < B; b++) s += ga_part[b * anumel + j];
+        grad_alpha[j] = (T)s;
+    }
+    for (int64_t o = 0; o < Cout; o++)
+    {
+        ACC s = 0;
+        for (int64_t b = 0; b < B; b++) s += gb_part[b * Cout + o];
+        grad_beta[o] = (T)s;
+    }
+    free(gx_acc);
+    free(gw_part);
+    free(ga_part);
+    free(gb_part);
+    return 0;
+}
+
 #undef FN
 #undef CAT
 #undef CAT_

@@ -59,6 +59,12 @@ def lib() -> ctypes.CDLL:
             f = getattr(_lib, f"oracle_smorph_backward_{sfx}")
             f.argtypes = [i32, p, p, p, p, p, p, p] + geom
             f.restype = i32
+            f = getattr(_lib, f"oracle_smorph_scm_forward_{sfx}")
+            f.argtypes = [p, p, p, p, p] + geom
+            f.restype = i32
+            f = getattr(_lib, f"oracle_smorph_scm_backward_{sfx}")
+            f.argtypes = [p, p, p, p, p, p, p, p, p] + geom
+            f.restype = i32
         _lib.oracle_expf.argtypes = [ctypes.c_float]
         _lib.oracle_expf.restype = ctypes.c_float
         _lib.oracle_exp.argtypes = [ctypes.c_double]
@@ -184,6 +190,52 @@ def smorph_backward(merge, x, w_tilde, alpha, grad_out):
     else:
         ga = ga.reshape(alpha.shape)
     return gx, gw, ga
+
+
+def smorph_scm_forward(x, w_tilde, alpha, beta):
+    """Op-level smorph with the SMOOTH channel merge (the smorph_scm operator, smorph_scm.cpp:13-53):
+    ``beta`` holds one value per output channel; ``alpha`` one per pair or one shared value."""
+    x = np.ascontiguousarray(x)
+    dtype = x.dtype
+    w_tilde = np.ascontiguousarray(w_tilde, dtype=dtype)
+    B, Cin, H, W = x.shape
+    Cout, Cw, KH, KW = w_tilde.shape
+    a = np.ascontiguousarray(pair_alphas(alpha, SMOOTH, Cin, Cout), dtype=dtype)
+    b = np.ascontiguousarray(np.asarray(beta, dtype=dtype).reshape(-1))
+    if b.size != Cout:
+        raise ValueError("Beta must have shape [out_channels]")
+    out = np.empty((B, Cout, H, W), dtype=dtype)
+    rc = getattr(lib(), f"oracle_smorph_scm_forward_{_sfx(dtype)}")(_ptr(x), _ptr(w_tilde), _ptr(a), _ptr(b), _ptr(out), B, Cin, Cout, Cw,
+                                                                   H, W, KH, KW)
+    if rc != 0:
+        raise RuntimeError(f"oracle_smorph_scm_forward failed ({rc})")
+    return out
+
+
+def smorph_scm_backward(x, w_tilde, alpha, beta, grad_out):
+    """Op-level smorph_scm backward (smorph_scm.cpp:55-96). Returns ``(grad_input, grad_w_tilde,
+    grad_alpha, grad_beta)``, grad_alpha shaped like ``alpha`` (a shared alpha receives the sum over
+    pairs) and grad_beta like ``beta``."""
+    x = np.ascontiguousarray(x)
+    dtype = x.dtype
+    w_tilde = np.ascontiguousarray(w_tilde, dtype=dtype)
+    grad_out = np.ascontiguousarray(grad_out, dtype=dtype)
+    B, Cin, H, W = x.shape
+    Cout, Cw, KH, KW = w_tilde.shape
+    alpha = np.asarray(alpha)
+    beta = np.asarray(beta)
+    a = np.ascontiguousarray(pair_alphas(alpha, SMOOTH, Cin, Cout), dtype=dtype)
+    b = np.ascontiguousarray(beta.astype(dtype).reshape(-1))
+    gx, gw, ga, gb = np.empty_like(x), np.empty_like(w_tilde), np.empty_like(a), np.empty_like(b)
+    rc = getattr(lib(), f"oracle_smorph_scm_backward_{_sfx(dtype)}")(_ptr(x), _ptr(w_tilde), _ptr(a), _ptr(b), _ptr(grad_out), _ptr(gx),
+                                                                    _ptr(gw), _ptr(ga), _ptr(gb), B, Cin, Cout, Cw, H, W, KH, KW)
+    if rc != 0:
+        raise RuntimeError(f"oracle_smorph_scm_backward failed ({rc})")
+    if alpha.size != a.size:
+        ga = np.asarray(ga.sum(dtype=np.float64), dtype=dtype).reshape(alpha.shape)
+    else:
+        ga = ga.reshape(alpha.shape)
+    return gx, gw, ga, gb.reshape(beta.shape)
 
 
 # ----------------------------------------------------------------------------------------------

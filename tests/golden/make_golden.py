@@ -52,6 +52,16 @@ def smorph_case(ops, merge, x, wt, alpha, g):
     return out.detach(), xr.grad, wr.grad, ar.grad
 
 
+def smorph_scm_case(ops, x, wt, alpha, beta, g):
+    xr = x.clone().requires_grad_(True)
+    wr = wt.clone().requires_grad_(True)
+    ar = alpha.clone().requires_grad_(True)
+    br = beta.clone().requires_grad_(True)
+    out = ops.smorph_scm(xr, wr, ar, br)
+    out.backward(g)
+    return out.detach(), xr.grad, wr.grad, ar.grad, br.grad
+
+
 def main():
     if not os.path.exists(REF_LIB):
         sys.exit(f"{REF_LIB} is missing: build it with make -f oracle/Makefile.ref")
@@ -101,6 +111,23 @@ def main():
                 arrays[key + "/gx"] = gx.numpy()
                 arrays[key + "/gw"] = gw.numpy()
                 arrays[key + "/ga"] = ga.numpy()
+        # smorph_scm: the SMOOTH channel merge, one beta per output channel (smorph_scm.cpp:33).
+        wt = gen(9, Cout, Cin, KH, KW, dtype=dtype, scale=0.1)
+        arrays[f"{dname}/scm/w"] = wt.numpy()
+        alphas = {"mixed": gen(10, Cout, Cin, dtype=dtype, scale=3.0), "shared": torch.tensor(-0.8, dtype=dtype)}
+        betas = {"pos": torch.full((Cout,), 2.0, dtype=dtype), "neg": torch.full((Cout,), -3.0, dtype=dtype),
+                 "zero": torch.zeros(Cout, dtype=dtype), "mixed": gen(11, Cout, dtype=dtype, scale=10.0)}
+        for aname, alpha in alphas.items():
+            for bname, beta in betas.items():
+                out, gx, gw, ga, gb = smorph_scm_case(ops, x, wt, alpha, beta, g)
+                key = f"{dname}/scm/{aname}/{bname}"
+                arrays[key + "/alpha"] = alpha.numpy()
+                arrays[key + "/beta"] = beta.numpy()
+                arrays[key + "/out"] = out.numpy()
+                arrays[key + "/gx"] = gx.numpy()
+                arrays[key + "/gw"] = gw.numpy()
+                arrays[key + "/ga"] = ga.numpy()
+                arrays[key + "/gb"] = gb.numpy()
     np.savez_compressed(OUT, **arrays)
     print(f"wrote {len(arrays)} arrays to {OUT} ({os.path.getsize(OUT)} bytes)")
 

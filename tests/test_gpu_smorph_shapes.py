@@ -1,0 +1,75 @@
+"""Smorph parity on the GPU for the elements the static float32 kernels do not cover: rectangular,
+even and one-row elements (pad = K // 2 on each axis, so asymmetric windows), float64 at 7x7 and
+11x11, and NaN inputs through the generic kernels (float64, 9x9 and 3x5 float32). Every merge,
+alpha of both signs and zero; the oracle is the checker (reference smorph_cpu_kernels.hxx:30-147 for
+the window bounds)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import TOL, normwise_error, seeded
+from tests.test_gpu_parity import MERGES, _smorph_case, _weight_shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _alpha(merge, Cin, Cout, a, dtype, seed):
+    pairs = Cout if merge == "identity" else Cout * Cin
+    alpha = torch.full((pairs,), a, dtype=dtype) + seeded(seed, pairs, dtype=dtype, kind="randn", scale=0.1 if a != 0 else 0.0)
+    return alpha.reshape((Cout,) if merge == "identity" else (Cout, Cin))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("a", [-20.0, 0.0, 20.0])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("KH,KW", [(3, 5), (5, 3), (4, 2), (1, 5)])
+def test_smorph_rectangular_and_even_elements(KH, KW, merge, a, dtype):
+    B, Cin, Cout, H, W = 2, 3, 4, 18, 70
+    if merge == "identity":
+        Cout = Cin
+    print(f"smorph {KH}x{KW} {merge} alpha={a} {dtype}", flush=True)
+    x = seeded(81, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(82, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="randn", scale=0.1)
+    g = seeded(83, B, Cout, H, W, dtype=dtype, kind="randn")
+    for actual, expected in _smorph_case(merge, x, w, _alpha(merge, Cin, Cout, a, dtype, 84), g):
+        assert normwise_error(actual, expected) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("a", [-20.0, 1.0, 20.0])
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("K", [7, 11])
+def test_smorph_float64_large_elements(K, merge, a):
+    B, Cin, Cout, H, W = 1, 2, 3, 21, 75
+    if merge == "identity":
+        Cout = Cin
+    print(f"smorph f64 {K}x{K} {merge} alpha={a}", flush=True)
+    x = seeded(85, B, Cin, H, W, dtype=torch.float64, kind="randn")
+    w = seeded(86, *_weight_shape(merge, Cin, Cout, K, K), dtype=torch.float64, kind="randn", scale=0.1)
+    g = seeded(87, B, Cout, H, W, dtype=torch.float64, kind="randn")
+    for actual, expected in _smorph_case(merge, x, w, _alpha(merge, Cin, Cout, a, torch.float64, 88), g):
+        assert normwise_error(actual, expected) <= TOL[torch.float64]
+
+
+@pytest.mark.parametrize("merge", ["sum", "max", "identity"])
+@pytest.mark.parametrize("dtype,KH,KW", [(torch.float64, 3, 3), (torch.float64, 7, 7), (torch.float32, 9, 9), (torch.float32, 3, 5)])
+def test_smorph_generic_nan_input(dtype, KH, KW, merge):
+    """An in-image NaN propagates through the generic kernels as through the reference: its pairs'
+    outputs and routed gradients are NaN (a NaN never wins the window's extremum, nor the MAX merge);
+    out-of-image taps are excluded by position, not by value. Same NaN positions as the oracle, every
+    finite value within the tolerance."""
+    B, Cin, Cout, H, W = 1, 2, 3, 20, 100
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(89, B, Cin, H, W, dtype=dtype, kind="randn")
+    x[0, 0, 9, 50] = float("nan")
+    x[0, 1, 0, 2] = float("nan")
+    w = seeded(90, *_weight_shape(merge, Cin, Cout, KH, KW), dtype=dtype, kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    alpha = torch.where(torch.arange(pairs) % 2 == 0, 2.0, -3.0).to(dtype)
+    alpha = alpha.reshape((Cout,) if merge == "identity" else (Cout, Cin))
+    g = seeded(91, B, Cout, H, W, dtype=dtype, kind="randn")
+    results = _smorph_case(merge, x, w, alpha, g)
+    assert np.isnan(results[0][1]).any() == (merge != "max")
+    for actual, expected in results:
+        assert normwise_error(actual, expected) <= TOL[dtype]

@@ -331,3 +331,70 @@ def test_per_sample_weights_equal_per_sample_calls(merge):
         np.testing.assert_allclose(gx[b:b + 1], gxb, rtol=1e-12, atol=1e-12)
         gw_sum += gwb
     np.testing.assert_allclose(gw, gw_sum, rtol=1e-12, atol=1e-12)
+
+
+def test_golden_smorph_scm(golden):
+    """The SMOOTH channel merge (smorph_scm) against the reference's own CPU build: forward bit for
+    bit, gradients of x, w~, alpha and beta within the tolerance."""
+    n = 0
+    for dname in ("f32", "f64"):
+        x = golden[f"{dname}/x"]
+        g = golden[f"{dname}/g"]
+        wt = golden[f"{dname}/scm/w"]
+        for aname in ("mixed", "shared"):
+            for bname in ("pos", "neg", "zero", "mixed"):
+                key = f"{dname}/scm/{aname}/{bname}"
+                alpha, beta = golden[key + "/alpha"], golden[key + "/beta"]
+                out = O.smorph_scm_forward(x, wt, alpha, beta)
+                assert np.array_equal(out, golden[key + "/out"]), key
+                gx, gw, ga, gb = O.smorph_scm_backward(x, wt, alpha, beta, g)
+                for got, name in ((gx, "gx"), (gw, "gw"), (ga, "ga"), (gb, "gb")):
+                    assert got.shape == golden[f"{key}/{name}"].shape, (key, name)
+                    assert normwise_error(got, golden[f"{key}/{name}"]) <= TOLS[dname], (key, name)
+                n += 1
+    assert n == 16
+
+
+def test_smorph_scm_limits():
+    """What the mathematics fixes for the SMOOTH merge of the pair outputs c_i (each pair's smorph
+    output, taken from the oracle's ADD merge with a single input channel):
+    beta = 0 gives their mean, beta -> +inf their maximum and -inf their minimum (closed forms), and
+    one input channel gives c_0 itself, bit for bit (q = exp(0) = 1)."""
+    rng = np.random.default_rng(21)
+    B, Cin, Cout, H, W, K = 2, 3, 2, 6, 7, 3
+    x = rng.standard_normal((B, Cin, H, W))
+    w = rng.standard_normal((Cout, Cin, K, K)) * 0.2
+    alpha = rng.standard_normal((Cout, Cin)) * 2
+    # c[b, o, i] from single-channel smorph calls
+    c = np.stack([np.stack([O.smorph_forward(O.ADD, x[:, i:i + 1], w[o:o + 1, i:i + 1], alpha[o, i])[:, 0] for i in range(Cin)], 1)
+                  for o in range(Cout)], 1)
+    assert c.shape == (B, Cout, Cin, H, W)
+    mean = O.smorph_scm_forward(x, w, alpha, np.zeros(Cout))
+    np.testing.assert_allclose(mean, c.mean(axis=2), rtol=1e-13, atol=1e-13)
+    hi = O.smorph_scm_forward(x, w, alpha, np.full(Cout, 1e6))
+    np.testing.assert_allclose(hi, c.max(axis=2), rtol=0, atol=1e-4)
+    lo = O.smorph_scm_forward(x, w, alpha, np.full(Cout, -1e6))
+    np.testing.assert_allclose(lo, c.min(axis=2), rtol=0, atol=1e-4)
+    for dtype in (np.float32, np.float64):
+        x1, w1 = x[:, :1].astype(dtype), w[:, :1].astype(dtype)
+        one = O.smorph_scm_forward(x1, w1, alpha[:, :1].astype(dtype), np.array([3.0, -2.0], dtype))
+        assert np.array_equal(one, O.smorph_forward(O.ADD, x1, w1, alpha[:, :1].astype(dtype)))
+
+
+def test_smorph_scm_gradients_match_finite_differences():
+    """float64 central finite differences of a weighted sum of smorph_scm outputs, for x, w~, alpha
+    and beta (a dropped or mis-signed term of the channel merge's derivative fails here)."""
+    rng = np.random.default_rng(22)
+    B, Cin, Cout, H, W, K = 1, 3, 2, 4, 5, 3
+    x = rng.standard_normal((B, Cin, H, W))
+    w = rng.standard_normal((Cout, Cin, K, K)) * 0.3
+    alpha = rng.standard_normal((Cout, Cin)) * 2
+    beta = np.array([1.7, -2.4])
+    g = rng.standard_normal((B, Cout, H, W))
+
+    def loss():
+        return float(np.sum(O.smorph_scm_forward(x, w, alpha, beta) * g))
+
+    gx, gw, ga, gb = O.smorph_scm_backward(x, w, alpha, beta, g)
+    for got, arr in ((gx, x), (gw, w), (ga, alpha), (gb, beta)):
+        np.testing.assert_allclose(got, _finite_difference(loss, arr, 1e-6), rtol=1e-5, atol=1e-7)
