@@ -191,6 +191,13 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                 double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Test probe, no reference counterpart: y[j] = the exponential every smorph kernel evaluates, applied
+ * to x[j] (n values, device pointers). It restates the reference's vector exponential
+ * (morphocore/functional/csrc/cpp/morpho_cpu_simd.hpp:127-169) for the arguments the kernels pass,
+ * alpha (v - ref) <= 0 or NaN; the tests compare its bits with the oracle's. */
+int mca_probe_smorph_exp_f32(const float* x, float* y, int64_t n, void* stream);
+int mca_probe_smorph_exp_f64(const double* x, double* y, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,8 @@ EXPORTS = (
     "mca_smorph_scm_backward_workspace_size_f64",
     "mca_smorph_scm_backward_f32",
     "mca_smorph_scm_backward_f64",
+    "mca_probe_smorph_exp_f32",
+    "mca_probe_smorph_exp_f64",
 )
 
 _lib = None
@@ -91,6 +93,9 @@ def lib() -> ctypes.CDLL:
             f = getattr(so, f"mca_smorph_scm_{d}_workspace_size_{sfx}")
             f.argtypes = list(_GEOM)
             f.restype = _SZ
+        f = getattr(so, f"mca_probe_smorph_exp_{sfx}")
+        f.argtypes = [_P, _P, _I64, _P]
+        f.restype = _I
         f = getattr(so, f"mca_smorph_scm_forward_{sfx}")
         f.argtypes = [_P] * 6 + _GEOM + [_P, _SZ, _P]
         f.restype = _I
@@ -229,3 +234,8 @@ def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out
     f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
     _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w),
              _ptr(grad_alpha), _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def probe_smorph_exp(x, y):
+    """y = the smorph kernels' exponential of x, elementwise (C ABI mca_probe_smorph_exp_*; tests)."""
+    _check(getattr(lib(), f"mca_probe_smorph_exp_{_sfx(x)}")(_ptr(x), _ptr(y), x.numel(), _stream(x)))

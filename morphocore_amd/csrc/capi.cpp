@@ -471,4 +471,16 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                      grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
 }
 
+int mca_probe_smorph_exp_f32(const float* x, float* y, int64_t n, void* stream)
+{
+    if (n < 0) return fail("n must be non negative");
+    return hip_status(mca::exp_probe<float>(x, y, n, (hipStream_t)stream));
+}
+
+int mca_probe_smorph_exp_f64(const double* x, double* y, int64_t n, void* stream)
+{
+    if (n < 0) return fail("n must be non negative");
+    return hip_status(mca::exp_probe<double>(x, y, n, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -101,6 +101,10 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
 
+// The smorph kernels' exponential applied elementwise (test probe).
+template <typename T>
+hipError_t exp_probe(const T* x, T* y, int64_t n, hipStream_t stream);
+
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);

@@ -627,6 +627,25 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
 }
 
+// The smorph kernels' exponential, elementwise (a test probe of its bits).
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void exp_probe_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) y[j] = exp_ref(x[j]);
+}
+
+template <typename T>
+hipError_t exp_probe(const T* x, T* y, int64_t n, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + BLOCK - 1) / BLOCK;
+    exp_probe_kernel<T><<<(unsigned)(blocks > 8192 ? 8192 : blocks), BLOCK, 0, stream>>>(x, y, n);
+    return hipGetLastError();
+}
+
+template hipError_t exp_probe<float>(const float*, float*, int64_t, hipStream_t);
+template hipError_t exp_probe<double>(const double*, double*, int64_t, hipStream_t);
+
 // ------------------------------------------------------------------------------------------------
 // SMOOTH merge (smorph_scm): the generic kernels for every size and both types.
 // ------------------------------------------------------------------------------------------------

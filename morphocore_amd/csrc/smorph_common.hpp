@@ -11,7 +11,7 @@ namespace mca
 // Cody-Waite reduction x = n ln2 + r with ln2 split in a high and a low part, exp(r) by its Taylor
 // series in Horner form with fused multiply-adds (degree 7 for float, 13 for double, coefficients
 // 1/k! by repeated division in the element type), 2^n assembled in the exponent bits; inputs below
-// the log of the smallest normal give 0, inputs above the overflow threshold are clamped.
+// the log of the smallest normal give 0 (exp_ref below).
 // The kernels need these exact roundings: the smorph gradients scale the rounding error of each
 // pair's output by alpha, so an exponential that differs by an ulp (even a correctly rounded one)
 // moves float32 gradients by ~1e-6 relative at |alpha| = 20.
@@ -61,23 +61,6 @@ __device__ __forceinline__ T horner(T r)
         return InvFact<T, K>::value;
     else
         return fma(horner<T, K + 1>(r), r, InvFact<T, K>::value);
-}
-
-template <typename T>
-__device__ __forceinline__ T exp_t(T x)
-{
-    using C = ExpConsts<T>;
-    using Bits = typename C::Bits;
-    const T xc = fmin(fmax(x, C::min_input), C::max_input);
-    const T nm = fma(xc, C::log2e, C::magic);
-    const T n = nm - C::magic;
-    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, xc));
-    const T p = horner<T, 0>(r);
-    // The low bits of nm hold n (two's complement): shifting them into the exponent field and
-    // adding the bias builds 2^n without a float to int conversion.
-    const Bits bits = (Bits)(((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant) + ((uint64_t)C::bias << C::mant));
-    const T scale = x < C::min_input ? T(0) : __builtin_bit_cast(T, bits);
-    return p * scale;
 }
 
 // The target the reference's MAX / MIN backward compares the pair outputs with: the extremum over the

@@ -20,6 +20,7 @@
  */
 #include <float.h>
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -106,6 +107,19 @@ static inline double oracle_exp_f64(double x)
 /* Exported for the oracle's own tests of the exponential. */
 float oracle_expf(float x) { return oracle_exp_f32(x); }
 double oracle_exp(double x) { return oracle_exp_f64(x); }
+
+/* The exponential over an array (y[j] = exp(x[j])), for bitwise comparisons of many arguments. */
+void oracle_expf_array(const float* x, float* y, int64_t n)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < n; j++) y[j] = oracle_exp_f32(x[j]);
+}
+
+void oracle_exp_array(const double* x, double* y, int64_t n)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < n; j++) y[j] = oracle_exp_f64(x[j]);
+}
 
 #define T float
 #define ACC double

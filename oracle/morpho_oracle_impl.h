@@ -347,22 +347,30 @@ int FN(oracle_smorph_backward)(int merge, const T* x, const T* wt, const T* alph
     const int64_t wnumel = Cout * Cw * taps;
     const int64_t anumel = identity ? Cout : Cout * Cin;
 
-    ACC* gx_acc = (ACC*)calloc((size_t)(B * Cin * plane), sizeof(ACC));
+    const int nthreads = omp_get_max_threads();
+    const int64_t gx_numel = B * Cin * plane;
+    /* One grad_input accumulator per thread: the (b, o) units of different threads add to the same
+     * input pixels. Summed in thread order at the end. */
+    ACC* gx_thr = (ACC*)calloc((size_t)(nthreads * gx_numel), sizeof(ACC));
     ACC* gw_part = (ACC*)calloc((size_t)(B * wnumel), sizeof(ACC));
     ACC* ga_part = (ACC*)calloc((size_t)(B * anumel), sizeof(ACC));
-    if (!gx_acc || !gw_part || !ga_part) return 2;
+    if (!gx_thr || !gw_part || !ga_part) return 2;
 
 #pragma omp parallel
     {
         T* exps = (T*)malloc((size_t)taps * sizeof(T));
         T* outs = (T*)malloc((size_t)Cin * sizeof(T));
-#pragma omp for schedule(dynamic)
+        ACC* gx_acc = gx_thr + (int64_t)omp_get_thread_num() * gx_numel;
+#pragma omp for collapse(2) schedule(dynamic)
         for (int64_t b = 0; b < B; b++)
         {
+          for (int64_t o_unit = 0; o_unit < Cout; o_unit++)
+          {
+            /* grad_weight and grad_alpha of the pairs of output channel o_unit belong to this unit alone. */
             ACC* gw = gw_part + b * wnumel;
             ACC* ga = ga_part + b * anumel;
-            for (int64_t o = 0; o < Cout; o++)
             {
+                const int64_t o = o_unit;
                 for (int64_t h = 0; h < H; h++)
                 {
                     int64_t kh_begin = h + pad_h - (H - 1);
@@ -434,12 +442,18 @@ int FN(oracle_smorph_backward)(int merge, const T* x, const T* wt, const T* alph
                     }
                 }
             }
+          }
         }
         free(exps);
         free(outs);
     }
 
-    for (int64_t j = 0; j < B * Cin * plane; j++) grad_in[j] = (T)gx_acc[j];
+    for (int64_t j = 0; j < gx_numel; j++)
+    {
+        ACC sx = 0;
+        for (int t = 0; t < nthreads; t++) sx += gx_thr[(int64_t)t * gx_numel + j];
+        grad_in[j] = (T)sx;
+    }
     for (int64_t j = 0; j < wnumel; j++)
     {
         ACC s = 0;
@@ -452,7 +466,7 @@ int FN(oracle_smorph_backward)(int merge, const T* x, const T* wt, const T* alph
         for (int64_t b = 0; b < B; b++) s += ga_part[b * anumel + j];
         grad_alpha[j] = (T)s;
     }
-    free(gx_acc);
+    free(gx_thr);
     free(gw_part);
     free(ga_part);
     return 0;
@@ -537,24 +551,32 @@ int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, cons
     const int64_t wnumel = Cout * Cw * taps;
     const int64_t anumel = Cout * Cin;
 
-    ACC* gx_acc = (ACC*)calloc((size_t)(B * Cin * plane), sizeof(ACC));
+    const int nthreads = omp_get_max_threads();
+    const int64_t gx_numel = B * Cin * plane;
+    /* One grad_input accumulator per thread: the (b, o) units of different threads add to the same
+     * input pixels. Summed in thread order at the end. */
+    ACC* gx_thr = (ACC*)calloc((size_t)(nthreads * gx_numel), sizeof(ACC));
     ACC* gw_part = (ACC*)calloc((size_t)(B * wnumel), sizeof(ACC));
     ACC* ga_part = (ACC*)calloc((size_t)(B * anumel), sizeof(ACC));
     ACC* gb_part = (ACC*)calloc((size_t)(B * Cout), sizeof(ACC));
-    if (!gx_acc || !gw_part || !ga_part || !gb_part) return 2;
+    if (!gx_thr || !gw_part || !ga_part || !gb_part) return 2;
 
 #pragma omp parallel
     {
         T* exps = (T*)malloc((size_t)taps * sizeof(T));
         T* outs = (T*)malloc((size_t)Cin * sizeof(T));
-#pragma omp for schedule(dynamic)
+        ACC* gx_acc = gx_thr + (int64_t)omp_get_thread_num() * gx_numel;
+#pragma omp for collapse(2) schedule(dynamic)
         for (int64_t b = 0; b < B; b++)
         {
+          for (int64_t o_unit = 0; o_unit < Cout; o_unit++)
+          {
+            /* grad_weight and grad_alpha of the pairs of output channel o_unit belong to this unit alone. */
             ACC* gw = gw_part + b * wnumel;
             ACC* ga = ga_part + b * anumel;
             ACC* gb = gb_part + b * Cout;
-            for (int64_t o = 0; o < Cout; o++)
             {
+                const int64_t o = o_unit;
                 const T bt = beta[o];
                 for (int64_t h = 0; h < H; h++)
                 {
@@ -613,12 +635,18 @@ int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, cons
                     }
                 }
             }
+          }
         }
         free(exps);
         free(outs);
     }
 
-    for (int64_t j = 0; j < B * Cin * plane; j++) grad_in[j] = (T)gx_acc[j];
+    for (int64_t j = 0; j < gx_numel; j++)
+    {
+        ACC sx = 0;
+        for (int t = 0; t < nthreads; t++) sx += gx_thr[(int64_t)t * gx_numel + j];
+        grad_in[j] = (T)sx;
+    }
     for (int64_t j = 0; j < wnumel; j++)
     {
         ACC s = 0;
@@ -637,7 +665,7 @@ int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, cons
         for (int64_t b = 0; b < B; b++) s += gb_part[b * Cout + o];
         grad_beta[o] = (T)s;
     }
-    free(gx_acc);
+    free(gx_thr);
     free(gw_part);
     free(ga_part);
     free(gb_part);

@@ -69,6 +69,10 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_expf.restype = ctypes.c_float
         _lib.oracle_exp.argtypes = [ctypes.c_double]
         _lib.oracle_exp.restype = ctypes.c_double
+        _lib.oracle_expf_array.argtypes = [p, p, i64]
+        _lib.oracle_expf_array.restype = None
+        _lib.oracle_exp_array.argtypes = [p, p, i64]
+        _lib.oracle_exp_array.restype = None
     return _lib
 
 
@@ -342,3 +346,12 @@ class brute:
         e = np.where(ok, np.exp((v - ref) * alpha), 0)
         S = e.sum(axis=0)
         return (e * v).sum(axis=0) / S
+
+
+def exp_array(x):
+    """The reference's vector exponential (morpho_cpu_simd.hpp:127-169) over a float32 / float64 array."""
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    fn = lib().oracle_expf_array if x.dtype == np.float32 else lib().oracle_exp_array
+    fn(_ptr(x), _ptr(y), x.size)
+    return y

@@ -597,27 +597,28 @@ def test_config2_erosion_sum(variant):
 
 @pytest.mark.parametrize("a", [-20.0, -1.0, 0.0, 1.0, 20.0])
 def test_config3_smorph_mean(a):
-    """configs[2] at (1,16,64,64), w (16,16,7,7) ~N(0,0.1), alpha = full(a)."""
-    x = seeded(0, 1, 16, 64, 64, kind="randn")
-    w = seeded(1, 16, 16, 7, 7, kind="randn", scale=0.1)
-    alpha = torch.full((16, 16), a)
+    """configs[2] with its channel counts, Cin = Cout = 64, at a small image (1, 64, 24, 70): w (64,64,7,7)
+    ~N(0,0.1), alpha = full(a)."""
+    x = seeded(0, 1, 64, 24, 70, kind="randn")
+    w = seeded(1, 64, 64, 7, 7, kind="randn", scale=0.1)
+    alpha = torch.full((64, 64), a)
     wt = torch.from_numpy(O.smorph_w_tilde(w.numpy(), alpha.numpy(), "mean"))
-    g = seeded(2, 1, 16, 64, 64, kind="randn")
+    g = seeded(2, 1, 64, 24, 70, kind="randn")
     for actual, expected in _smorph_case("mean", x, wt, alpha, g):
         assert normwise_error(actual, expected) <= 1e-6
 
 
 def test_config4_dilation_identity_f64():
-    """configs[3] at (2,16,56,56) float64, identity, w (16,1,3,3) ~N(0,0.1); the literal
-    (C,C,3,3) weight is rejected as by the reference."""
-    x = seeded(0, 2, 16, 56, 56, dtype=torch.float64, low=-1.0, scale=2.0)
-    w = seeded(1, 16, 1, 3, 3, dtype=torch.float64, kind="randn", scale=0.1)
-    g = seeded(2, 2, 16, 56, 56, dtype=torch.float64, kind="randn")
+    """configs[3] with its 128 channels at (4,128,112,112) float64, identity, w (128,1,3,3) ~N(0,0.1);
+    the literal (C,C,3,3) weight is rejected as by the reference."""
+    x = seeded(0, 4, 128, 112, 112, dtype=torch.float64, low=-1.0, scale=2.0)
+    w = seeded(1, 128, 1, 3, 3, dtype=torch.float64, kind="randn", scale=0.1)
+    g = seeded(2, 4, 128, 112, 112, dtype=torch.float64, kind="randn")
     out, ref, gx, rgx, gw, rgw = _backward_case(O.DILATION, "identity", "replicate", torch.float64, x, w, g)
     assert np.array_equal(out, ref)
     assert normwise_error(gx, rgx) <= 1e-12 and normwise_error(gw, rgw) <= 1e-12
     with pytest.raises(RuntimeError, match="Identity mode requires weight.shape\\[1\\] == 1"):
-        torch.ops.morphocore.dilation(x.cuda(), torch.zeros(16, 16, 3, 3, dtype=torch.float64, device="cuda"), 5, 3, 0.0, True, 0.0)
+        torch.ops.morphocore.dilation(x.cuda(), torch.zeros(128, 128, 3, 3, dtype=torch.float64, device="cuda"), 5, 3, 0.0, True, 0.0)
 
 
 def test_config5_stack_reduced():
@@ -634,7 +635,9 @@ def test_config5_stack_reduced():
     wd = [w.to(dev).requires_grad_(True) for w in ws]
     ad = alpha.to(dev).requires_grad_(True)
     y1 = mca.functional.dilation(xd, wd[0], "max", "replicate")
+    y1.retain_grad()
     y2 = mca.functional.smorph(y1, wd[1], ad, channel_merge_mode="sum")
+    y2.retain_grad()
     y3 = mca.functional.erosion(y2, wd[2], "min", "replicate")
     y3.backward(g.to(dev))
     # Oracle, layer by layer, with the GPU's own intermediate activations as inputs so that each
@@ -647,9 +650,22 @@ def test_config5_stack_reduced():
     w3f = np.ascontiguousarray(ws[2].flip((-2, -1)).numpy())
     r3, i3 = O.morpho_forward(O.EROSION, O.MIN, O.REPLICATE, 0.0, _np(y2), w3f, save_indices=True)
     assert np.array_equal(_np(y3), r3)
+    # Backward, layer by layer from the top, each layer fed the GPU's own output gradient.
     gy2, gw3f = O.morpho_backward(O.EROSION, O.MIN, O.REPLICATE, 0.0, _np(y2), w3f, g.numpy(), indices=i3)
     assert normwise_error(_np(wd[2].grad), gw3f[:, :, ::-1, ::-1]) <= 1e-6
-    assert np.isfinite(_np(xd.grad)).all() and np.isfinite(_np(wd[0].grad)).all() and np.isfinite(_np(ad.grad)).all()
+    assert normwise_error(_np(y2.grad), gy2) <= 1e-6
+    gy1, gwt, ga_direct = O.smorph_backward(O.ADD, _np(y1), wt, alpha.numpy(), _np(y2.grad))
+    assert normwise_error(_np(y1.grad), gy1) <= 1e-6
+    # w~ -> (w1, alpha) through torch on the CPU (functional/smorph.py:56-70), plus alpha's direct term.
+    w1c, ac = ws[1].clone().requires_grad_(True), alpha.clone().requires_grad_(True)
+    t = torch.tanh(ac).unsqueeze(-1).unsqueeze(-1)
+    wtt = t * ((1 - t) / 2 * w1c.flip(dims=(-2, -1)) + (1 + t) / 2 * w1c)
+    torch.autograd.backward([wtt, ac], [torch.from_numpy(gwt), torch.from_numpy(ga_direct)])
+    assert normwise_error(_np(wd[1].grad), w1c.grad.numpy()) <= 1e-6
+    assert normwise_error(_np(ad.grad), ac.grad.numpy()) <= 1e-6
+    gx, gw0 = O.morpho_backward(O.DILATION, O.MAX, O.REPLICATE, 0.0, x.numpy(), ws[0].numpy(), _np(y1.grad), indices=i1)
+    assert normwise_error(_np(xd.grad), gx) <= 1e-6
+    assert normwise_error(_np(wd[0].grad), gw0) <= 1e-6
 
 
 # ------------------------------------------------------------------------------------------------
@@ -707,6 +723,10 @@ def test_smorph_large_grid_saved_matches_recomputed(merge, K, a, monkeypatch):
         assert normwise_error(s_, r_) <= 1e-6
     ref = O.smorph_forward(O.MERGES[merge], x[:1].numpy(), w.numpy(), alpha.numpy())
     assert normwise_error(saved[0][:1], ref) <= 1e-6
+    # grad_input of batch element 0 depends on that element alone: the oracle's batch-1 backward.
+    rgx, _, _ = O.smorph_backward(O.MERGES[merge], x[:1].numpy(), w.numpy(), alpha.numpy(), g[:1].numpy())
+    assert normwise_error(saved[1][:1], rgx) <= 1e-6
+    assert normwise_error(recomputed[1][:1], rgx) <= 1e-6
 
 
 # ------------------------------------------------------------------------------------------------
