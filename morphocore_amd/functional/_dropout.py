@@ -1,0 +1,24 @@
+"""Weight dropout of the dilation and erosion functionals (reference: functional/dilation.py:78-87,
+functional/erosion.py:78-87).
+
+The reference draws ``rand_like(w) > p``, then walks the (out, in) channel pairs in order and, for
+each pair left without a surviving tap, draws one ``randint(0, taps, (1,))`` on the default CPU
+generator and keeps that tap; on a GPU every pair's ``.any()`` is a host synchronisation. Here the
+pairs without a survivor are found in one pass and their taps drawn in one ``randint`` of as many
+values, in the same pair order: the CPU generator produces the same values for one call of n draws as
+for n calls of one, so a seeded run keeps exactly the reference's taps, with one host synchronisation.
+"""
+import torch
+
+
+def dropout_keep(w: torch.Tensor, p: float) -> torch.Tensor:
+    """Boolean mask of the taps of ``w`` that survive weight dropout with probability ``p``; at least
+    one tap of every (out, in) pair (dims 0 and 1) survives."""
+    keep = torch.rand_like(w) > p
+    rows = keep.reshape(w.shape[0] * w.shape[1], -1)  # a view: rand_like's result is contiguous
+    dead = ~rows.any(dim=1)
+    n_dead = int(dead.sum())  # the one host synchronisation
+    if n_dead:
+        taps = torch.randint(0, rows.shape[1], (n_dead,))
+        rows[dead.nonzero().squeeze(1), taps.to(rows.device)] = True
+    return keep

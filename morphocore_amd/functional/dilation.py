@@ -1,5 +1,6 @@
 import torch
 
+from ._dropout import dropout_keep
 from ._ops import ops
 from .merge_enum import str_to_merge, str_to_padding
 
@@ -31,14 +32,9 @@ def dilation(x: torch.Tensor, w: torch.Tensor, channel_merge_mode: str = 'sum', 
     torch.Tensor of shape [N, C_out, H, W] (the input's rank is kept).
     """
     if training and weight_dropout > 0.0:
-        # The dropout draw and its one-survivor rule, in the reference's order (dilation.py:78-87), so
-        # that seeded runs drop the same taps.
-        keep = torch.rand_like(w) > weight_dropout
-        for i in range(w.shape[0]):
-            for j in range(w.shape[1]):
-                if not keep[i, j].any():
-                    flat = torch.randint(0, keep[i, j].numel(), (1,)).item()
-                    keep[i, j].view(-1)[flat] = True
+        # The reference's draws and one-survivor rule, in its order (dilation.py:78-87), so that seeded
+        # runs drop the same taps; one host synchronisation instead of one per channel pair.
+        keep = dropout_keep(w, weight_dropout)
         w = torch.where(keep, w, torch.tensor(-float('inf'), device=w.device, dtype=w.dtype))
 
     return ops.dilation(x, w, str_to_merge(channel_merge_mode), str_to_padding(padding_mode), padding_value, save_indices,

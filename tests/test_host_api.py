@@ -124,3 +124,36 @@ def test_saved_statistics_admission_rule():
             avail -= 30 * GB
         avail -= 10 * GB  # the layer's output
     assert admitted == [True, True, False]
+
+
+def _reference_dropout_loop(w, p):
+    """The reference's loop (functional/dilation.py:78-87), for comparison."""
+    keep = torch.rand_like(w) > p
+    for i in range(w.shape[0]):
+        for j in range(w.shape[1]):
+            if not keep[i, j].any():
+                flat = torch.randint(0, keep[i, j].numel(), (1,)).item()
+                keep[i, j].view(-1)[flat] = True
+    return keep
+
+
+@pytest.mark.parametrize("shape,p", [((4, 3, 3, 3), 0.9), ((8, 8, 5, 5), 0.97), ((3, 1, 3, 5), 0.999), ((5, 4, 1, 1), 0.5),
+                                     ((16, 16, 7, 7), 0.995), ((3, 5), 0.6)])
+def test_dropout_mask_matches_the_reference_loop(shape, p):
+    """One pass + one randint of n draws keeps exactly the taps of the reference's per-pair loop, seed
+    for seed (the generator yields the same values for one call of n draws as for n calls of one), and
+    leaves the generator in the same state."""
+    from morphocore_amd.functional._dropout import dropout_keep
+
+    w = torch.randn(*shape)
+    for seed in range(5):
+        torch.manual_seed(seed)
+        ref = _reference_dropout_loop(w, p)
+        after_ref = torch.rand(3)
+        torch.manual_seed(seed)
+        got = dropout_keep(w, p)
+        after_got = torch.rand(3)
+        assert torch.equal(got, ref)
+        assert torch.equal(after_got, after_ref)
+        rows = got.reshape(shape[0] * shape[1], -1)
+        assert bool(rows.any(dim=1).all())
