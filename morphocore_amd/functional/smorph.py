@@ -21,7 +21,9 @@ def smorph(x: torch.Tensor, w: torch.Tensor, alpha: torch.Tensor, beta: torch.Te
     x : [N, C_in, H, W] input on a HIP device, float32 or float64.
     w : [C_out, C_in, K_h, K_w] structuring element ([C, 1, K_h, K_w] for 'identity').
     alpha : [C_out, C_in] (or [C_out] / [C, 1] for 'identity'), or a single value shared by all pairs.
-    beta : selects the SMOOTH channel merge (smorph_scm), which this package does not provide.
+    beta : [C_out], one value per output channel: selects the SMOOTH channel merge (the smorph_scm
+        operator), a soft extremum of the pair outputs with temperature beta (max-like for beta > 0,
+        min-like for beta < 0, their mean at 0); ``channel_merge_mode`` is then ignored.
     channel_merge_mode : 'sum', 'mean', 'max', 'min' or 'identity'.
     """
     if channel_merge_mode == 'identity' or alpha.dim() == 1:

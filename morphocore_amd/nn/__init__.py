@@ -1,8 +1,11 @@
 """Layers (reference: morphocore/nn/__init__.py)."""
 from .dilation import Dilation
 from .erosion import Erosion
+from .opening import Opening
+from .closing import Closing
+from .sigma_layer import SigmaLayer
 from .smorph import SMorph
 from .morpho_module import MorphoModule
 from .alpha_module import AlphaModule
 
-__all__ = ['Dilation', 'Erosion', 'SMorph', 'MorphoModule', 'AlphaModule']
+__all__ = ['Dilation', 'Erosion', 'Opening', 'Closing', 'SigmaLayer', 'SMorph', 'MorphoModule', 'AlphaModule']

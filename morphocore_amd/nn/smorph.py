@@ -11,7 +11,10 @@ class SMorph(AlphaModule):
     ``SMorph(in_channels, out_channels, kernel_size, channel_merge_mode='sum', init_alpha=0.0,
     dtype=torch.float32, init_beta=None)``: parameters ``weight`` (zeros), ``alpha`` (``init_alpha``)
     and, when ``init_beta`` is given, ``beta`` of shape (out_channels, in_channels), which selects the
-    SMOOTH channel merge (not provided by this package). Forward: :func:`morphocore_amd.functional.smorph`.
+    SMOOTH channel merge (the smorph_scm operator). As in the reference, the operator takes one beta per
+    output channel, so that shape runs only with in_channels == 1 (other widths raise "Beta must have
+    shape [out_channels]"); :func:`morphocore_amd.functional.smorph` takes a [C_out] beta directly.
+    Forward: :func:`morphocore_amd.functional.smorph`.
     """
 
     def __init__(self, in_channels: int, out_channels: int, kernel_size: tuple, channel_merge_mode: str = "sum",

@@ -157,3 +157,20 @@ def test_dropout_mask_matches_the_reference_loop(shape, p):
         assert torch.equal(after_got, after_ref)
         rows = got.reshape(shape[0] * shape[1], -1)
         assert bool(rows.any(dim=1).all())
+
+
+def test_composition_layers_construction():
+    """Opening / Closing share one structuring element by default, which needs equal channel counts
+    and the identity merge (reference nn/opening.py:104-140 messages); SigmaLayer has weight and
+    alpha."""
+    o = mca.nn.Opening(3, 3, 5)
+    assert o.erosion.weight is o.dilation.weight and len(list(o.parameters())) == 1
+    c = mca.nn.Closing(3, 8, 5, share_weights=False)
+    assert len(list(c.parameters())) == 2 and c.dilation.channel_merge_mode == "sum"
+    with pytest.raises(ValueError, match="in_channels == out_channels"):
+        mca.nn.Opening(3, 8, 5)
+    with pytest.raises(ValueError, match="channel_merge_mode='identity'"):
+        mca.nn.Closing(3, 3, 5, channel_merge_mode="sum")
+    s = mca.nn.SigmaLayer(3, 4, 3)
+    assert [tuple(p.shape) for p in s.parameters()] == [(4, 3, 3, 3), (4, 3)]
+    assert set(mca.functional.__all__) >= {"opening", "closing", "sigma_layer"}
