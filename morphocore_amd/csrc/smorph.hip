@@ -287,7 +287,13 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
                         // (so that a NaN of the pair reaches the gradients, as in the reference).
                         if (!in[r] || !tap_in_image(iy0 + r, ix, kh, kw, g)) continue;
                         const T v = tbase[(r - kh) * t.pitch - kw] + wk;
-                        const T e = exp_ref((v - ref[r]) * a, lo);
+                        // The routing's exponential: the hardware one in float32 (the sums above,
+                        // and so the output, use the reference's).
+                        T e;
+                        if constexpr (sizeof(T) == 4)
+                            e = exp_route((v - ref[r]) * a);
+                        else
+                            e = exp_ref((v - ref[r]) * a, lo);
                         const T pg = e * scaled[r];
                         const T centered = v - outp[r];
                         const T c = fma(a * pg, centered, pg);

@@ -152,6 +152,16 @@ __device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
     return under ? T(0) : e;
 }
 
+// exp(x) for the routing of gradients only, from the hardware base-2 exponential (v_exp_f32, one
+// transcendental instruction) of x log2(e): relative error about 1.2e-7 (the instruction's) plus
+// |x| 7.5e-8 (the rounding of the product and of log2(e)), i.e. within 5e-7 wherever e > 1e-3, and a
+// far smaller absolute error below. The routing scales each e by 1 / S (S >= 1 holds the extremum's
+// e = 1), so gradients move by a few 1e-7 of their size at most: inside the 1e-6 contract. Never used
+// where S, W or the output are formed: those need the reference's exponential bit for bit (exp_ref),
+// since the gradients amplify an output's rounding by alpha. -inf gives 0 and NaN gives NaN, as
+// exp_ref; 2^x below the normal range may give a subnormal where exp_ref gives 0.
+__device__ __forceinline__ float exp_route(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+
 // Whether a wave-uniform alpha is zero (+0 or -0), as a scalar condition (a branch, not a mask).
 __device__ __forceinline__ bool alpha_is_zero(float a)
 {

@@ -413,7 +413,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             float ekr;
             if (k >= KE)
             {
-                ekr = exp_ref(MASKED ? (vk - ref) * a - tm.pen[kw] : (vk - ref) * a, lo);
+                ekr = exp_route(MASKED ? (vk - ref) * a - tm.pen[kw] : (vk - ref) * a);
             }
             else
             {
@@ -698,7 +698,7 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
         const float vk = x + wl[k];
         const float arg = MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a;
-        const float ek = ZA ? exp_ref_zero_alpha(arg, lo) : exp_ref(arg, lo);
+        const float ek = ZA ? exp_ref_zero_alpha(arg, lo) : exp_route(arg);
         const float pg = ek * P.scaled;
         const float centered = vk - P.outc;
         float c = fmaf(a * pg, centered, pg);
