@@ -162,6 +162,22 @@ __device__ __forceinline__ T exp_ref(T x, T lo = ExpConsts<T>::min_input)
 // exp_ref; 2^x below the normal range may give a subnormal where exp_ref gives 0.
 __device__ __forceinline__ float exp_route(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
 
+// exp_ref for an argument known to be at or above its lower threshold (or NaN): the same bits
+// without the final select.
+template <typename T>
+__device__ __forceinline__ T exp_ref_above(T x)
+{
+    using C = ExpConsts<T>;
+    using Bits = typename C::Bits;
+    constexpr T magic = C::magic + T(C::bias + 1);
+    const T nm = fma(x, C::log2e, magic);
+    const T n = nm - magic;
+    const T r = fma(-n, C::ln2_lo, fma(-n, C::ln2_hi, x));
+    const T ph = horner_half<T, 0>(r);
+    const T scale = __builtin_bit_cast(T, (Bits)((uint64_t)__builtin_bit_cast(Bits, nm) << C::mant));
+    return ph * scale;
+}
+
 // Whether a wave-uniform alpha is zero (+0 or -0), as a scalar condition (a branch, not a mask).
 __device__ __forceinline__ bool alpha_is_zero(float a)
 {

@@ -47,6 +47,7 @@ struct TapMask
 {
     unsigned rows;
     float pen[KW];
+    float keep[KW];  // 1 in the image, 0 outside
 
     __device__ __forceinline__ void init(const Geom& g, int h, int wc)
     {
@@ -63,6 +64,7 @@ struct TapMask
         {
             const int c = wc + KW / 2 - kw;
             pen[kw] = c >= 0 && c < g.W ? 0.0f : std::numeric_limits<float>::infinity();
+            keep[kw] = c >= 0 && c < g.W ? 1.0f : 0.0f;
         }
     }
     __device__ __forceinline__ bool row(int kh) const { return (rows >> kh) & 1u; }
@@ -108,6 +110,51 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
     return ref;
 }
 
+// Pass 1 of a pair on an interior tile: the extremum `ref` (as smorph_ref) and the opposite one,
+// `far`, so that (far - ref) * a bounds every tap's exponential argument from below (the taps round
+// (v - ref) * a the same way, and rounding is monotone).
+// MASKED: ref over the in-image taps only (as smorph_ref), far over every tap of the in-image rows,
+// the out-of-image columns included (their staged x is 0): it bounds the arguments of all the taps
+// the sums evaluate.
+template <int KH, int KW, bool MASKED>
+__device__ __forceinline__ float smorph_ref_far(const float* xb, const float* wl, bool dil, const TapMask<KH, KW>& tm, float& far)
+{
+    constexpr int COLS = TILE_W + KW - 1;
+    float ref = smorph_init(dil), opp = smorph_init(!dil);
+    if (dil)
+    {
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+        {
+            if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw)
+            {
+                const float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+                ref = fmaxf(ref, MASKED ? v - tm.pen[kw] : v);
+                opp = fminf(opp, v);
+            }
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+        {
+            if (MASKED && !tm.row(kh)) continue;
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw)
+            {
+                const float v = xb[-(kh * COLS + kw)] + wl[kh * KW + kw];
+                ref = fminf(ref, MASKED ? v + tm.pen[kw] : v);
+                opp = fmaxf(opp, v);
+            }
+        }
+    }
+    far = opp;
+    return ref;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------
@@ -117,7 +164,10 @@ __device__ __forceinline__ float smorph_ref(const float* xb, const float* wl, bo
 
 // Pass 2 of a pair: S and W in tap order (kh, then kw), W fused as in the reference's AVX2 build.
 // ZA: the pair's alpha is zero (every e is 1 on an in-image tap of finite v).
-template <int KH, int KW, bool MASKED, bool ZA>
+// SAFE: no tap's argument lies below the exponential's lower threshold and every v is finite (checked
+// by the caller for the whole wave): exp_ref's final select never fires and is left out, and with
+// ZA every e is exactly 1 (S counts the taps, W sums the v).
+template <int KH, int KW, bool MASKED, bool ZA, bool SAFE = false>
 __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, float a, float ref, const TapMask<KH, KW>& tm, float& S, float& Wsum)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
@@ -136,6 +186,23 @@ __device__ __forceinline__ void smorph_sums(const float* xb, const float* wl, fl
             // An out-of-image tap adds e = 0 (its staged x is 0, so v and the argument are finite, and
             // the argument less +inf is -inf): S + 0 and fma(0, v, W) leave both sums exactly as
             // skipping it does.
+            if constexpr (SAFE && ZA)
+            {
+                // e = 1 in the image, 0 outside: S + e and fma(e, v, W) with one rounding each.
+                s = s + (MASKED ? tm.keep[kw] : 1.0f);
+                wsum = MASKED ? fmaf(tm.keep[kw], v, wsum) : wsum + v;
+                continue;
+            }
+            if constexpr (SAFE)
+            {
+                // Every argument lies at or above the threshold and is finite; an out-of-image tap's e
+                // is multiplied by 0 (exactly 0: its v is finite).
+                const float ef = exp_ref_above((v - ref) * a);
+                const float e = MASKED ? ef * tm.keep[kw] : ef;
+                s = s + e;
+                wsum = fmaf(e, v, wsum);
+                continue;
+            }
             const float arg = MASKED ? (v - ref) * a - tm.pen[kw] : (v - ref) * a;
             const float e = ZA ? exp_ref_zero_alpha(arg, lo) : exp_ref(arg, lo);
             s = s + e;  // unfused, as in the reference (e is rounded before the sum)
@@ -236,21 +303,62 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         const bool dil = a >= 0.0f;
         const bool za = alpha_is_zero(a);
         float ref, S, Wsum;
+        // Every lane's smallest argument at or above the exponential's threshold and every v finite
+        // (ref and far finite): the wave takes the select-free sums, bit for bit the same.
+        auto safe_wave = [&](float far) {
+            const float bound = (far - ref) * a;
+            const bool ok = bound >= ExpConsts<float>::min_input && fabsf(far) <= 3.40282347e38f && fabsf(ref) <= 3.40282347e38f;
+            return __builtin_amdgcn_uicmp((unsigned)!ok, 0u, 33) == 0;  // no lane fails
+        };
         if (interior)
         {
-            ref = smorph_ref<KH, KW, false>(xb, w, dil, tm);
+            float far;
+            ref = smorph_ref_far<KH, KW, false>(xb, w, dil, tm, far);
+            const bool safe = safe_wave(far);
             if (za)
-                smorph_sums<KH, KW, false, true>(xb, w, a, ref, tm, S, Wsum);
+            {
+                if (safe)
+                    smorph_sums<KH, KW, false, true, true>(xb, w, a, ref, tm, S, Wsum);
+                else
+                    smorph_sums<KH, KW, false, true>(xb, w, a, ref, tm, S, Wsum);
+            }
             else
-                smorph_sums<KH, KW, false, false>(xb, w, a, ref, tm, S, Wsum);
+            {
+                if (safe)
+                    smorph_sums<KH, KW, false, false, true>(xb, w, a, ref, tm, S, Wsum);
+                else
+                    smorph_sums<KH, KW, false, false>(xb, w, a, ref, tm, S, Wsum);
+            }
         }
-        else
+        else if constexpr (KW > 7)
         {
+            // 11x11: the border tiles keep the select (the keep factors of the select-free masked sums
+            // spill registers there: 60 bytes per lane, measured 1.5% slower on configs[4]).
             ref = smorph_ref<KH, KW, true>(xb, w, dil, tm);
             if (za)
                 smorph_sums<KH, KW, true, true>(xb, w, a, ref, tm, S, Wsum);
             else
                 smorph_sums<KH, KW, true, false>(xb, w, a, ref, tm, S, Wsum);
+        }
+        else
+        {
+            float far;
+            ref = smorph_ref_far<KH, KW, true>(xb, w, dil, tm, far);
+            const bool safe = safe_wave(far);
+            if (za)
+            {
+                if (safe)
+                    smorph_sums<KH, KW, true, true, true>(xb, w, a, ref, tm, S, Wsum);
+                else
+                    smorph_sums<KH, KW, true, true>(xb, w, a, ref, tm, S, Wsum);
+            }
+            else
+            {
+                if (safe)
+                    smorph_sums<KH, KW, true, false, true>(xb, w, a, ref, tm, S, Wsum);
+                else
+                    smorph_sums<KH, KW, true, false>(xb, w, a, ref, tm, S, Wsum);
+            }
         }
         const float inv = 1.0f / S;
         if constexpr (STATS)

@@ -73,3 +73,27 @@ def test_smorph_generic_nan_input(dtype, KH, KW, merge):
     assert np.isnan(results[0][1]).any() == (merge != "max")
     for actual, expected in results:
         assert normwise_error(actual, expected) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("merge", MERGES)
+@pytest.mark.parametrize("K", [3, 5, 7, 11])
+def test_smorph_static_forward_bit_exact(K, merge):
+    """The float32 static forward equals the oracle bit for bit, on interior and border tiles, for
+    pairs whose window passes the bound that drops the exponential's underflow select (small |alpha|,
+    alpha = 0) and pairs that keep it (|alpha| = 20 on N(0, 1) data, a NaN-free input with -87 below
+    the bound), and an input with +inf (never on the select-free path)."""
+    B, Cin, Cout, H, W = 1, 3, 2, 22, 200
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(141, B, Cin, H, W, kind="randn")
+    w = seeded(142, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
+    pairs = Cout if merge == "identity" else Cout * Cin
+    for alphas in ([0.0, 0.7, -2.0, 3.0, 20.0, -20.0], [20.0, -20.0, 0.5, 0.0, -0.5, 9.0]):
+        alpha = torch.tensor([alphas[p % len(alphas)] for p in range(pairs)]).reshape((Cout,) if merge == "identity" else (Cout, Cin))
+        for xin in (x, torch.where(torch.arange(W) == 130, torch.tensor(float("inf")), x)):
+            import morphocore_amd  # noqa: F401
+
+            with torch.no_grad():
+                out = torch.ops.morphocore.smorph(xin.cuda(), w.cuda(), alpha.cuda(), O.MERGES[merge]).cpu().numpy()
+            ref = O.smorph_forward(O.MERGES[merge], xin.numpy(), w.numpy(), alpha.numpy())
+            assert np.array_equal(out, ref, equal_nan=True), (alphas, float(np.nanmax(np.abs(out - ref))))
