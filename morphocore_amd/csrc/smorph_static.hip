@@ -803,10 +803,16 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     float halo[HREGS];
 #pragma unroll
     for (int r = 0; r < HREGS; ++r) halo[r] = 0.0f;
+    // alpha log2(e) once per pair, in a vector register: each tap's exponential is 2^((v - ref) a2).
+    float a2 = a * 1.44269504088896340736f;
+    asm volatile("" : "+v"(a2));
     auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
         const float vk = x + wl[k];
-        const float arg = MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a;
-        const float ek = ZA ? exp_ref_zero_alpha(arg, lo) : exp_route(arg);
+        float ek;
+        if constexpr (ZA)
+            ek = exp_ref_zero_alpha(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
+        else
+            ek = __builtin_amdgcn_exp2f(MASKED ? (vk - P.ref) * a2 - pen[kw] : (vk - P.ref) * a2);  // exp_route, log2(e) folded
         const float pg = ek * P.scaled;
         const float centered = vk - P.outc;
         float c = fmaf(a * pg, centered, pg);
