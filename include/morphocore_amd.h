@@ -191,6 +191,41 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                 double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Opening / closing with 'identity' merges in one pass (x to the final output per tile; the
+ * intermediate image stays in on-chip memory). Replaces the two operator calls of
+ * morphocore/functional/opening.py:96-101 (erosion, then dilation) and closing.py:96-101 (dilation,
+ * then erosion) when both stages merge per channel, the form nn/opening.py:104-180 and
+ * nn/closing.py build by default (one shared structuring element). first_op: MCA-level op of the first
+ * stage (1 = erosion: opening; 0 = dilation: closing). w_first / w_second: [C, 1, K, K] as each
+ * operator receives it (an erosion's element already flipped, as functional/erosion.py passes it), or
+ * one per batch element, weight_batch_stride apart. fill_first / fill_second: the border value each
+ * stage reads (its op's fill for the padding; unused with replicate). Output, tap by tap and value by
+ * value, that of the two separate IDENTITY launches; taps_first / taps_second receive each stage's
+ * first extremal tap per pixel ([B, C, H, W] bytes; both NULL when no backward follows). Square odd
+ * elements 3x3, 5x5, 7x7 only (mca_morpho_pair_supported); others: run the two separate launches. */
+int mca_morpho_pair_supported(int64_t KH, int64_t KW);
+int mca_morpho_pair_forward_f32(int first_op, int replicate, float fill_first, float fill_second, const float* input, const float* w_first,
+                                const float* w_second, int64_t weight_batch_stride, float* output, uint8_t* taps_first,
+                                uint8_t* taps_second, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+int mca_morpho_pair_forward_f64(int first_op, int replicate, double fill_first, double fill_second, const double* input,
+                                const double* w_first, const double* w_second, int64_t weight_batch_stride, double* output,
+                                uint8_t* taps_first, uint8_t* taps_second, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                int64_t KW, void* stream);
+
+/* Backward of mca_morpho_pair_forward from its saved taps: grad_input [B, C, H, W] and the gradient of
+ * each stage's element [C, 1, K, K] (in the frame the operator received it), all overwritten; the same
+ * routing as the two separate IDENTITY backwards (a tap that read outside the image sends nothing to
+ * its input; an element tap receives +g for a dilation, -g for an erosion). Workspace: the bytes
+ * mca_morpho_pair_backward_workspace_size_* returns (0: unsupported). */
+size_t mca_morpho_pair_backward_workspace_size_f32(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW);
+size_t mca_morpho_pair_backward_workspace_size_f64(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW);
+int mca_morpho_pair_backward_f32(int first_op, const uint8_t* taps_first, const uint8_t* taps_second, const float* grad_output,
+                                 float* grad_input, float* grad_w_first, float* grad_w_second, int64_t B, int64_t C, int64_t H, int64_t W,
+                                 int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_morpho_pair_backward_f64(int first_op, const uint8_t* taps_first, const uint8_t* taps_second, const double* grad_output,
+                                 double* grad_input, double* grad_w_first, double* grad_w_second, int64_t B, int64_t C, int64_t H,
+                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Test probe, no reference counterpart: y[j] = the exponential every smorph kernel evaluates, applied
  * to x[j] (n values, device pointers). It restates the reference's vector exponential
  * (morphocore/functional/csrc/cpp/morpho_cpu_simd.hpp:127-169) for the arguments the kernels pass,

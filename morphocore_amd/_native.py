@@ -43,6 +43,13 @@ EXPORTS = (
     "mca_smorph_scm_backward_workspace_size_f64",
     "mca_smorph_scm_backward_f32",
     "mca_smorph_scm_backward_f64",
+    "mca_morpho_pair_supported",
+    "mca_morpho_pair_forward_f32",
+    "mca_morpho_pair_forward_f64",
+    "mca_morpho_pair_backward_workspace_size_f32",
+    "mca_morpho_pair_backward_workspace_size_f64",
+    "mca_morpho_pair_backward_f32",
+    "mca_morpho_pair_backward_f64",
     "mca_probe_smorph_exp_f32",
     "mca_probe_smorph_exp_f64",
 )
@@ -61,7 +68,7 @@ def lib() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(
             f"morphocore_amd: native library {LIB_PATH} is not built; build it with "
-            "`make -C morphocore_amd/csrc` or `python -c 'import __graft_entry__ as g; g.build()'`"
+            "`python setup.py build_ext --inplace` or `python -c 'import __graft_entry__ as g; g.build()'`"
         )
     so = ctypes.CDLL(LIB_PATH)
     so.mca_version.restype = ctypes.c_char_p
@@ -101,6 +108,19 @@ def lib() -> ctypes.CDLL:
         f.restype = _I
         f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
         f.argtypes = [_P] * 11 + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+    _PGEOM = [_I64] * 6
+    so.mca_morpho_pair_supported.argtypes = [_I64, _I64]
+    so.mca_morpho_pair_supported.restype = _I
+    for sfx, real in (("f32", ctypes.c_float), ("f64", ctypes.c_double)):
+        f = getattr(so, f"mca_morpho_pair_forward_{sfx}")
+        f.argtypes = [_I, _I, real, real, _P, _P, _P, _I64, _P, _P, _P] + _PGEOM + [_P]
+        f.restype = _I
+        f = getattr(so, f"mca_morpho_pair_backward_workspace_size_{sfx}")
+        f.argtypes = list(_PGEOM)
+        f.restype = _SZ
+        f = getattr(so, f"mca_morpho_pair_backward_{sfx}")
+        f.argtypes = [_I, _P, _P, _P, _P, _P, _P] + _PGEOM + [_P, _SZ, _P]
         f.restype = _I
     so.mca_morpho_backward_noalloc_f32.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P]
     so.mca_morpho_backward_noalloc_f32.restype = _I
@@ -234,6 +254,28 @@ def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out
     f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
     _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w),
              _ptr(grad_alpha), _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def morpho_pair_supported(KH, KW) -> bool:
+    """Whether the fused opening / closing has kernels for this element (C ABI mca_morpho_pair_supported)."""
+    return bool(lib().mca_morpho_pair_supported(KH, KW))
+
+
+def morpho_pair_forward(first_op, replicate, fill_first, fill_second, x, w_first, w_second, weight_batch_stride, out, taps_first,
+                        taps_second, pgeom):
+    """Enqueue the fused opening / closing forward (C ABI mca_morpho_pair_forward_*); pgeom = (B, C, H, W, KH, KW)."""
+    f = getattr(lib(), f"mca_morpho_pair_forward_{_sfx(x)}")
+    _check(f(first_op, int(replicate), fill_first, fill_second, _ptr(x), _ptr(w_first), _ptr(w_second), weight_batch_stride, _ptr(out),
+             _ptr(taps_first), _ptr(taps_second), *pgeom, _stream(x)))
+
+
+def morpho_pair_backward(first_op, taps_first, taps_second, grad_out, grad_in, grad_w_first, grad_w_second, pgeom):
+    """Enqueue the fused opening / closing backward (C ABI mca_morpho_pair_backward_*), workspace from torch."""
+    so, sfx = lib(), _sfx(grad_out)
+    ws = _workspace(getattr(so, f"mca_morpho_pair_backward_workspace_size_{sfx}")(*pgeom), grad_out.device)
+    f = getattr(so, f"mca_morpho_pair_backward_{sfx}")
+    _check(f(first_op, _ptr(taps_first), _ptr(taps_second), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w_first), _ptr(grad_w_second), *pgeom,
+             _ptr(ws), ws.numel(), _stream(grad_out)))
 
 
 def probe_smorph_exp(x, y):

@@ -233,6 +233,54 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_noalloc_mutex;
 void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];
 
+// Geometry of the fused opening / closing entry points: C channels, identity merges, a supported
+// square element.
+int make_pair_geom(int first_op, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t wbs, mca::Geom& g)
+{
+    if (first_op != mca::DILATION && first_op != mca::EROSION) return fail("Unknown morphological operation " + std::to_string(first_op));
+    int rc = make_geom(mca::MERGE_IDENTITY, B, C, C, 1, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if (!mca::morpho_pair_supported(g)) return fail("The fused opening / closing takes square 3x3, 5x5 or 7x7 structuring elements");
+    // Its tiles are 64 - (K - 1) columns by 16 rows.
+    if (B * C * ((W + mca::TILE_W - KW) / (mca::TILE_W - KW + 1)) * ((H + 15) / 16) > 0x7fffffff) return fail("Problem too large for one launch");
+    return MCA_OK;
+}
+
+template <typename T>
+int pair_forward_impl(int first_op, int replicate, T fill1, T fill2, const T* input, const T* w1, const T* w2, int64_t wbs, T* output,
+                      uint8_t* taps1, uint8_t* taps2, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_pair_geom(first_op, B, C, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if ((taps1 == nullptr) != (taps2 == nullptr)) return fail("taps_first and taps_second must both be given or both be NULL");
+    return hip_status(mca::morpho_pair_forward<T>(first_op, replicate != 0, fill1, fill2, input, w1, w2, output, taps1, taps2, g,
+                                                  (hipStream_t)stream));
+}
+
+template <typename T>
+size_t pair_workspace_impl(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_pair_geom(mca::EROSION, B, C, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return mca::morpho_pair_backward_workspace<T>(g);
+}
+
+template <typename T>
+int pair_backward_impl(int first_op, const uint8_t* taps1, const uint8_t* taps2, const T* grad_output, T* grad_input, T* grad_w1,
+                       T* grad_w2, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace,
+                       size_t workspace_bytes, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_pair_geom(first_op, B, C, H, W, KH, KW, 0, g);
+    if (rc != MCA_OK) return rc;
+    if (!taps1 || !taps2) return fail("The fused opening / closing backward needs both stages' saved taps");
+    const size_t need = mca::morpho_pair_backward_workspace<T>(g);
+    if ((rc = check_workspace(workspace_bytes, need, workspace)) != MCA_OK) return rc;
+    return hip_status(mca::morpho_pair_backward<T>(first_op, taps1, taps2, grad_output, grad_input, grad_w1, grad_w2, g, workspace,
+                                                   workspace_bytes, (hipStream_t)stream));
+}
+
 int noalloc_scratch(int device, void** out)
 {
     if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail("Device index out of range for the no-allocation scratch");
@@ -469,6 +517,57 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
 {
     return scm_backward_impl<double>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight, grad_alpha,
                                      grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_pair_supported(int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    g.KH = (int)(KH > 0 && KH < 64 ? KH : 0);
+    g.KW = (int)(KW > 0 && KW < 64 ? KW : 0);
+    return mca::morpho_pair_supported(g) ? 1 : 0;
+}
+
+int mca_morpho_pair_forward_f32(int first_op, int replicate, float fill_first, float fill_second, const float* input, const float* w_first,
+                                const float* w_second, int64_t weight_batch_stride, float* output, uint8_t* taps_first,
+                                uint8_t* taps_second, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return pair_forward_impl<float>(first_op, replicate, fill_first, fill_second, input, w_first, w_second, weight_batch_stride, output,
+                                    taps_first, taps_second, B, C, H, W, KH, KW, stream);
+}
+
+int mca_morpho_pair_forward_f64(int first_op, int replicate, double fill_first, double fill_second, const double* input,
+                                const double* w_first, const double* w_second, int64_t weight_batch_stride, double* output,
+                                uint8_t* taps_first, uint8_t* taps_second, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                int64_t KW, void* stream)
+{
+    return pair_forward_impl<double>(first_op, replicate, fill_first, fill_second, input, w_first, w_second, weight_batch_stride, output,
+                                     taps_first, taps_second, B, C, H, W, KH, KW, stream);
+}
+
+size_t mca_morpho_pair_backward_workspace_size_f32(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    return pair_workspace_impl<float>(B, C, H, W, KH, KW);
+}
+
+size_t mca_morpho_pair_backward_workspace_size_f64(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    return pair_workspace_impl<double>(B, C, H, W, KH, KW);
+}
+
+int mca_morpho_pair_backward_f32(int first_op, const uint8_t* taps_first, const uint8_t* taps_second, const float* grad_output,
+                                 float* grad_input, float* grad_w_first, float* grad_w_second, int64_t B, int64_t C, int64_t H, int64_t W,
+                                 int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return pair_backward_impl<float>(first_op, taps_first, taps_second, grad_output, grad_input, grad_w_first, grad_w_second, B, C, H, W,
+                                     KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_pair_backward_f64(int first_op, const uint8_t* taps_first, const uint8_t* taps_second, const double* grad_output,
+                                 double* grad_input, double* grad_w_first, double* grad_w_second, int64_t B, int64_t C, int64_t H,
+                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return pair_backward_impl<double>(first_op, taps_first, taps_second, grad_output, grad_input, grad_w_first, grad_w_second, B, C, H,
+                                      W, KH, KW, workspace, workspace_bytes, stream);
 }
 
 int mca_probe_smorph_exp_f32(const float* x, float* y, int64_t n, void* stream)

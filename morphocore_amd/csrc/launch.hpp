@@ -101,6 +101,18 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
 
+// Opening / closing with IDENTITY merges fused into one pass (morpho_pair.hip). g: Cin == Cout == C,
+// Cw == 1; first_op: the first stage's op.
+bool morpho_pair_supported(const Geom& g);
+template <typename T>
+hipError_t morpho_pair_forward(int first_op, bool replicate, T fill1, T fill2, const T* x, const T* w1, const T* w2, T* out, uint8_t* taps1,
+                               uint8_t* taps2, const Geom& g, hipStream_t stream);
+template <typename T>
+size_t morpho_pair_backward_workspace(const Geom& g);
+template <typename T>
+hipError_t morpho_pair_backward(int first_op, const uint8_t* taps1, const uint8_t* taps2, const T* grad_out, T* grad_in, T* grad_w1,
+                                T* grad_w2, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 // The smorph kernels' exponential applied elementwise (test probe).
 template <typename T>
 hipError_t exp_probe(const T* x, T* y, int64_t n, hipStream_t stream);

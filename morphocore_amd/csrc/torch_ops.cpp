@@ -1,5 +1,6 @@
 // PyTorch-ROCm extension morphocore_amd._C: registers torch.ops.morphocore.{dilation, erosion, smorph,
-// smorph_scm} with the reference's schemas and dispatch key, and implements them as C++ autograd
+// smorph_scm} with the reference's schemas and dispatch key (plus opening_closing, the fused form of
+// the reference's Python opening / closing), and implements them as C++ autograd
 // Functions whose device work is the C ABI of libmorphocore_amd.so (include/morphocore_amd.h).
 //
 // This is the MI355X counterpart of the reference's host layer: bindings.cpp:15-156 (int checks,
@@ -411,6 +412,128 @@ Tensor morpho_erosion(const Tensor& input, const Tensor& weight, int64_t merge, 
 }
 
 // ------------------------------------------------------------------------------------------------
+// Opening / closing with per-channel merges in one pass. The reference composes them in Python from
+// two operator calls (functional/opening.py:96-101, functional/closing.py:96-101); this operator
+// computes the same output from one kernel and keeps each stage's taps (one byte per pixel each) for
+// a backward that only routes.
+// ------------------------------------------------------------------------------------------------
+
+class PairFunction : public torch::autograd::Function<PairFunction>
+{
+public:
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, const Tensor& w1_4, const Tensor& w2_4, int64_t first_op, int64_t padding,
+                          double padding_value, double noise_scale, bool needs_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const Tensor w1 = w1_4.contiguous();
+        const Tensor w2 = w2_4.contiguous();
+        const int64_t B = x.size(0), C = x.size(1), H = x.size(2), W = x.size(3), K = w1.size(2);
+        // Weight noise: each stage draws its own, the first stage first, as the two operator calls of
+        // the composition do (MorphoFunction above, morpho_op_wrap.hxx:55-64).
+        Tensor s1, s2;
+        if (noise_scale > 0.0)
+        {
+            const Tensor n1 = (torch::rand({B, C, 1, K, K}, w1.options()) * 2.0 - 1.0) * noise_scale;
+            s1 = (w1.unsqueeze(0) + n1).contiguous();
+            const Tensor n2 = (torch::rand({B, C, 1, K, K}, w2.options()) * 2.0 - 1.0) * noise_scale;
+            s2 = (w2.unsqueeze(0) + n2).contiguous();
+        }
+        const Tensor& k1 = s1.defined() ? s1 : w1;
+        const Tensor& k2 = s2.defined() ? s2 : w2;
+        const int64_t wbs = s1.defined() ? C * K * K : 0;
+        Tensor out = torch::empty_like(x);
+        Tensor taps = needs_grad ? torch::empty({2, B, C, H, W}, x.options().dtype(torch::kUInt8)) : Tensor();
+        uint8_t* t1 = taps.defined() ? taps.data_ptr<uint8_t>() : nullptr;
+        uint8_t* t2 = taps.defined() ? t1 + B * C * H * W : nullptr;
+        const int64_t op2 = first_op == DILATION ? EROSION : DILATION;
+        const double f1 = fill_value(first_op, padding, padding_value), f2 = fill_value(op2, padding, padding_value);
+        const int replicate = padding == REPLICATE;
+        if (x.scalar_type() == c10::kFloat)
+            check_rc(mca_morpho_pair_forward_f32((int)first_op, replicate, (float)f1, (float)f2, x.data_ptr<float>(), k1.data_ptr<float>(),
+                                                 k2.data_ptr<float>(), wbs, out.data_ptr<float>(), t1, t2, B, C, H, W, K, K, stream_of(x)));
+        else
+            check_rc(mca_morpho_pair_forward_f64((int)first_op, replicate, f1, f2, x.data_ptr<double>(), k1.data_ptr<double>(),
+                                                 k2.data_ptr<double>(), wbs, out.data_ptr<double>(), t1, t2, B, C, H, W, K, K, stream_of(x)));
+        ctx->save_for_backward({taps, w1});
+        ctx->saved_data["first_op"] = first_op;
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor& taps = saved[0];
+        const Tensor& w1 = saved[1];
+        const int64_t first_op = ctx->saved_data["first_op"].toInt();
+        TORCH_CHECK(taps.defined(), "opening_closing: the forward ran without gradients and kept no taps");
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        std::vector<int64_t> expected = taps.sizes().vec();
+        expected.erase(expected.begin());
+        TORCH_CHECK(grad_output.sizes() == expected, "grad_output shape mismatch: expected [", expected, "] but got [", grad_output.sizes(),
+                    "]");
+        TORCH_CHECK(grad_output.device() == taps.device(), "grad_output must be on the same device as input");
+        TORCH_CHECK(grad_output.scalar_type() == w1.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(taps.device());
+        const int64_t B = expected[0], C = expected[1], H = expected[2], W = expected[3], K = w1.size(2);
+        Tensor grad_input = torch::empty_like(grad_output);
+        Tensor gw1 = torch::empty_like(w1);
+        Tensor gw2 = torch::empty_like(w1);
+        const uint8_t* t1 = taps.data_ptr<uint8_t>();
+        const uint8_t* t2 = t1 + B * C * H * W;
+        if (grad_output.scalar_type() == c10::kFloat)
+        {
+            Tensor ws = byte_buffer((int64_t)mca_morpho_pair_backward_workspace_size_f32(B, C, H, W, K, K), grad_output);
+            check_rc(mca_morpho_pair_backward_f32((int)first_op, t1, t2, grad_output.data_ptr<float>(), grad_input.data_ptr<float>(),
+                                                  gw1.data_ptr<float>(), gw2.data_ptr<float>(), B, C, H, W, K, K, ws.data_ptr(),
+                                                  (size_t)ws.numel(), stream_of(grad_output)));
+        }
+        else
+        {
+            Tensor ws = byte_buffer((int64_t)mca_morpho_pair_backward_workspace_size_f64(B, C, H, W, K, K), grad_output);
+            check_rc(mca_morpho_pair_backward_f64((int)first_op, t1, t2, grad_output.data_ptr<double>(), grad_input.data_ptr<double>(),
+                                                  gw1.data_ptr<double>(), gw2.data_ptr<double>(), B, C, H, W, K, K, ws.data_ptr(),
+                                                  (size_t)ws.numel(), stream_of(grad_output)));
+        }
+        return {grad_input, gw1, gw2, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// Opening (first_op erosion) or closing (first_op dilation) with 'identity' merges on both stages; the
+// weights as the two operators receive them (an erosion's element flipped, functional/erosion.py:89).
+// Square 3x3 / 5x5 / 7x7 elements of equal size run fused; any other size, and a backward whose taps
+// would exceed MORPHOCORE_AMD_SAVED_TAPS_LIMIT or that save_indices=False asks to recompute, run the
+// two operators one after the other, exactly as the composition does.
+Tensor opening_closing(const Tensor& input, const Tensor& w_first, const Tensor& w_second, int64_t first_op, int64_t padding,
+                       double padding_value, bool save_indices, double noise_scale)
+{
+    padding = to_padding(padding);
+    TORCH_CHECK(first_op == DILATION || first_op == EROSION, "Unknown morphological operation ", first_op);
+    TORCH_CHECK(noise_scale >= 0.0, "noise_scale must be non negative");
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    const Tensor w1 = weight_to_4d(w_first);
+    const Tensor w2 = weight_to_4d(w_second);
+    check_4d(x4, w1);
+    check_4d(x4, w2);
+    check_identity(x4, w1, false);
+    check_identity(x4, w2, false);
+    check_device("morpho_pair_forward_hip", x4, {w1, w2});
+    const bool needs_grad = torch::GradMode::is_enabled() && (input.requires_grad() || w_first.requires_grad() || w_second.requires_grad());
+    const bool same = w1.size(2) == w2.size(2) && w1.size(3) == w2.size(3);
+    const int64_t tap_bytes = 2 * x4.numel();
+    const bool fused = same && mca_morpho_pair_supported(w1.size(2), w1.size(3)) &&
+                       (!needs_grad || (save_indices && tap_bytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30)));
+    if (!fused)
+    {
+        const int64_t op2 = first_op == DILATION ? EROSION : DILATION;
+        const Tensor mid = morpho_operation(first_op, x4, w1, IDENTITY, padding, padding_value, save_indices, noise_scale);
+        return output_to_original(morpho_operation(op2, mid, w2, IDENTITY, padding, padding_value, save_indices, noise_scale), input_dims);
+    }
+    return output_to_original(PairFunction::apply(x4, w1, w2, first_op, padding, padding_value, noise_scale, needs_grad), input_dims);
+}
+
+// ------------------------------------------------------------------------------------------------
 // Smorph: Smorph<merge> (smorph.cpp:20-111).
 // ------------------------------------------------------------------------------------------------
 
@@ -708,6 +831,9 @@ TORCH_LIBRARY(morphocore, m)
           "float noise_scale=0.) -> Tensor");
     m.def("smorph(Tensor input, Tensor weight, Tensor alpha, int merge) -> Tensor");
     m.def("smorph_scm(Tensor input, Tensor weight, Tensor alpha, Tensor beta) -> Tensor");
+    // No reference counterpart: the fused form of the reference's Python opening / closing.
+    m.def("opening_closing(Tensor input, Tensor w_first, Tensor w_second, int first_op, int padding, float padding_value=0., "
+          "bool save_indices=True, float noise_scale=0.) -> Tensor");
 }
 
 // CompositeImplicitAutograd, as the reference (bindings.cpp:142-148): the kernels run above autograd
@@ -718,6 +844,7 @@ TORCH_LIBRARY_IMPL(morphocore, CompositeImplicitAutograd, m)
     m.impl("erosion", &morpho_erosion);
     m.impl("smorph", &smorph);
     m.impl("smorph_scm", &smorph_scm);
+    m.impl("opening_closing", &opening_closing);
 }
 
 // Importing morphocore_amd._C loads this library, which runs the registrations above.

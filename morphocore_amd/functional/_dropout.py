@@ -22,3 +22,10 @@ def dropout_keep(w: torch.Tensor, p: float) -> torch.Tensor:
         taps = torch.randint(0, rows.shape[1], (n_dead,))
         rows[dead.nonzero().squeeze(1), taps.to(rows.device)] = True
     return keep
+
+
+def drop_weights(w: torch.Tensor, p: float) -> torch.Tensor:
+    """``w`` with the taps dropout removes set to -inf (they never win a dilation, nor an erosion, which
+    subtracts them), as the reference's dilation / erosion do in training (dilation.py:78-87)."""
+    keep = dropout_keep(w, p)
+    return torch.where(keep, w, torch.tensor(-float('inf'), device=w.device, dtype=w.dtype))

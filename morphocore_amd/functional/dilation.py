@@ -1,6 +1,6 @@
 import torch
 
-from ._dropout import dropout_keep
+from ._dropout import drop_weights
 from ._ops import ops
 from .merge_enum import str_to_merge, str_to_padding
 
@@ -34,8 +34,7 @@ def dilation(x: torch.Tensor, w: torch.Tensor, channel_merge_mode: str = 'sum', 
     if training and weight_dropout > 0.0:
         # The reference's draws and one-survivor rule, in its order (dilation.py:78-87), so that seeded
         # runs drop the same taps; one host synchronisation instead of one per channel pair.
-        keep = dropout_keep(w, weight_dropout)
-        w = torch.where(keep, w, torch.tensor(-float('inf'), device=w.device, dtype=w.dtype))
+        w = drop_weights(w, weight_dropout)
 
     return ops.dilation(x, w, str_to_merge(channel_merge_mode), str_to_padding(padding_mode), padding_value, save_indices,
                         noise_scale if training else 0.0)

@@ -1,8 +1,11 @@
 import torch
 import torch.nn as nn
 
+from ..functional._pair import DILATION, fused_pair
 from .dilation import Dilation
 from .erosion import Erosion
+
+_SHARED = ('padding_mode', 'padding_value', 'save_indices', 'weight_dropout', 'noise_scale', 'training')
 
 
 class Closing(nn.Module):
@@ -46,4 +49,11 @@ class Closing(nn.Module):
             self.erosion.weight = self.dilation.weight
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.erosion(self.dilation(x))
+        # Both stages per channel with the same settings: one fused operator call (same values and draws).
+        a, b = self.dilation, self.erosion
+        if a.channel_merge_mode == 'identity' and all(getattr(a, k) == getattr(b, k) for k in _SHARED):
+            out = fused_pair(x, a.weight, b.weight, DILATION, a.padding_mode, a.save_indices, a.padding_value, a.weight_dropout, a.training,
+                             a.noise_scale)
+            if out is not None:
+                return out
+        return b(a(x))

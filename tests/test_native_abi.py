@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 29
+    assert len(symbols) == 36
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -161,3 +161,29 @@ def test_noalloc_backward_rejects_problems_beyond_its_scratch():
     assert "Problem too large for the no-allocation backward" in lib.mca_last_error().decode()
     rc = lib.mca_morpho_backward_noalloc_f32(0, 9, 1, 0.0, None, None, 0, None, None, None, None, *GEOM, None)
     assert rc == 1 and lib.mca_last_error().decode() == "Unknown merge mode 9"
+
+
+def test_pair_supported_sizes():
+    lib = _native.lib()
+    assert [k for k in range(1, 13) if lib.mca_morpho_pair_supported(k, k)] == [3, 5, 7]
+    assert not lib.mca_morpho_pair_supported(3, 5)
+    assert not lib.mca_morpho_pair_supported(-3, -3)
+
+
+def test_pair_rejects_bad_arguments():
+    lib = _native.lib()
+    pg = (2, 3, 16, 16, 3, 3)
+    assert lib.mca_morpho_pair_forward_f32(4, 0, 0.0, 0.0, None, None, None, 0, None, None, None, *pg, None) == 1
+    assert "Unknown morphological operation 4" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_pair_forward_f32(1, 0, 0.0, 0.0, None, None, None, 0, None, None, None, 2, 3, 16, 16, 9, 9, None) == 1
+    assert "3x3, 5x5 or 7x7" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_pair_forward_f32(1, 0, 0.0, 0.0, None, None, None, 0, None, ctypes.c_void_p(16), None, *pg, None) == 1
+    assert "both be given or both be NULL" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_pair_backward_f32(1, None, None, None, None, None, None, *pg, None, 0, None) == 1
+    assert "saved taps" in lib.mca_last_error().decode()
+    need = lib.mca_morpho_pair_backward_workspace_size_f32(*pg)
+    assert need > 0 and lib.mca_morpho_pair_backward_workspace_size_f64(*pg) > need
+    assert lib.mca_morpho_pair_backward_workspace_size_f32(2, 3, 16, 16, 4, 4) == 0
+    t = ctypes.c_void_p(16)
+    assert lib.mca_morpho_pair_backward_f32(1, t, t, None, None, None, None, *pg, None, need - 1, None) == 1
+    assert "Workspace too small" in lib.mca_last_error().decode()
