@@ -1,6 +1,6 @@
 """Benchmark of the morphocore_amd hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu-baseline] [--no-extra]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..6] [--no-cpu-baseline] [--no-extra]
 
 K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
 millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
@@ -17,6 +17,11 @@ the config's dominant kernel (launched through the C ABI after the timed region 
 events on torch's current stream, the stream it runs on; HBM traffic and VALU instruction counts
 from the committed rocprofv3 counter summaries) and the CPU baseline (the reference's own CPU
 extension, or the C oracle, on a bounded sample on the host cores, in a child process).
+
+--config 1..5 are BASELINE.json's configs[0..4]. --config 6 is a workload of the fused compositions:
+the opening with one shared 3x3 element and per-channel merges (nn.Opening's default form) at
+configs[3]'s float64 shape, as one fused operator; its line also carries the same step run as the
+reference's composition of two operators ("composition_step").
 
 --kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
 rocprofv3 counter runs.
@@ -53,7 +58,15 @@ CONFIGS = {
             sample=dict(x=(4, 128, 112, 112))),
     5: dict(name="dilation(max) -> smorph(alpha=5,sum) -> erosion(min) fwd+bwd fp32", kind="stack", dtype="f32", x=(8, 64, 512, 512),
             w=(64, 64, 11, 11), x_dist=("rand", 0.0, 1.0), w_std=0.05, bound="valu", sample=dict(x=(1, 64, 128, 128))),
+    6: dict(name="opening fwd+bwd fp64 (erosion -> dilation, merge=identity, one shared element), fused", kind="pair", first="erosion",
+            dtype="f64", x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
+            sample=dict(x=(4, 128, 112, 112)), key="pair_opening_f64"),
 }
+
+
+def config_key(config):
+    """Name of a config in the committed profile records and the bench line."""
+    return CONFIGS[config].get("key", f"configs[{config - 1}]")
 
 
 def parse():
@@ -83,7 +96,7 @@ def parse():
 # Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
 # after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
 # millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
-DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1)}
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20)}
 
 
 def taps(cfg, x_shape=None):
@@ -136,6 +149,17 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
         phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
         n_out = 3 * B * Cout * H * W
         params = [xr] + wr + [alpha]
+    elif cfg["kind"] in ("pair", "pair_composition"):
+        # One structuring element shared by both stages (nn.Opening / nn.Closing's default).
+        first, second = (F.erosion, F.dilation) if cfg["first"] == "erosion" else (F.dilation, F.erosion)
+        fused = F.opening if cfg["first"] == "erosion" else F.closing
+        if cfg["kind"] == "pair":
+            fwd = lambda: [fused(xr, wr[0], wr[0], "identity", "replicate")]  # noqa: E731
+        else:
+            fwd = lambda: [second(first(xr, wr[0], "identity", "replicate"), wr[0], "identity", "replicate")]  # noqa: E731
+        phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
+        n_out = B * Cout * H * W
+        params = [xr] + wr
     else:
         op = F.dilation if cfg["op"] == "dilation" else F.erosion
         phases = [(lambda: [op(xr, wr[0], cfg["merge"], "replicate")]), (lambda outs: torch.autograd.backward(outs, [grad]))]
@@ -174,6 +198,21 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
     geom = (B, Cin, Cout, Cw, H, W, KH, KW)
     t = taps(cfg)
     esz = 8 if cfg["dtype"] == "f64" else 4
+    if cfg["kind"] == "pair":
+        # The fused forward: x read once, the output and one tap byte per stage written once.
+        first = 1 if cfg["first"] == "erosion" else 0
+        pg = (B, Cin, H, W, KH, KW)
+        out = torch.empty_like(x)
+        tp = torch.empty((2, B, Cin, H, W), dtype=torch.uint8, device=dev)
+        w1 = ws[0].flip((-2, -1)).contiguous() if first == 1 else ws[0]
+        w2 = ws[0] if first == 1 else ws[0].flip((-2, -1)).contiguous()
+        fills = (float("inf"), float("-inf")) if first == 1 else (float("-inf"), float("inf"))
+
+        def launch():
+            native.morpho_pair_forward(first, True, fills[0], fills[1], x, w1, w2, 0, out, tp[0], tp[1], pg)
+
+        what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
+        return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "morpho":
         op = 0 if cfg["op"] == "dilation" else 1
         merge = MERGE_CODE[cfg["merge"]]
@@ -228,6 +267,11 @@ def step_work(cfg):
     if cfg["kind"] == "morpho" and cfg.get("bound") == "hbm":
         esz = 8 if cfg["dtype"] == "f64" else 4
         return 5 * B * Cin * H * W * esz, "bytes"
+    if cfg["kind"] == "pair":
+        # Forward: x read, output and two tap bytes written; backward: grad_out and two tap bytes
+        # read, grad_x written.
+        esz = 8 if cfg["dtype"] == "f64" else 4
+        return B * Cin * H * W * (4 * esz + 4), "bytes"
     if cfg["kind"] == "morpho":
         return (None if B * Cout * H * W < (1 << 20) else (4 * t + 2 * B * Cout * Cin * H * W, "flop"))
     if cfg["kind"] == "smorph":
@@ -274,7 +318,7 @@ def profile_record(config):
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get(f"configs[{config - 1}]")
+        return json.load(f).get(config_key(config))
 
 
 def measured_traffic(config):
@@ -319,7 +363,7 @@ def host_cpu():
 def cpu_baseline(cfg, seconds):
     threads = min(len(os.sched_getaffinity(0)), 16)
     sx = cfg["sample"]["x"]
-    spec = dict(kind=cfg["kind"], op=cfg.get("op", "dilation"), merge=cfg.get("merge", "sum"), padding="replicate", dtype=cfg["dtype"],
+    spec = dict(kind=cfg["kind"], op=cfg.get("op", cfg.get("first", "dilation")), merge=cfg.get("merge", "sum"), padding="replicate", dtype=cfg["dtype"],
                 x=list(sx), w=list(cfg["w"]), w_std=cfg["w_std"], x_low=cfg["x_dist"][1], x_scale=cfg["x_dist"][2], threads=threads,
                 min_seconds=seconds, max_steps=50)
     if cfg["kind"] == "smorph":
@@ -437,7 +481,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f64" if cfg["dtype"] == "f64" else "f32",
         "data": "synthetic (seeded torch generators), inputs resident in HBM",
-        "config": {"workload": f"configs[{args.config - 1}]: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]),
+        "config": {"workload": f"{config_key(args.config)}: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]),
                    "parallelism": "none (1 GPU)"},
         "roofline": roof,
         "step_roofline": step_roofline(cfg, ms_per_step, roof.get("peak", PEAK_FP32_TFLOPS)),
@@ -454,6 +498,15 @@ def main():
                                  "fwd_ms": r3["fwd_ms"], "bwd_ms": r3["bwd_ms"], "value": r3["n_out"] / (r3["ms_per_step"] * 1e-3),
                                  "unit": "output-elements/s", "step_roofline": step_roofline(c3, r3["ms_per_step"], PEAK_FP32_TFLOPS)}
         del r3
+        torch.cuda.empty_cache()
+    if cfg["kind"] == "pair" and not args.no_extra:
+        # The same step as the reference writes it: two operator calls, the intermediate in HBM.
+        torch.cuda.empty_cache()
+        comp = dict(cfg, kind="pair_composition")
+        rc = run_steps(comp, torch, mca, dev, args.steps, args.warmup)
+        line["composition_step"] = {"workload": "the same step as two operator calls (erosion, then dilation)", "ms_per_step": rc["ms_per_step"],
+                                    "fwd_ms": rc["fwd_ms"], "bwd_ms": rc["bwd_ms"], "value": rc["n_out"] / (rc["ms_per_step"] * 1e-3)}
+        del rc
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)

@@ -8,7 +8,8 @@ prints one JSON object:
   {"seconds_per_step": s, "output_elements": n, "kind": "reference"|"port", "threads": t, "steps": k}
 
 Usage: python oracle/cpu_baseline.py '<json spec>' where the spec holds
-  kind: "morpho" | "smorph" | "stack", op: "dilation"|"erosion", merge, padding, dtype: "f32"|"f64",
+  kind: "morpho" | "smorph" | "stack" | "pair", op: "dilation"|"erosion" (pair: the first stage), merge, padding,
+  dtype: "f32"|"f64",
   x: [B,C,H,W], w: [Cout,Cw,KH,KW], alpha (smorph), threads, min_seconds.
 """
 import json
@@ -55,6 +56,12 @@ def run_reference(spec, threads):
             t = torch.tanh(a).unsqueeze(-1).unsqueeze(-1) if a.dim() == 2 else torch.tanh(a).view(-1, 1, 1, 1)
             wt = t * ((1 - t) / 2 * wr[0].flip(dims=(-2, -1)) + (1 + t) / 2 * wr[0])
             out = ops.smorph(xr, wt, a, merge)
+        elif spec["kind"] == "pair":
+            # The reference's opening / closing with per-channel merges and one shared element
+            # (functional/opening.py:96-101).
+            ero = lambda v: ops.erosion(v, wr[0].flip((-2, -1)), MERGES["identity"], padding, 0.0, True, 0.0)  # noqa: E731
+            dil = lambda v: ops.dilation(v, wr[0], MERGES["identity"], padding, 0.0, True, 0.0)  # noqa: E731
+            out = dil(ero(xr)) if spec["op"] == "erosion" else ero(dil(xr))
         else:
             a = torch.full((x.shape[1], x.shape[1]), 5.0, dtype=dtype, requires_grad=True)
             y = ops.dilation(xr, wr[0], MERGES["max"], padding, 0.0, True, 0.0)
@@ -94,7 +101,15 @@ def run_port(spec, threads):
             out = O.smorph_forward(merge, xn, wt, alpha)
             O.smorph_backward(merge, xn, wt, alpha, np.ones_like(out))
             return out.size
-        raise ValueError("the port baseline covers single operators")
+        if spec["kind"] == "pair":
+            ops_ = (O.EROSION, O.DILATION) if spec["op"] == "erosion" else (O.DILATION, O.EROSION)
+            wk = {O.DILATION: wn[0], O.EROSION: np.ascontiguousarray(wn[0][:, :, ::-1, ::-1])}
+            mid, _ = O.morpho_forward(ops_[0], MERGES["identity"], padding, 0.0, xn, wk[ops_[0]])
+            out, _ = O.morpho_forward(ops_[1], MERGES["identity"], padding, 0.0, mid, wk[ops_[1]])
+            gm, _ = O.morpho_backward(ops_[1], MERGES["identity"], padding, 0.0, mid, wk[ops_[1]], np.ones_like(out))
+            O.morpho_backward(ops_[0], MERGES["identity"], padding, 0.0, xn, wk[ops_[0]], gm)
+            return out.size
+        raise ValueError("the port baseline covers single operators and the opening / closing pair")
 
     return step
 
