@@ -1,6 +1,6 @@
 """Benchmark of the morphocore_amd hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..6] [--no-cpu-baseline] [--no-extra]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..7] [--no-cpu-baseline] [--no-extra]
 
 K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
 millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
@@ -18,10 +18,10 @@ events on torch's current stream, the stream it runs on; HBM traffic and VALU in
 from the committed rocprofv3 counter summaries) and the CPU baseline (the reference's own CPU
 extension, or the C oracle, on a bounded sample on the host cores, in a child process).
 
---config 1..5 are BASELINE.json's configs[0..4]. --config 6 is a workload of the fused compositions:
-the opening with one shared 3x3 element and per-channel merges (nn.Opening's default form) at
-configs[3]'s float64 shape, as one fused operator; its line also carries the same step run as the
-reference's composition of two operators ("composition_step").
+--config 1..5 are BASELINE.json's configs[0..4]. --config 6 and 7 are workloads of the fused
+compositions at configs[3]'s float64 shape, per-channel merges and one 3x3 element: the opening
+(nn.Opening's default form) and sigma_layer, each as one fused operator; their lines also carry the
+same step run as the reference's composition of operators ("composition_step").
 
 --kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
 rocprofv3 counter runs.
@@ -61,6 +61,9 @@ CONFIGS = {
     6: dict(name="opening fwd+bwd fp64 (erosion -> dilation, merge=identity, one shared element), fused", kind="pair", first="erosion",
             dtype="f64", x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
             sample=dict(x=(4, 128, 112, 112)), key="pair_opening_f64"),
+    7: dict(name="sigma_layer fwd+bwd fp64 (erosion and dilation blended, merge=identity), fused", kind="sigma", dtype="f64",
+            x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
+            sample=dict(x=(4, 128, 112, 112)), key="sigma_identity_f64"),
 }
 
 
@@ -96,7 +99,7 @@ def parse():
 # Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
 # after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
 # millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
-DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20)}
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20)}
 
 
 def taps(cfg, x_shape=None):
@@ -160,6 +163,19 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
         phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
         n_out = B * Cout * H * W
         params = [xr] + wr
+    elif cfg["kind"] in ("sigma", "sigma_composition"):
+        alpha = torch.full((Cout, 1), 0.3, dtype=dtype, device=dev, requires_grad=True)
+        if cfg["kind"] == "sigma":
+            fwd = lambda: [F.sigma_layer(xr, wr[0], alpha, "identity", "replicate")]  # noqa: E731
+        else:
+            def fwd():
+                e = F.erosion(xr, wr[0], "identity", "replicate")
+                d = F.dilation(xr, wr[0], "identity", "replicate")
+                soft = torch.sigmoid(alpha.mean(dim=1)).view(1, -1, 1, 1)
+                return [e * (1.0 - soft) + d * soft]
+        phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
+        n_out = B * Cout * H * W
+        params = [xr] + wr + [alpha]
     else:
         op = F.dilation if cfg["op"] == "dilation" else F.erosion
         phases = [(lambda: [op(xr, wr[0], cfg["merge"], "replicate")]), (lambda outs: torch.autograd.backward(outs, [grad]))]
@@ -212,6 +228,19 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
             native.morpho_pair_forward(first, True, fills[0], fills[1], x, w1, w2, 0, out, tp[0], tp[1], pg)
 
         what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
+        return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
+    if cfg["kind"] == "sigma":
+        # The fused forward: x read once, the output and one tap byte per operation written once.
+        pg = (B, Cin, H, W, KH, KW)
+        out = torch.empty_like(x)
+        tp = torch.empty((2, B, Cin, H, W), dtype=torch.uint8, device=dev)
+        we = ws[0].flip((-2, -1)).contiguous()
+        soft = torch.full((Cout,), 0.574442516811659, dtype=dtype, device=dev)
+
+        def launch():
+            native.morpho_sigma_forward(True, float("inf"), float("-inf"), x, we, ws[0], 0, soft, out, tp[0], tp[1], pg)
+
+        what = "fused sigma_layer forward, identity merge (mca_morpho_sigma_forward, one kernel)"
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "morpho":
         op = 0 if cfg["op"] == "dilation" else 1
@@ -272,6 +301,11 @@ def step_work(cfg):
         # read, grad_x written.
         esz = 8 if cfg["dtype"] == "f64" else 4
         return B * Cin * H * W * (4 * esz + 4), "bytes"
+    if cfg["kind"] == "sigma":
+        # Forward: x read, output and two tap bytes written; backward: x, grad_out and two tap bytes
+        # read, grad_x written.
+        esz = 8 if cfg["dtype"] == "f64" else 4
+        return B * Cin * H * W * (5 * esz + 4), "bytes"
     if cfg["kind"] == "morpho":
         return (None if B * Cout * H * W < (1 << 20) else (4 * t + 2 * B * Cout * Cin * H * W, "flop"))
     if cfg["kind"] == "smorph":
@@ -499,12 +533,14 @@ def main():
                                  "unit": "output-elements/s", "step_roofline": step_roofline(c3, r3["ms_per_step"], PEAK_FP32_TFLOPS)}
         del r3
         torch.cuda.empty_cache()
-    if cfg["kind"] == "pair" and not args.no_extra:
-        # The same step as the reference writes it: two operator calls, the intermediate in HBM.
+    if cfg["kind"] in ("pair", "sigma") and not args.no_extra:
+        # The same step as the reference writes it: separate operator calls, intermediates in HBM.
         torch.cuda.empty_cache()
-        comp = dict(cfg, kind="pair_composition")
+        comp = dict(cfg, kind=cfg["kind"] + "_composition")
         rc = run_steps(comp, torch, mca, dev, args.steps, args.warmup)
-        line["composition_step"] = {"workload": "the same step as two operator calls (erosion, then dilation)", "ms_per_step": rc["ms_per_step"],
+        desc = ("two operator calls (erosion, then dilation)" if cfg["kind"] == "pair"
+                else "two operator calls (erosion, dilation) and torch's blend")
+        line["composition_step"] = {"workload": "the same step as " + desc, "ms_per_step": rc["ms_per_step"],
                                     "fwd_ms": rc["fwd_ms"], "bwd_ms": rc["bwd_ms"], "value": rc["n_out"] / (rc["ms_per_step"] * 1e-3)}
         del rc
         torch.cuda.empty_cache()

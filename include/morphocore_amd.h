@@ -226,6 +226,43 @@ int mca_morpho_pair_backward_f64(int first_op, const uint8_t* taps_first, const 
                                  double* grad_input, double* grad_w_first, double* grad_w_second, int64_t B, int64_t C, int64_t H,
                                  int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* sigma_layer with the 'identity' merge in one pass: out = erosion(x) (1 - soft) + dilation(x) soft per
+ * channel, with torch's roundings of that expression. Replaces the two operator calls and the blend of
+ * morphocore/functional/sigma_layer.py:73-83 when the merge is 'identity' (soft = sigmoid(mean(alpha)),
+ * [C], computed by the caller). w_erosion / w_dilation: [C, 1, K, K] as each operator receives its
+ * element (the erosion's flipped, as functional/erosion.py passes it), or one per batch element,
+ * weight_batch_stride apart. fill_erosion / fill_dilation: each operation's border value; they must
+ * be equal, or the geodesic pair (+inf, -inf). taps_erosion / taps_dilation receive each operation's
+ * first extremal tap ([B, C, H, W] bytes; both NULL when no backward follows). Square odd elements 3x3,
+ * 5x5, 7x7 (mca_morpho_pair_supported). */
+int mca_morpho_sigma_forward_f32(int replicate, float fill_erosion, float fill_dilation, const float* input, const float* w_erosion,
+                                 const float* w_dilation, int64_t weight_batch_stride, const float* soft, float* output,
+                                 uint8_t* taps_erosion, uint8_t* taps_dilation, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                 int64_t KW, void* stream);
+int mca_morpho_sigma_forward_f64(int replicate, double fill_erosion, double fill_dilation, const double* input, const double* w_erosion,
+                                 const double* w_dilation, int64_t weight_batch_stride, const double* soft, double* output,
+                                 uint8_t* taps_erosion, uint8_t* taps_dilation, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                 int64_t KW, void* stream);
+
+/* Backward of mca_morpho_sigma_forward from its saved taps: grad_input, the gradients of both
+ * elements (in the frame each operator received) and grad_terms [2, C]: per channel the sum of
+ * grad_output * erosion and of grad_output * dilation, from which the caller forms the gradient of soft
+ * (their difference, dilation minus erosion). The routing is that of the two IDENTITY backwards with
+ * grad_output (1 - soft) and grad_output soft; grad_input is their sum. Workspace:
+ * mca_morpho_sigma_backward_workspace_size_* bytes (0: unsupported). */
+size_t mca_morpho_sigma_backward_workspace_size_f32(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW);
+size_t mca_morpho_sigma_backward_workspace_size_f64(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW);
+int mca_morpho_sigma_backward_f32(int replicate, float fill_erosion, float fill_dilation, const float* input, const float* w_erosion,
+                                  const float* w_dilation, int64_t weight_batch_stride, const float* soft, const uint8_t* taps_erosion,
+                                  const uint8_t* taps_dilation, const float* grad_output, float* grad_input, float* grad_w_erosion,
+                                  float* grad_w_dilation, float* grad_terms, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                  int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_morpho_sigma_backward_f64(int replicate, double fill_erosion, double fill_dilation, const double* input, const double* w_erosion,
+                                  const double* w_dilation, int64_t weight_batch_stride, const double* soft, const uint8_t* taps_erosion,
+                                  const uint8_t* taps_dilation, const double* grad_output, double* grad_input, double* grad_w_erosion,
+                                  double* grad_w_dilation, double* grad_terms, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                  int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Test probe, no reference counterpart: y[j] = the exponential every smorph kernel evaluates, applied
  * to x[j] (n values, device pointers). It restates the reference's vector exponential
  * (morphocore/functional/csrc/cpp/morpho_cpu_simd.hpp:127-169) for the arguments the kernels pass,

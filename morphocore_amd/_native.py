@@ -50,6 +50,12 @@ EXPORTS = (
     "mca_morpho_pair_backward_workspace_size_f64",
     "mca_morpho_pair_backward_f32",
     "mca_morpho_pair_backward_f64",
+    "mca_morpho_sigma_forward_f32",
+    "mca_morpho_sigma_forward_f64",
+    "mca_morpho_sigma_backward_workspace_size_f32",
+    "mca_morpho_sigma_backward_workspace_size_f64",
+    "mca_morpho_sigma_backward_f32",
+    "mca_morpho_sigma_backward_f64",
     "mca_probe_smorph_exp_f32",
     "mca_probe_smorph_exp_f64",
 )
@@ -121,6 +127,15 @@ def lib() -> ctypes.CDLL:
         f.restype = _SZ
         f = getattr(so, f"mca_morpho_pair_backward_{sfx}")
         f.argtypes = [_I, _P, _P, _P, _P, _P, _P] + _PGEOM + [_P, _SZ, _P]
+        f.restype = _I
+        f = getattr(so, f"mca_morpho_sigma_forward_{sfx}")
+        f.argtypes = [_I, real, real, _P, _P, _P, _I64, _P, _P, _P, _P] + _PGEOM + [_P]
+        f.restype = _I
+        f = getattr(so, f"mca_morpho_sigma_backward_workspace_size_{sfx}")
+        f.argtypes = list(_PGEOM)
+        f.restype = _SZ
+        f = getattr(so, f"mca_morpho_sigma_backward_{sfx}")
+        f.argtypes = [_I, real, real, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P] + _PGEOM + [_P, _SZ, _P]
         f.restype = _I
     so.mca_morpho_backward_noalloc_f32.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P]
     so.mca_morpho_backward_noalloc_f32.restype = _I
@@ -276,6 +291,25 @@ def morpho_pair_backward(first_op, taps_first, taps_second, grad_out, grad_in, g
     f = getattr(so, f"mca_morpho_pair_backward_{sfx}")
     _check(f(first_op, _ptr(taps_first), _ptr(taps_second), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w_first), _ptr(grad_w_second), *pgeom,
              _ptr(ws), ws.numel(), _stream(grad_out)))
+
+
+def morpho_sigma_forward(replicate, fill_erosion, fill_dilation, x, w_erosion, w_dilation, weight_batch_stride, soft, out, taps_erosion,
+                         taps_dilation, pgeom):
+    """Enqueue the fused sigma_layer forward, 'identity' merge (C ABI mca_morpho_sigma_forward_*)."""
+    f = getattr(lib(), f"mca_morpho_sigma_forward_{_sfx(x)}")
+    _check(f(int(replicate), fill_erosion, fill_dilation, _ptr(x), _ptr(w_erosion), _ptr(w_dilation), weight_batch_stride, _ptr(soft),
+             _ptr(out), _ptr(taps_erosion), _ptr(taps_dilation), *pgeom, _stream(x)))
+
+
+def morpho_sigma_backward(replicate, fill_erosion, fill_dilation, x, w_erosion, w_dilation, weight_batch_stride, soft, taps_erosion,
+                          taps_dilation, grad_out, grad_in, grad_w_erosion, grad_w_dilation, grad_terms, pgeom):
+    """Enqueue the fused sigma_layer backward (C ABI mca_morpho_sigma_backward_*), workspace from torch."""
+    so, sfx = lib(), _sfx(x)
+    ws = _workspace(getattr(so, f"mca_morpho_sigma_backward_workspace_size_{sfx}")(*pgeom), x.device)
+    f = getattr(so, f"mca_morpho_sigma_backward_{sfx}")
+    _check(f(int(replicate), fill_erosion, fill_dilation, _ptr(x), _ptr(w_erosion), _ptr(w_dilation), weight_batch_stride, _ptr(soft),
+             _ptr(taps_erosion), _ptr(taps_dilation), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w_erosion), _ptr(grad_w_dilation),
+             _ptr(grad_terms), *pgeom, _ptr(ws), ws.numel(), _stream(x)))
 
 
 def probe_smorph_exp(x, y):

@@ -3,6 +3,7 @@
 // include/morphocore_amd.h.
 #include "../../include/morphocore_amd.h"
 
+#include <limits>
 #include <mutex>
 #include <string>
 
@@ -279,6 +280,63 @@ int pair_backward_impl(int first_op, const uint8_t* taps1, const uint8_t* taps2,
     if ((rc = check_workspace(workspace_bytes, need, workspace)) != MCA_OK) return rc;
     return hip_status(mca::morpho_pair_backward<T>(first_op, taps1, taps2, grad_output, grad_input, grad_w1, grad_w2, g, workspace,
                                                    workspace_bytes, (hipStream_t)stream));
+}
+
+// The one border value both operations of the fused sigma_layer read: their common fill, or, for the
+// geodesic pair (+inf for the erosion, -inf for the dilation), NaN, which neither operation ever
+// picks, as it never picks its own geodesic fill.
+template <typename T>
+int sigma_fill(int replicate, T fill_e, T fill_d, T& fill)
+{
+    if (replicate || fill_e == fill_d)
+    {
+        fill = fill_e;
+        return MCA_OK;
+    }
+    if (fill_e == std::numeric_limits<T>::infinity() && fill_d == -std::numeric_limits<T>::infinity())
+    {
+        fill = std::numeric_limits<T>::quiet_NaN();
+        return MCA_OK;
+    }
+    return fail("The fused sigma_layer needs one border value for both operations (or the geodesic pair +inf / -inf)");
+}
+
+template <typename T>
+int sigma_forward_impl(int replicate, T fill_e, T fill_d, const T* input, const T* we, const T* wd, int64_t wbs, const T* soft, T* output,
+                       uint8_t* tapse, uint8_t* tapsd, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_pair_geom(mca::EROSION, B, C, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if ((tapse == nullptr) != (tapsd == nullptr)) return fail("taps_erosion and taps_dilation must both be given or both be NULL");
+    T fill{};
+    if ((rc = sigma_fill<T>(replicate, fill_e, fill_d, fill)) != MCA_OK) return rc;
+    return hip_status(mca::morpho_sigma_forward<T>(replicate != 0, fill, input, we, wd, soft, output, tapse, tapsd, g, (hipStream_t)stream));
+}
+
+template <typename T>
+size_t sigma_workspace_impl(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_pair_geom(mca::EROSION, B, C, H, W, KH, KW, 0, g) != MCA_OK) return 0;
+    return mca::morpho_sigma_backward_workspace<T>(g);
+}
+
+template <typename T>
+int sigma_backward_impl(int replicate, T fill_e, T fill_d, const T* input, const T* we, const T* wd, int64_t wbs, const T* soft,
+                        const uint8_t* tapse, const uint8_t* tapsd, const T* grad_output, T* grad_input, T* grad_we, T* grad_wd, T* grad_terms,
+                        int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes,
+                        void* stream)
+{
+    mca::Geom g{};
+    int rc = make_pair_geom(mca::EROSION, B, C, H, W, KH, KW, wbs, g);
+    if (rc != MCA_OK) return rc;
+    if (!tapse || !tapsd) return fail("The fused sigma_layer backward needs both operations' saved taps");
+    T fill{};
+    if ((rc = sigma_fill<T>(replicate, fill_e, fill_d, fill)) != MCA_OK) return rc;
+    if ((rc = check_workspace(workspace_bytes, mca::morpho_sigma_backward_workspace<T>(g), workspace)) != MCA_OK) return rc;
+    return hip_status(mca::morpho_sigma_backward<T>(replicate != 0, fill, input, we, wd, soft, tapse, tapsd, grad_output, grad_input, grad_we,
+                                                    grad_wd, grad_terms, g, workspace, workspace_bytes, (hipStream_t)stream));
 }
 
 int noalloc_scratch(int device, void** out)
@@ -568,6 +626,56 @@ int mca_morpho_pair_backward_f64(int first_op, const uint8_t* taps_first, const 
 {
     return pair_backward_impl<double>(first_op, taps_first, taps_second, grad_output, grad_input, grad_w_first, grad_w_second, B, C, H,
                                       W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_sigma_forward_f32(int replicate, float fill_erosion, float fill_dilation, const float* input, const float* w_erosion,
+                                 const float* w_dilation, int64_t weight_batch_stride, const float* soft, float* output,
+                                 uint8_t* taps_erosion, uint8_t* taps_dilation, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                 int64_t KW, void* stream)
+{
+    return sigma_forward_impl<float>(replicate, fill_erosion, fill_dilation, input, w_erosion, w_dilation, weight_batch_stride, soft, output,
+                                     taps_erosion, taps_dilation, B, C, H, W, KH, KW, stream);
+}
+
+int mca_morpho_sigma_forward_f64(int replicate, double fill_erosion, double fill_dilation, const double* input, const double* w_erosion,
+                                 const double* w_dilation, int64_t weight_batch_stride, const double* soft, double* output,
+                                 uint8_t* taps_erosion, uint8_t* taps_dilation, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                 int64_t KW, void* stream)
+{
+    return sigma_forward_impl<double>(replicate, fill_erosion, fill_dilation, input, w_erosion, w_dilation, weight_batch_stride, soft,
+                                      output, taps_erosion, taps_dilation, B, C, H, W, KH, KW, stream);
+}
+
+size_t mca_morpho_sigma_backward_workspace_size_f32(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    return sigma_workspace_impl<float>(B, C, H, W, KH, KW);
+}
+
+size_t mca_morpho_sigma_backward_workspace_size_f64(int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    return sigma_workspace_impl<double>(B, C, H, W, KH, KW);
+}
+
+int mca_morpho_sigma_backward_f32(int replicate, float fill_erosion, float fill_dilation, const float* input, const float* w_erosion,
+                                  const float* w_dilation, int64_t weight_batch_stride, const float* soft, const uint8_t* taps_erosion,
+                                  const uint8_t* taps_dilation, const float* grad_output, float* grad_input, float* grad_w_erosion,
+                                  float* grad_w_dilation, float* grad_terms, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                  int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return sigma_backward_impl<float>(replicate, fill_erosion, fill_dilation, input, w_erosion, w_dilation, weight_batch_stride, soft,
+                                      taps_erosion, taps_dilation, grad_output, grad_input, grad_w_erosion, grad_w_dilation, grad_terms, B, C,
+                                      H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_sigma_backward_f64(int replicate, double fill_erosion, double fill_dilation, const double* input, const double* w_erosion,
+                                  const double* w_dilation, int64_t weight_batch_stride, const double* soft, const uint8_t* taps_erosion,
+                                  const uint8_t* taps_dilation, const double* grad_output, double* grad_input, double* grad_w_erosion,
+                                  double* grad_w_dilation, double* grad_terms, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
+                                  int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return sigma_backward_impl<double>(replicate, fill_erosion, fill_dilation, input, w_erosion, w_dilation, weight_batch_stride, soft,
+                                       taps_erosion, taps_dilation, grad_output, grad_input, grad_w_erosion, grad_w_dilation, grad_terms, B,
+                                       C, H, W, KH, KW, workspace, workspace_bytes, stream);
 }
 
 int mca_probe_smorph_exp_f32(const float* x, float* y, int64_t n, void* stream)

@@ -101,7 +101,7 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
 
-// Opening / closing with IDENTITY merges fused into one pass (morpho_pair.hip). g: Cin == Cout == C,
+// Opening / closing with IDENTITY merges fused into one pass (morpho_fused.hip). g: Cin == Cout == C,
 // Cw == 1; first_op: the first stage's op.
 bool morpho_pair_supported(const Geom& g);
 template <typename T>
@@ -112,6 +112,20 @@ size_t morpho_pair_backward_workspace(const Geom& g);
 template <typename T>
 hipError_t morpho_pair_backward(int first_op, const uint8_t* taps1, const uint8_t* taps2, const T* grad_out, T* grad_in, T* grad_w1,
                                 T* grad_w2, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// sigma_layer with the IDENTITY merge in one pass (morpho_fused.hip): out = erosion (1 - soft) + dilation
+// soft per channel; we / wd as each operator receives its element (the erosion's flipped). fill: the
+// border value both operations read. The backward writes grad_in, both elements' gradients and
+// grad_terms [2][C] (sum of g * erosion, sum of g * dilation per channel).
+template <typename T>
+hipError_t morpho_sigma_forward(bool replicate, T fill, const T* x, const T* we, const T* wd, const T* soft, T* out, uint8_t* tapse,
+                                uint8_t* tapsd, const Geom& g, hipStream_t stream);
+template <typename T>
+size_t morpho_sigma_backward_workspace(const Geom& g);
+template <typename T>
+hipError_t morpho_sigma_backward(bool replicate, T fill, const T* x, const T* we, const T* wd, const T* soft, const uint8_t* tapse,
+                                 const uint8_t* tapsd, const T* grad_out, T* grad_in, T* grad_we, T* grad_wd, T* grad_terms, const Geom& g,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The smorph kernels' exponential applied elementwise (test probe).
 template <typename T>

@@ -1,6 +1,6 @@
 // PyTorch-ROCm extension morphocore_amd._C: registers torch.ops.morphocore.{dilation, erosion, smorph,
-// smorph_scm} with the reference's schemas and dispatch key (plus opening_closing, the fused form of
-// the reference's Python opening / closing), and implements them as C++ autograd
+// smorph_scm} with the reference's schemas and dispatch key (plus opening_closing and sigma_identity,
+// fused forms of the reference's Python opening / closing and sigma_layer), and implements them as C++ autograd
 // Functions whose device work is the C ABI of libmorphocore_amd.so (include/morphocore_amd.h).
 //
 // This is the MI355X counterpart of the reference's host layer: bindings.cpp:15-156 (int checks,
@@ -534,6 +534,143 @@ Tensor opening_closing(const Tensor& input, const Tensor& w_first, const Tensor&
 }
 
 // ------------------------------------------------------------------------------------------------
+// sigma_layer with the 'identity' merge in one pass. The reference composes it in Python from two
+// operator calls and a blend (functional/sigma_layer.py:73-83); this operator computes the same output
+// in one kernel and keeps each operation's taps for a backward that only routes.
+// ------------------------------------------------------------------------------------------------
+
+class SigmaFunction : public torch::autograd::Function<SigmaFunction>
+{
+public:
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, const Tensor& we4, const Tensor& wd4, const Tensor& soft_in, int64_t padding,
+                          double padding_value, double noise_scale, bool needs_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const Tensor we = we4.contiguous();
+        const Tensor wd = wd4.contiguous();
+        const Tensor soft = soft_in.contiguous().reshape({-1});
+        const int64_t B = x.size(0), C = x.size(1), H = x.size(2), W = x.size(3), K = we.size(2);
+        // Weight noise: the erosion's draw, then the dilation's, as the composition's two operator
+        // calls draw them (MorphoFunction above, morpho_op_wrap.hxx:55-64).
+        Tensor se, sd;
+        if (noise_scale > 0.0)
+        {
+            const Tensor ne = (torch::rand({B, C, 1, K, K}, we.options()) * 2.0 - 1.0) * noise_scale;
+            se = (we.unsqueeze(0) + ne).contiguous();
+            const Tensor nd = (torch::rand({B, C, 1, K, K}, wd.options()) * 2.0 - 1.0) * noise_scale;
+            sd = (wd.unsqueeze(0) + nd).contiguous();
+        }
+        const Tensor& ke = se.defined() ? se : we;
+        const Tensor& kd = sd.defined() ? sd : wd;
+        const int64_t wbs = se.defined() ? C * K * K : 0;
+        Tensor out = torch::empty_like(x);
+        Tensor taps = needs_grad ? torch::empty({2, B, C, H, W}, x.options().dtype(torch::kUInt8)) : Tensor();
+        uint8_t* te = taps.defined() ? taps.data_ptr<uint8_t>() : nullptr;
+        uint8_t* td = taps.defined() ? te + B * C * H * W : nullptr;
+        const double fe = fill_value(EROSION, padding, padding_value), fd = fill_value(DILATION, padding, padding_value);
+        const int replicate = padding == REPLICATE;
+        if (x.scalar_type() == c10::kFloat)
+            check_rc(mca_morpho_sigma_forward_f32(replicate, (float)fe, (float)fd, x.data_ptr<float>(), ke.data_ptr<float>(), kd.data_ptr<float>(),
+                                                  wbs, soft.data_ptr<float>(), out.data_ptr<float>(), te, td, B, C, H, W, K, K, stream_of(x)));
+        else
+            check_rc(mca_morpho_sigma_forward_f64(replicate, fe, fd, x.data_ptr<double>(), ke.data_ptr<double>(), kd.data_ptr<double>(), wbs,
+                                                  soft.data_ptr<double>(), out.data_ptr<double>(), te, td, B, C, H, W, K, K, stream_of(x)));
+        ctx->save_for_backward({x, ke, kd, soft, taps, we});
+        ctx->saved_data["padding"] = padding;
+        ctx->saved_data["padding_value"] = padding_value;
+        ctx->saved_data["wbs"] = wbs;
+        ctx->saved_data["soft_sizes"] = soft_in.sizes().vec();
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor& x = saved[0];
+        const Tensor& ke = saved[1];
+        const Tensor& kd = saved[2];
+        const Tensor& soft = saved[3];
+        const Tensor& taps = saved[4];
+        const Tensor& we = saved[5];
+        TORCH_CHECK(taps.defined(), "sigma_identity: the forward ran without gradients and kept no taps");
+        const int64_t padding = ctx->saved_data["padding"].toInt();
+        const double padding_value = ctx->saved_data["padding_value"].toDouble();
+        const int64_t wbs = ctx->saved_data["wbs"].toInt();
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        TORCH_CHECK(grad_output.sizes() == x.sizes(), "grad_output shape mismatch: expected [", x.sizes(), "] but got [", grad_output.sizes(),
+                    "]");
+        TORCH_CHECK(grad_output.device() == x.device(), "grad_output must be on the same device as input");
+        TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(x.device());
+        const int64_t B = x.size(0), C = x.size(1), H = x.size(2), W = x.size(3), K = we.size(2);
+        Tensor grad_input = torch::empty_like(x);
+        Tensor gwe = torch::empty_like(we);
+        Tensor gwd = torch::empty_like(we);
+        Tensor terms = torch::empty({2, C}, x.options());
+        const uint8_t* te = taps.data_ptr<uint8_t>();
+        const uint8_t* td = te + B * C * H * W;
+        const double fe = fill_value(EROSION, padding, padding_value), fd = fill_value(DILATION, padding, padding_value);
+        const int replicate = padding == REPLICATE;
+        if (x.scalar_type() == c10::kFloat)
+        {
+            Tensor ws = byte_buffer((int64_t)mca_morpho_sigma_backward_workspace_size_f32(B, C, H, W, K, K), x);
+            check_rc(mca_morpho_sigma_backward_f32(replicate, (float)fe, (float)fd, x.data_ptr<float>(), ke.data_ptr<float>(), kd.data_ptr<float>(),
+                                                   wbs, soft.data_ptr<float>(), te, td, grad_output.data_ptr<float>(), grad_input.data_ptr<float>(),
+                                                   gwe.data_ptr<float>(), gwd.data_ptr<float>(), terms.data_ptr<float>(), B, C, H, W, K, K,
+                                                   ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        }
+        else
+        {
+            Tensor ws = byte_buffer((int64_t)mca_morpho_sigma_backward_workspace_size_f64(B, C, H, W, K, K), x);
+            check_rc(mca_morpho_sigma_backward_f64(replicate, fe, fd, x.data_ptr<double>(), ke.data_ptr<double>(), kd.data_ptr<double>(), wbs,
+                                                   soft.data_ptr<double>(), te, td, grad_output.data_ptr<double>(),
+                                                   grad_input.data_ptr<double>(), gwe.data_ptr<double>(), gwd.data_ptr<double>(),
+                                                   terms.data_ptr<double>(), B, C, H, W, K, K, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        }
+        // d out / d soft = sum g * dilation - sum g * erosion (the blend's two products).
+        const Tensor grad_soft = (terms[1] - terms[0]).reshape(ctx->saved_data["soft_sizes"].toIntVector());
+        return {grad_input, gwe, gwd, grad_soft, Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// sigma_layer with the 'identity' merge; the elements as the two operators receive them (the
+// erosion's flipped, functional/erosion.py:89) and soft = sigmoid(mean(alpha)) per channel. Square
+// 3x3 / 5x5 / 7x7 elements of equal size run fused; other sizes, and a backward whose taps would exceed
+// MORPHOCORE_AMD_SAVED_TAPS_LIMIT or that save_indices=False asks to recompute, run the two operators
+// and the blend as the composition does.
+Tensor sigma_identity(const Tensor& input, const Tensor& w_erosion, const Tensor& w_dilation, const Tensor& soft, int64_t padding,
+                      double padding_value, bool save_indices, double noise_scale)
+{
+    padding = to_padding(padding);
+    TORCH_CHECK(noise_scale >= 0.0, "noise_scale must be non negative");
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    const Tensor we = weight_to_4d(w_erosion);
+    const Tensor wd = weight_to_4d(w_dilation);
+    check_4d(x4, we);
+    check_4d(x4, wd);
+    check_identity(x4, we, false);
+    check_identity(x4, wd, false);
+    TORCH_CHECK(soft.numel() == x4.size(1), "soft must hold one value per channel");
+    check_device("morpho_sigma_forward_hip", x4, {we, wd, soft});
+    const bool needs_grad = torch::GradMode::is_enabled() &&
+                            (input.requires_grad() || w_erosion.requires_grad() || w_dilation.requires_grad() || soft.requires_grad());
+    const bool same = we.size(2) == wd.size(2) && we.size(3) == wd.size(3);
+    const int64_t tap_bytes = 2 * x4.numel();
+    const bool fused = same && mca_morpho_pair_supported(we.size(2), we.size(3)) &&
+                       (!needs_grad || (save_indices && tap_bytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30)));
+    if (!fused)
+    {
+        const Tensor e = morpho_operation(EROSION, x4, we, IDENTITY, padding, padding_value, save_indices, noise_scale);
+        const Tensor d = morpho_operation(DILATION, x4, wd, IDENTITY, padding, padding_value, save_indices, noise_scale);
+        const Tensor s = soft.reshape({1, -1, 1, 1});
+        return output_to_original(e * (1.0 - s) + d * s, input_dims);
+    }
+    return output_to_original(SigmaFunction::apply(x4, we, wd, soft, padding, padding_value, noise_scale, needs_grad), input_dims);
+}
+
+// ------------------------------------------------------------------------------------------------
 // Smorph: Smorph<merge> (smorph.cpp:20-111).
 // ------------------------------------------------------------------------------------------------
 
@@ -834,6 +971,9 @@ TORCH_LIBRARY(morphocore, m)
     // No reference counterpart: the fused form of the reference's Python opening / closing.
     m.def("opening_closing(Tensor input, Tensor w_first, Tensor w_second, int first_op, int padding, float padding_value=0., "
           "bool save_indices=True, float noise_scale=0.) -> Tensor");
+    // No reference counterpart: the fused form of the reference's Python sigma_layer, 'identity' merge.
+    m.def("sigma_identity(Tensor input, Tensor w_erosion, Tensor w_dilation, Tensor soft, int padding, float padding_value=0., "
+          "bool save_indices=True, float noise_scale=0.) -> Tensor");
 }
 
 // CompositeImplicitAutograd, as the reference (bindings.cpp:142-148): the kernels run above autograd
@@ -845,6 +985,7 @@ TORCH_LIBRARY_IMPL(morphocore, CompositeImplicitAutograd, m)
     m.impl("smorph", &smorph);
     m.impl("smorph_scm", &smorph_scm);
     m.impl("opening_closing", &opening_closing);
+    m.impl("sigma_identity", &sigma_identity);
 }
 
 // Importing morphocore_amd._C loads this library, which runs the registrations above.

@@ -8,7 +8,7 @@ prints one JSON object:
   {"seconds_per_step": s, "output_elements": n, "kind": "reference"|"port", "threads": t, "steps": k}
 
 Usage: python oracle/cpu_baseline.py '<json spec>' where the spec holds
-  kind: "morpho" | "smorph" | "stack" | "pair", op: "dilation"|"erosion" (pair: the first stage), merge, padding,
+  kind: "morpho" | "smorph" | "stack" | "pair" | "sigma", op: "dilation"|"erosion" (pair: the first stage), merge, padding,
   dtype: "f32"|"f64",
   x: [B,C,H,W], w: [Cout,Cw,KH,KW], alpha (smorph), threads, min_seconds.
 """
@@ -62,6 +62,13 @@ def run_reference(spec, threads):
             ero = lambda v: ops.erosion(v, wr[0].flip((-2, -1)), MERGES["identity"], padding, 0.0, True, 0.0)  # noqa: E731
             dil = lambda v: ops.dilation(v, wr[0], MERGES["identity"], padding, 0.0, True, 0.0)  # noqa: E731
             out = dil(ero(xr)) if spec["op"] == "erosion" else ero(dil(xr))
+        elif spec["kind"] == "sigma":
+            # The reference's sigma_layer, per-channel merge (functional/sigma_layer.py:73-83).
+            a = torch.full((x.shape[1], 1), 0.3, dtype=dtype, requires_grad=True)
+            e = ops.erosion(xr, wr[0].flip((-2, -1)), MERGES["identity"], padding, 0.0, True, 0.0)
+            d = ops.dilation(xr, wr[0], MERGES["identity"], padding, 0.0, True, 0.0)
+            soft = torch.sigmoid(a.mean(dim=1)).view(1, -1, 1, 1)
+            out = e * (1.0 - soft) + d * soft
         else:
             a = torch.full((x.shape[1], x.shape[1]), 5.0, dtype=dtype, requires_grad=True)
             y = ops.dilation(xr, wr[0], MERGES["max"], padding, 0.0, True, 0.0)

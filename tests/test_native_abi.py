@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 36
+    assert len(symbols) == 42
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -186,4 +186,26 @@ def test_pair_rejects_bad_arguments():
     assert lib.mca_morpho_pair_backward_workspace_size_f32(2, 3, 16, 16, 4, 4) == 0
     t = ctypes.c_void_p(16)
     assert lib.mca_morpho_pair_backward_f32(1, t, t, None, None, None, None, *pg, None, need - 1, None) == 1
+    assert "Workspace too small" in lib.mca_last_error().decode()
+
+
+def test_sigma_rejects_bad_arguments():
+    lib = _native.lib()
+    pg = (2, 3, 16, 16, 3, 3)
+    inf = float("inf")
+    args = lambda fe, fd: (0, fe, fd, None, None, None, 0, None, None, None, None, *pg, None)  # noqa: E731
+    assert lib.mca_morpho_sigma_forward_f32(*args(1.0, 2.0)) == 1
+    assert "one border value for both operations" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_sigma_forward_f32(*args(-inf, inf)) == 1
+    assert lib.mca_morpho_sigma_forward_f32(0, 0.0, 0.0, None, None, None, 0, None, None, ctypes.c_void_p(16), None, *pg, None) == 1
+    assert "both be given or both be NULL" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_sigma_forward_f64(0, 0.0, 0.0, None, None, None, 0, None, None, None, None, 2, 3, 16, 16, 9, 9, None) == 1
+    assert "3x3, 5x5 or 7x7" in lib.mca_last_error().decode()
+    need = lib.mca_morpho_sigma_backward_workspace_size_f32(*pg)
+    assert need > 0 and lib.mca_morpho_sigma_backward_workspace_size_f32(2, 3, 16, 16, 3, 5) == 0
+    t = ctypes.c_void_p(16)
+    common = (None, None, None, 0, None)
+    assert lib.mca_morpho_sigma_backward_f32(0, inf, -inf, *common, None, None, None, None, None, None, None, *pg, None, need, None) == 1
+    assert "saved taps" in lib.mca_last_error().decode()
+    assert lib.mca_morpho_sigma_backward_f32(0, inf, -inf, *common, t, t, None, None, None, None, None, *pg, None, need - 1, None) == 1
     assert "Workspace too small" in lib.mca_last_error().decode()
