@@ -191,6 +191,16 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                 double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Per-sample structuring elements of weight noise in one pass: out[b][j] = weight[j] + (uniform[b][j] * 2
+ * - 1) * scale for b < batch, j < n, with the roundings of the four elementwise operations the
+ * reference composes it from (morphocore/functional/csrc/cpp/morpho_op_wrap.hxx:55-64: torch::rand's
+ * draw, times 2, minus 1, times noise_scale, plus the shared weight), so the elements are bit for bit
+ * those; `uniform` holds the caller's draw ([batch, n], in [0, 1)). For the forward launchers'
+ * weight_batch_stride = n. */
+int mca_noise_sample_weights_f32(const float* weight, const float* uniform, float scale, float* out, int64_t batch, int64_t n, void* stream);
+int mca_noise_sample_weights_f64(const double* weight, const double* uniform, double scale, double* out, int64_t batch, int64_t n,
+                                 void* stream);
+
 /* Opening / closing with 'identity' merges in one pass (x to the final output per tile; the
  * intermediate image stays in on-chip memory). Replaces the two operator calls of
  * morphocore/functional/opening.py:96-101 (erosion, then dilation) and closing.py:96-101 (dilation,

@@ -43,6 +43,8 @@ EXPORTS = (
     "mca_smorph_scm_backward_workspace_size_f64",
     "mca_smorph_scm_backward_f32",
     "mca_smorph_scm_backward_f64",
+    "mca_noise_sample_weights_f32",
+    "mca_noise_sample_weights_f64",
     "mca_morpho_pair_supported",
     "mca_morpho_pair_forward_f32",
     "mca_morpho_pair_forward_f64",
@@ -114,6 +116,10 @@ def lib() -> ctypes.CDLL:
         f.restype = _I
         f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
         f.argtypes = [_P] * 11 + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
+    for sfx, real in (("f32", ctypes.c_float), ("f64", ctypes.c_double)):
+        f = getattr(so, f"mca_noise_sample_weights_{sfx}")
+        f.argtypes = [_P, _P, real, _P, _I64, _I64, _P]
         f.restype = _I
     _PGEOM = [_I64] * 6
     so.mca_morpho_pair_supported.argtypes = [_I64, _I64]
@@ -269,6 +275,13 @@ def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out
     f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
     _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w),
              _ptr(grad_alpha), _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))
+
+
+def noise_sample_weights(weight, uniform, scale, out):
+    """Enqueue the per-sample elements of weight noise (C ABI mca_noise_sample_weights_*): out[b] =
+    weight + (uniform[b] * 2 - 1) * scale with torch's roundings; uniform and out [B, *weight.shape]."""
+    f = getattr(lib(), f"mca_noise_sample_weights_{_sfx(weight)}")
+    _check(f(_ptr(weight), _ptr(uniform), scale, _ptr(out), uniform.shape[0], weight.numel(), _stream(weight)))
 
 
 def morpho_pair_supported(KH, KW) -> bool:

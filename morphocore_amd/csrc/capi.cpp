@@ -577,6 +577,19 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                      grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
 }
 
+int mca_noise_sample_weights_f32(const float* weight, const float* uniform, float scale, float* out, int64_t batch, int64_t n, void* stream)
+{
+    if (batch < 0 || n < 0) return fail("batch and n must be non negative");
+    return hip_status(mca::noise_sample_async<float>(weight, uniform, scale, out, n, batch, (hipStream_t)stream));
+}
+
+int mca_noise_sample_weights_f64(const double* weight, const double* uniform, double scale, double* out, int64_t batch, int64_t n,
+                                 void* stream)
+{
+    if (batch < 0 || n < 0) return fail("batch and n must be non negative");
+    return hip_status(mca::noise_sample_async<double>(weight, uniform, scale, out, n, batch, (hipStream_t)stream));
+}
+
 int mca_morpho_pair_supported(int64_t KH, int64_t KW)
 {
     mca::Geom g{};

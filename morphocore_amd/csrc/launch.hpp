@@ -131,6 +131,11 @@ hipError_t morpho_sigma_backward(bool replicate, T fill, const T* x, const T* we
 template <typename T>
 hipError_t exp_probe(const T* x, T* y, int64_t n, hipStream_t stream);
 
+// Per-sample elements of weight noise from uniform draws u [batch, n]: w + (u * 2 - 1) * scale with the
+// roundings of torch's four elementwise operations (util.hip).
+template <typename T>
+hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n, int64_t batch, hipStream_t stream);
+
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);

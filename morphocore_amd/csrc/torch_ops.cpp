@@ -279,6 +279,25 @@ private:
     std::vector<Entry> live_;
 };
 
+// Weight noise: one structuring element per batch element, [B, *w.shape], from torch::rand's draw on the
+// weight's device (its generator, the reference's draw, morpho_op_wrap.hxx:55-64), formed by one
+// kernel with the roundings of the reference's four elementwise operations.
+Tensor sample_weights(const Tensor& w, int64_t B, double noise_scale)
+{
+    std::vector<int64_t> shape = w.sizes().vec();
+    shape.insert(shape.begin(), B);
+    const Tensor u = torch::rand(shape, w.options());
+    Tensor out = torch::empty(shape, w.options());
+    const int64_t n = w.numel();
+    if (w.scalar_type() == c10::kFloat)
+        check_rc(mca_noise_sample_weights_f32(w.data_ptr<float>(), u.data_ptr<float>(), (float)noise_scale, out.data_ptr<float>(), B, n,
+                                              stream_of(w)));
+    else
+        check_rc(mca_noise_sample_weights_f64(w.data_ptr<double>(), u.data_ptr<double>(), noise_scale, out.data_ptr<double>(), B, n,
+                                              stream_of(w)));
+    return out;
+}
+
 // ------------------------------------------------------------------------------------------------
 // Dilation and erosion: MorphoOperation<op, merge, kind> (morpho_op_wrap.hxx:24-211).
 // ------------------------------------------------------------------------------------------------
@@ -296,11 +315,7 @@ public:
         // Weight noise: one structuring element per batch element, drawn on the weight's device from
         // its generator as morpho_op_wrap.hxx:55-64 draws it.
         Tensor sample_weight;
-        if (noise_scale > 0.0)
-        {
-            const Tensor noise = (torch::rand({g.B, g.Cout, g.Cw, g.KH, g.KW}, w.options()) * 2.0 - 1.0) * noise_scale;
-            sample_weight = (w.unsqueeze(0) + noise).contiguous();
-        }
+        if (noise_scale > 0.0) sample_weight = sample_weights(w, g.B, noise_scale);
         const Tensor& kw = sample_weight.defined() ? sample_weight : w;
         const int64_t wbs = sample_weight.defined() ? g.Cout * g.Cw * g.KH * g.KW : 0;
         const int64_t nbytes = (int64_t)mca_morpho_indices_bytes((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
@@ -434,10 +449,8 @@ public:
         Tensor s1, s2;
         if (noise_scale > 0.0)
         {
-            const Tensor n1 = (torch::rand({B, C, 1, K, K}, w1.options()) * 2.0 - 1.0) * noise_scale;
-            s1 = (w1.unsqueeze(0) + n1).contiguous();
-            const Tensor n2 = (torch::rand({B, C, 1, K, K}, w2.options()) * 2.0 - 1.0) * noise_scale;
-            s2 = (w2.unsqueeze(0) + n2).contiguous();
+            s1 = sample_weights(w1, B, noise_scale);
+            s2 = sample_weights(w2, B, noise_scale);
         }
         const Tensor& k1 = s1.defined() ? s1 : w1;
         const Tensor& k2 = s2.defined() ? s2 : w2;
@@ -556,10 +569,8 @@ public:
         Tensor se, sd;
         if (noise_scale > 0.0)
         {
-            const Tensor ne = (torch::rand({B, C, 1, K, K}, we.options()) * 2.0 - 1.0) * noise_scale;
-            se = (we.unsqueeze(0) + ne).contiguous();
-            const Tensor nd = (torch::rand({B, C, 1, K, K}, wd.options()) * 2.0 - 1.0) * noise_scale;
-            sd = (wd.unsqueeze(0) + nd).contiguous();
+            se = sample_weights(we, B, noise_scale);
+            sd = sample_weights(wd, B, noise_scale);
         }
         const Tensor& ke = se.defined() ? se : we;
         const Tensor& kd = sd.defined() ? sd : wd;

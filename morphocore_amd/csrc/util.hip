@@ -47,6 +47,22 @@ __global__ __launch_bounds__(BLOCK) void round_kernel(const double* __restrict__
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) dst[j] = (T)src[j];
 }
 
+// Per-sample structuring elements of weight noise: out[b][j] = w[j] + (u[b][j] * 2 - 1) * scale, with
+// the roundings of the four elementwise operations torch evaluates it with (morpho_op_wrap.hxx:55-64),
+// in their order, so that the elements are bit for bit the ones the composed expression gives.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void noise_sample_kernel(const T* __restrict__ w, const T* __restrict__ u, T scale, T* __restrict__ out,
+                                                             int64_t n, int64_t total)
+{
+#pragma clang fp contract(off)
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < total; j += (int64_t)gridDim.x * BLOCK)
+    {
+        const T t = u[j] * T(2);
+        const T v = (t - T(1)) * scale;
+        out[j] = w[j % n] + v;
+    }
+}
+
 static int grid_for(int64_t n)
 {
     const int64_t blocks = (n + BLOCK - 1) / BLOCK;
@@ -91,6 +107,17 @@ hipError_t round_async(const double* src, T* dst, int64_t n, hipStream_t stream)
     return hipGetLastError();
 }
 
+template <typename T>
+hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n, int64_t batch, hipStream_t stream)
+{
+    const int64_t total = n * batch;
+    if (total <= 0) return hipSuccess;
+    noise_sample_kernel<T><<<grid_for(total), BLOCK, 0, stream>>>(w, u, scale, out, n, total);
+    return hipGetLastError();
+}
+
+template hipError_t noise_sample_async<float>(const float*, const float*, float, float*, int64_t, int64_t, hipStream_t);
+template hipError_t noise_sample_async<double>(const double*, const double*, double, double*, int64_t, int64_t, hipStream_t);
 template hipError_t round_async<float>(const double*, float*, int64_t, hipStream_t);
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
 template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
