@@ -89,6 +89,32 @@ int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const
                             double* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Dilation / erosion in float16 and bfloat16 (no reference counterpart: the reference's
+ * "TODO: Add float16 support", morphocore/functional/csrc/cpp/morpho_op.cpp:7). Buffers hold IEEE
+ * binary16 / bfloat16 bits; the arithmetic is float32 (every 16-bit value converts exactly) and each
+ * stored result is rounded once to nearest even, so an output equals the float32 operator's on the
+ * same values, rounded. `fill` is a float32. The forward reads and writes 16-bit data directly; the
+ * backward converts grad_output to float32 in its workspace, routes it with the float32 kernels and
+ * rounds grad_input and grad_weight once. Arguments otherwise as the f32 entry points. */
+int mca_morpho_forward_f16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                           int64_t weight_batch_stride, uint16_t* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                           int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+int mca_morpho_forward_bf16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                            int64_t weight_batch_stride, uint16_t* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                            int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream);
+size_t mca_morpho_backward_workspace_size_f16(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW);
+size_t mca_morpho_backward_workspace_size_bf16(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                               int64_t W, int64_t KH, int64_t KW);
+int mca_morpho_backward_f16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                            int64_t weight_batch_stride, const void* indices, const uint16_t* grad_output, uint16_t* grad_input,
+                            uint16_t* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+int mca_morpho_backward_bf16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                             int64_t weight_batch_stride, const void* indices, const uint16_t* grad_output, uint16_t* grad_input,
+                             uint16_t* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of device scratch each GPU holds for mca_morpho_backward_noalloc_f32 (64 MiB). */
 #define MCA_NOALLOC_SCRATCH_BYTES (64u << 20)
 

@@ -26,6 +26,12 @@ EXPORTS = (
     "mca_morpho_backward_f32",
     "mca_morpho_backward_f64",
     "mca_morpho_backward_noalloc_f32",
+    "mca_morpho_forward_f16",
+    "mca_morpho_forward_bf16",
+    "mca_morpho_backward_workspace_size_f16",
+    "mca_morpho_backward_workspace_size_bf16",
+    "mca_morpho_backward_f16",
+    "mca_morpho_backward_bf16",
     "mca_smorph_forward_f32",
     "mca_smorph_forward_f64",
     "mca_smorph_backward_workspace_size_f32",
@@ -121,6 +127,16 @@ def lib() -> ctypes.CDLL:
         f = getattr(so, f"mca_noise_sample_weights_{sfx}")
         f.argtypes = [_P, _P, real, _P, _I64, _I64, _P]
         f.restype = _I
+    for sfx in ("f16", "bf16"):
+        f = getattr(so, f"mca_morpho_forward_{sfx}")
+        f.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P] + _GEOM + [_P]
+        f.restype = _I
+        f = getattr(so, f"mca_morpho_backward_workspace_size_{sfx}")
+        f.argtypes = [_I, _I] + _GEOM
+        f.restype = _SZ
+        f = getattr(so, f"mca_morpho_backward_{sfx}")
+        f.argtypes = [_I, _I, _I, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
+        f.restype = _I
     _PGEOM = [_I64] * 6
     so.mca_morpho_pair_supported.argtypes = [_I64, _I64]
     so.mca_morpho_pair_supported.restype = _I
@@ -169,7 +185,11 @@ def _sfx(t: torch.Tensor) -> str:
         return "f32"
     if t.dtype == torch.float64:
         return "f64"
-    raise RuntimeError(f"morphocore_amd supports float32 and float64 tensors, got {t.dtype}")
+    if t.dtype == torch.float16:
+        return "f16"
+    if t.dtype == torch.bfloat16:
+        return "bf16"
+    raise RuntimeError(f"morphocore_amd supports float32, float64, float16 and bfloat16 tensors, got {t.dtype}")
 
 
 def _ptr(t):

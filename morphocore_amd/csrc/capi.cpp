@@ -77,7 +77,7 @@ int check_lds(size_t bytes)
 }
 
 template <typename T>
-int morpho_forward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, T* output,
+int morpho_forward_impl(int op, int merge, int replicate, mca::compute_t<T> fill, const T* input, const T* weight, int64_t wbs, T* output,
                         void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW,
                         void* stream)
 {
@@ -101,7 +101,7 @@ size_t morpho_workspace_impl(int merge, int has_indices, int64_t B, int64_t Cin,
 }
 
 template <typename T>
-int morpho_backward_impl(int op, int merge, int replicate, T fill, const T* input, const T* weight, int64_t wbs, const void* indices,
+int morpho_backward_impl(int op, int merge, int replicate, mca::compute_t<T> fill, const T* input, const T* weight, int64_t wbs, const void* indices,
                          const T* grad_output, T* grad_input, T* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                          int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
 {
@@ -414,6 +414,60 @@ int mca_morpho_backward_f64(int op, int merge, int replicate, double fill, const
 {
     return morpho_backward_impl<double>(op, merge, replicate, fill, input, weight, weight_batch_stride, indices, grad_output, grad_input,
                                         grad_weight, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+int mca_morpho_forward_f16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                           int64_t weight_batch_stride, uint16_t* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                           int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return morpho_forward_impl<_Float16>(op, merge, replicate, fill, reinterpret_cast<const _Float16*>(input),
+                                         reinterpret_cast<const _Float16*>(weight), weight_batch_stride, reinterpret_cast<_Float16*>(output),
+                                         indices, B, Cin, Cout, Cw, H, W, KH, KW, stream);
+}
+
+int mca_morpho_forward_bf16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                            int64_t weight_batch_stride, uint16_t* output, void* indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw,
+                            int64_t H, int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    return morpho_forward_impl<__bf16>(op, merge, replicate, fill, reinterpret_cast<const __bf16*>(input),
+                                       reinterpret_cast<const __bf16*>(weight), weight_batch_stride, reinterpret_cast<__bf16*>(output),
+                                       indices, B, Cin, Cout, Cw, H, W, KH, KW, stream);
+}
+
+size_t mca_morpho_backward_workspace_size_f16(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                              int64_t W, int64_t KH, int64_t KW)
+{
+    return morpho_workspace_impl<_Float16>(merge, has_indices, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+size_t mca_morpho_backward_workspace_size_bf16(int merge, int has_indices, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                               int64_t W, int64_t KH, int64_t KW)
+{
+    return morpho_workspace_impl<__bf16>(merge, has_indices, B, Cin, Cout, Cw, H, W, KH, KW);
+}
+
+int mca_morpho_backward_f16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                            int64_t weight_batch_stride, const void* indices, const uint16_t* grad_output, uint16_t* grad_input,
+                            uint16_t* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                            int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return morpho_backward_impl<_Float16>(op, merge, replicate, fill, reinterpret_cast<const _Float16*>(input),
+                                          reinterpret_cast<const _Float16*>(weight), weight_batch_stride, indices,
+                                          reinterpret_cast<const _Float16*>(grad_output), reinterpret_cast<_Float16*>(grad_input),
+                                          reinterpret_cast<_Float16*>(grad_weight), B, Cin, Cout, Cw, H, W, KH, KW, workspace,
+                                          workspace_bytes, stream);
+}
+
+int mca_morpho_backward_bf16(int op, int merge, int replicate, float fill, const uint16_t* input, const uint16_t* weight,
+                             int64_t weight_batch_stride, const void* indices, const uint16_t* grad_output, uint16_t* grad_input,
+                             uint16_t* grad_weight, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH,
+                             int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+{
+    return morpho_backward_impl<__bf16>(op, merge, replicate, fill, reinterpret_cast<const __bf16*>(input),
+                                        reinterpret_cast<const __bf16*>(weight), weight_batch_stride, indices,
+                                        reinterpret_cast<const __bf16*>(grad_output), reinterpret_cast<__bf16*>(grad_input),
+                                        reinterpret_cast<__bf16*>(grad_weight), B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes,
+                                        stream);
 }
 
 int mca_morpho_backward_noalloc_f32(int op, int merge, int replicate, float fill, const float* input, const float* weight,

@@ -145,10 +145,11 @@ __device__ __forceinline__ T read_padded(const T* __restrict__ plane, int H, int
     return plane[(int64_t)clampi(y, 0, H - 1) * W + clampi(x, 0, W - 1)];
 }
 
-// Stage rows [y0, y0 + t.rows) x columns [x0, x0 + t.cols) of `plane` into `tile`, out-of-image
-// positions resolved by read_padded. Wave v stages rows v, v + NWAVES, ...; lanes stride the columns.
-template <typename T>
-__device__ __forceinline__ void stage_tile(T* tile, const T* __restrict__ plane, const Geom& g, const Tiling& t, int y0, int x0,
+// Stage rows [y0, y0 + t.rows) x columns [x0, x0 + t.cols) of `plane` (storage type ST) into `tile`
+// (compute type T), out-of-image positions resolved by read_padded. Wave v stages rows v, v + NWAVES,
+// ...; lanes stride the columns.
+template <typename T, typename ST>
+__device__ __forceinline__ void stage_tile(T* tile, const ST* __restrict__ plane, const Geom& g, const Tiling& t, int y0, int x0,
                                            bool replicate, T fill)
 {
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -162,15 +163,36 @@ __device__ __forceinline__ void stage_tile(T* tile, const T* __restrict__ plane,
             const int x = x0 + lx;
             T v;
             if (row_in && x >= 0 && x < g.W)
-                v = plane[(int64_t)y * g.W + x];
+                v = (T)plane[(int64_t)y * g.W + x];
             else if (replicate)
-                v = plane[(int64_t)yc * g.W + clampi(x, 0, g.W - 1)];
+                v = (T)plane[(int64_t)yc * g.W + clampi(x, 0, g.W - 1)];
             else
                 v = fill;
             tile[ly * t.pitch + lx] = v;
         }
     }
 }
+
+// Storage types of the dilation / erosion operands: float32 and float64 compute in themselves, float16
+// and bfloat16 in float32 (every value converts exactly; a result is rounded once, to nearest even,
+// when it is stored).
+template <typename ST>
+struct ComputeOf
+{
+    using type = ST;
+};
+template <>
+struct ComputeOf<_Float16>
+{
+    using type = float;
+};
+template <>
+struct ComputeOf<__bf16>
+{
+    using type = float;
+};
+template <typename ST>
+using compute_t = typename ComputeOf<ST>::type;
 
 // Gradient accumulators kept in LDS are double, for float and double tensors alike: on gfx950 an
 // LDS float64 atomic add (ds_add_f64) issues in ~10 cycles per wave instruction while the float32

@@ -43,23 +43,28 @@ inline size_t indices_bytes(int merge, const Geom& g)
     return pix * cpair * pair_tap_bytes(g);
 }
 
-template <typename T>
-hipError_t morpho_forward(int op, int merge, bool replicate, T fill, const T* x, const T* w, T* out, void* indices, const Geom& g,
-                          hipStream_t stream);
+// ST: the storage type of x, w and out (float, double, _Float16 or __bf16); the fill value is in its
+// compute type (compute_t).
+template <typename ST>
+hipError_t morpho_forward(int op, int merge, bool replicate, compute_t<ST> fill, const ST* x, const ST* w, ST* out, void* indices,
+                          const Geom& g, hipStream_t stream);
 
 // Bytes of LDS the forward kernel needs; > LDS_LIMIT means the structuring element is too large.
-template <typename T>
+template <typename ST>
 size_t morpho_forward_lds(const Geom& g);
 
-template <typename T>
+// ST: the storage type, as for morpho_forward. Float16 and bfloat16 gradients are routed by the
+// float32 kernels (grad_output converted in, grad_input and grad_weight rounded out, in the workspace).
+template <typename ST>
 size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g);
 
-template <typename T>
+template <typename ST>
 size_t morpho_backward_lds(int merge, const Geom& g);
 
-template <typename T>
-hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
-                           T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream);
+template <typename ST>
+hipError_t morpho_backward(int op, int merge, bool replicate, compute_t<ST> fill, const ST* x, const ST* w, const void* indices,
+                           const ST* grad_out, ST* grad_in, ST* grad_w, const Geom& g, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
 
 // Values in each of the three arrays of saved smorph pair statistics (float32 static kernels only;
 // 0 when the configuration has none).
@@ -135,6 +140,10 @@ hipError_t exp_probe(const T* x, T* y, int64_t n, hipStream_t stream);
 // roundings of torch's four elementwise operations (util.hip).
 template <typename T>
 hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n, int64_t batch, hipStream_t stream);
+
+// dst = src converted between a 16-bit storage type and float32 (util.hip).
+template <typename S, typename D>
+hipError_t convert_async(const S* src, D* dst, int64_t n, hipStream_t stream);
 
 // Shared helpers (util.hip).
 template <typename T>

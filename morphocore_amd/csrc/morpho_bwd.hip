@@ -853,8 +853,9 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
 }
 
 template <typename T>
-hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x, const T* w, const void* indices, const T* grad_out,
-                           T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
+hipError_t morpho_backward(int op, int merge, bool replicate, compute_t<T> fill, const T* x, const T* w, const void* indices,
+                           const T* grad_out, T* grad_in, T* grad_w, const Geom& g, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream)
 {
     if (workspace_bytes < morpho_backward_workspace<T>(merge, indices != nullptr, g)) return hipErrorInvalidValue;
     unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
@@ -862,13 +863,89 @@ hipError_t morpho_backward(int op, int merge, bool replicate, T fill, const T* x
                           : backward_op<T, EROSION>(merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, ws, stream);
 }
 
+// Float16 / bfloat16: the winners come from the forward (or the 16-bit forward kernels recompute them
+// into the workspace); grad_output is converted to float32, the float32 kernels route it, and
+// grad_input and grad_weight are rounded once into the 16-bit outputs. Workspace: [float32 workspace
+// with winners | grad_output | grad_input | grad_weight (float32) | (recomputed winners | scratch output)].
+template <typename ST>
+static size_t half_parts(int merge, const Geom& g, size_t& inner, size_t& gout, size_t& gin, size_t& gw)
+{
+    inner = align_up(morpho_backward_workspace<float>(merge, true, g));
+    gout = align_up((size_t)g.B * g.Cout * g.plane() * sizeof(float));
+    gin = align_up((size_t)g.B * g.Cin * g.plane() * sizeof(float));
+    gw = align_up((size_t)g.Cout * g.Cw * g.taps() * sizeof(float));
+    return inner + gout + gin + gw;
+}
+
+template <typename ST>
+size_t half_backward_workspace(int merge, bool has_indices, const Geom& g)
+{
+    size_t inner, gout, gin, gw;
+    size_t bytes = half_parts<ST>(merge, g, inner, gout, gin, gw);
+    if (!has_indices) bytes += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(ST));
+    return bytes;
+}
+
+template <typename ST>
+hipError_t half_backward(int op, int merge, bool replicate, float fill, const ST* x, const ST* w, const void* indices, const ST* grad_out,
+                         ST* grad_in, ST* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+    if (workspace_bytes < half_backward_workspace<ST>(merge, indices != nullptr, g)) return hipErrorInvalidValue;
+    size_t inner, gout_b, gin_b, gw_b;
+    const size_t base = half_parts<ST>(merge, g, inner, gout_b, gin_b, gw_b);
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    float* gout = reinterpret_cast<float*>(ws + inner);
+    float* gin = reinterpret_cast<float*>(ws + inner + gout_b);
+    float* gw = reinterpret_cast<float*>(ws + inner + gout_b + gin_b);
+    hipError_t err;
+    if (!indices)
+    {
+        void* idx = ws + base;
+        ST* tmp_out = reinterpret_cast<ST*>(ws + base + align_up(indices_bytes(merge, g)));
+        if ((err = morpho_forward<ST>(op, merge, replicate, fill, x, w, tmp_out, idx, g, stream)) != hipSuccess) return err;
+        indices = idx;
+    }
+    const int64_t gout_n = (int64_t)g.B * g.Cout * g.plane(), gin_n = (int64_t)g.B * g.Cin * g.plane();
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    if ((err = convert_async<ST, float>(grad_out, gout, gout_n, stream)) != hipSuccess) return err;
+    // With the winners given, the float32 kernels read neither the input nor the element.
+    if ((err = morpho_backward<float>(op, merge, replicate, fill, nullptr, nullptr, indices, gout, gin, gw, g, ws, inner, stream)) !=
+        hipSuccess)
+        return err;
+    if ((err = convert_async<float, ST>(gin, grad_in, gin_n, stream)) != hipSuccess) return err;
+    return convert_async<float, ST>(gw, grad_w, wnumel, stream);
+}
+
 #define MCA_INSTANTIATE_BWD(T)                                                                                                          \
     template size_t morpho_backward_workspace<T>(int, bool, const Geom&);                                                               \
     template size_t morpho_backward_lds<T>(int, const Geom&);                                                                           \
-    template hipError_t morpho_backward<T>(int, int, bool, T, const T*, const T*, const void*, const T*, T*, T*, const Geom&, void*,    \
-                                           size_t, hipStream_t);
+    template hipError_t morpho_backward<T>(int, int, bool, compute_t<T>, const T*, const T*, const void*, const T*, T*, T*, const Geom&, \
+                                           void*, size_t, hipStream_t);
 
 MCA_INSTANTIATE_BWD(float)
 MCA_INSTANTIATE_BWD(double)
+
+#define MCA_INSTANTIATE_BWD_HALF(ST)                                                                                                    \
+    template <>                                                                                                                         \
+    size_t morpho_backward_workspace<ST>(int merge, bool has_indices, const Geom& g)                                                    \
+    {                                                                                                                                   \
+        return half_backward_workspace<ST>(merge, has_indices, g);                                                                      \
+    }                                                                                                                                   \
+    template <>                                                                                                                         \
+    size_t morpho_backward_lds<ST>(int merge, const Geom& g)                                                                            \
+    {                                                                                                                                   \
+        return morpho_backward_lds<float>(merge, g);                                                                                    \
+    }                                                                                                                                   \
+    template <>                                                                                                                         \
+    hipError_t morpho_backward<ST>(int op, int merge, bool replicate, float fill, const ST* x, const ST* w, const void* indices,         \
+                                   const ST* grad_out, ST* grad_in, ST* grad_w, const Geom& g, void* workspace, size_t workspace_bytes,  \
+                                   hipStream_t stream)                                                                                  \
+    {                                                                                                                                   \
+        return half_backward<ST>(op, merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, workspace, workspace_bytes,   \
+                                 stream);                                                                                               \
+    }
+
+MCA_INSTANTIATE_BWD_HALF(_Float16)
+MCA_INSTANTIATE_BWD_HALF(__bf16)
 
 }  // namespace mca

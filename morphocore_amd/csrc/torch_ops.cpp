@@ -160,13 +160,14 @@ const char* scalar_name(c10::ScalarType t)
     }
 }
 
-// The operators run only on a HIP device, in float32 or float64; everything else is an error, never
-// a fallback.
-void check_device(const char* name, const Tensor& x4, std::initializer_list<Tensor> others)
+// The operators run only on a HIP device, in float32 or float64 (dilation and erosion also in
+// float16 and bfloat16); everything else is an error, never a fallback.
+void check_device(const char* name, const Tensor& x4, std::initializer_list<Tensor> others, bool allow_16bit = false)
 {
     TORCH_CHECK(x4.is_cuda(), "morphocore_amd: ", name, " runs on AMD GPUs (HIP devices); got an input on ", x4.device());
-    TORCH_CHECK(x4.scalar_type() == c10::kFloat || x4.scalar_type() == c10::kDouble, "\"", name, "\" not implemented for '",
-                scalar_name(x4.scalar_type()), "'");
+    const auto st = x4.scalar_type();
+    TORCH_CHECK(st == c10::kFloat || st == c10::kDouble || (allow_16bit && (st == c10::kHalf || st == c10::kBFloat16)), "\"", name,
+                "\" not implemented for '", scalar_name(st), "'");
     for (const Tensor& t : others)
     {
         TORCH_CHECK(t.device() == x4.device(), "morphocore_amd: ", name, " expects every tensor on ", x4.device(), ", got one on ", t.device());
@@ -192,6 +193,9 @@ Geom geom_of(const Tensor& x4, const Tensor& w4)
 {
     return Geom{x4.size(0), x4.size(1), w4.size(0), w4.size(1), x4.size(2), x4.size(3), w4.size(2), w4.size(3)};
 }
+
+// The 16-bit payload of a float16 / bfloat16 tensor, as the C ABI takes it.
+uint16_t* bits16(const Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr()); }
 
 Tensor byte_buffer(int64_t nbytes, const Tensor& like) { return torch::empty({nbytes > 0 ? nbytes : 1}, like.options().dtype(torch::kUInt8)); }
 
@@ -287,6 +291,8 @@ Tensor sample_weights(const Tensor& w, int64_t B, double noise_scale)
     std::vector<int64_t> shape = w.sizes().vec();
     shape.insert(shape.begin(), B);
     const Tensor u = torch::rand(shape, w.options());
+    // 16-bit elements: the same expression in torch's own elementwise operations.
+    if (w.scalar_type() == c10::kHalf || w.scalar_type() == c10::kBFloat16) return (w.unsqueeze(0) + (u * 2.0 - 1.0) * noise_scale).contiguous();
     Tensor out = torch::empty(shape, w.options());
     const int64_t n = w.numel();
     if (w.scalar_type() == c10::kFloat)
@@ -332,6 +338,10 @@ public:
         if (x.scalar_type() == c10::kFloat)
             check_rc(mca_morpho_forward_f32((int)op, (int)merge, replicate, (float)fill, x.data_ptr<float>(), kw.data_ptr<float>(), wbs,
                                             out.data_ptr<float>(), idx, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        else if (x.scalar_type() == c10::kHalf || x.scalar_type() == c10::kBFloat16)
+            check_rc((x.scalar_type() == c10::kHalf ? mca_morpho_forward_f16 : mca_morpho_forward_bf16)(
+                (int)op, (int)merge, replicate, (float)fill, bits16(x), bits16(kw), wbs, bits16(out), idx, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W,
+                g.KH, g.KW, stream_of(x)));
         else
             check_rc(mca_morpho_forward_f64((int)op, (int)merge, replicate, fill, x.data_ptr<double>(), kw.data_ptr<double>(), wbs,
                                             out.data_ptr<double>(), idx, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
@@ -372,7 +382,18 @@ public:
         const double fill = fill_value(op, padding, padding_value);
         const void* idx = indices.defined() ? indices.data_ptr() : nullptr;
         const int has = idx != nullptr;
-        if (x.scalar_type() == c10::kFloat)
+        if (x.scalar_type() == c10::kHalf || x.scalar_type() == c10::kBFloat16)
+        {
+            const bool h = x.scalar_type() == c10::kHalf;
+            const size_t n = (h ? mca_morpho_backward_workspace_size_f16 : mca_morpho_backward_workspace_size_bf16)(
+                (int)merge, has, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            check_rc((h ? mca_morpho_backward_f16 : mca_morpho_backward_bf16)((int)op, (int)merge, replicate, (float)fill, bits16(x), bits16(kw),
+                                                                              wbs, idx, bits16(grad_output), bits16(grad_input),
+                                                                              bits16(grad_weight), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH,
+                                                                              g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        }
+        else if (x.scalar_type() == c10::kFloat)
         {
             const size_t n = mca_morpho_backward_workspace_size_f32((int)merge, has, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
             Tensor ws = byte_buffer((int64_t)n, x);
@@ -408,7 +429,7 @@ Tensor morpho_operation(int64_t op, const Tensor& input, const Tensor& weight, i
     check_4d(x4, w4);
     TORCH_CHECK(x4.size(1) == w4.size(1) || merge == IDENTITY, "Input channels must match weight input channels");
     if (merge == IDENTITY) check_identity(x4, w4, false);
-    check_device(op == DILATION ? "morpho_dilation_forward_hip" : "morpho_erosion_forward_hip", x4, {w4});
+    check_device(op == DILATION ? "morpho_dilation_forward_hip" : "morpho_erosion_forward_hip", x4, {w4}, true);
     const bool needs_grad = torch::GradMode::is_enabled() && (input.requires_grad() || weight.requires_grad());
     const Tensor out = MorphoFunction::apply(x4, w4, op, merge, padding, padding_value, save_indices, noise_scale, needs_grad);
     return output_to_original(out, input_dims);
@@ -531,11 +552,12 @@ Tensor opening_closing(const Tensor& input, const Tensor& w_first, const Tensor&
     check_4d(x4, w2);
     check_identity(x4, w1, false);
     check_identity(x4, w2, false);
-    check_device("morpho_pair_forward_hip", x4, {w1, w2});
+    check_device("morpho_pair_forward_hip", x4, {w1, w2}, true);
     const bool needs_grad = torch::GradMode::is_enabled() && (input.requires_grad() || w_first.requires_grad() || w_second.requires_grad());
     const bool same = w1.size(2) == w2.size(2) && w1.size(3) == w2.size(3);
     const int64_t tap_bytes = 2 * x4.numel();
-    const bool fused = same && mca_morpho_pair_supported(w1.size(2), w1.size(3)) &&
+    const bool wide = x4.scalar_type() == c10::kFloat || x4.scalar_type() == c10::kDouble;  // the fused kernels' types
+    const bool fused = wide && same && mca_morpho_pair_supported(w1.size(2), w1.size(3)) &&
                        (!needs_grad || (save_indices && tap_bytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30)));
     if (!fused)
     {
@@ -664,12 +686,13 @@ Tensor sigma_identity(const Tensor& input, const Tensor& w_erosion, const Tensor
     check_identity(x4, we, false);
     check_identity(x4, wd, false);
     TORCH_CHECK(soft.numel() == x4.size(1), "soft must hold one value per channel");
-    check_device("morpho_sigma_forward_hip", x4, {we, wd, soft});
+    check_device("morpho_sigma_forward_hip", x4, {we, wd, soft}, true);
     const bool needs_grad = torch::GradMode::is_enabled() &&
                             (input.requires_grad() || w_erosion.requires_grad() || w_dilation.requires_grad() || soft.requires_grad());
     const bool same = we.size(2) == wd.size(2) && we.size(3) == wd.size(3);
     const int64_t tap_bytes = 2 * x4.numel();
-    const bool fused = same && mca_morpho_pair_supported(we.size(2), we.size(3)) &&
+    const bool wide = x4.scalar_type() == c10::kFloat || x4.scalar_type() == c10::kDouble;  // the fused kernels' types
+    const bool fused = wide && same && mca_morpho_pair_supported(we.size(2), we.size(3)) &&
                        (!needs_grad || (save_indices && tap_bytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30)));
     if (!fused)
     {

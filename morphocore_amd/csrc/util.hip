@@ -63,6 +63,14 @@ __global__ __launch_bounds__(BLOCK) void noise_sample_kernel(const T* __restrict
     }
 }
 
+// dst[j] = src[j] converted: float16 / bfloat16 storage to its float32 compute type (exact) and back
+// (rounded to nearest even).
+template <typename S, typename D>
+__global__ __launch_bounds__(BLOCK) void convert_kernel(const S* __restrict__ src, D* __restrict__ dst, int64_t n)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) dst[j] = (D)(float)src[j];
+}
+
 static int grid_for(int64_t n)
 {
     const int64_t blocks = (n + BLOCK - 1) / BLOCK;
@@ -116,6 +124,18 @@ hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n
     return hipGetLastError();
 }
 
+template <typename S, typename D>
+hipError_t convert_async(const S* src, D* dst, int64_t n, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    convert_kernel<S, D><<<grid_for(n), BLOCK, 0, stream>>>(src, dst, n);
+    return hipGetLastError();
+}
+
+template hipError_t convert_async<_Float16, float>(const _Float16*, float*, int64_t, hipStream_t);
+template hipError_t convert_async<__bf16, float>(const __bf16*, float*, int64_t, hipStream_t);
+template hipError_t convert_async<float, _Float16>(const float*, _Float16*, int64_t, hipStream_t);
+template hipError_t convert_async<float, __bf16>(const float*, __bf16*, int64_t, hipStream_t);
 template hipError_t noise_sample_async<float>(const float*, const float*, float, float*, int64_t, int64_t, hipStream_t);
 template hipError_t noise_sample_async<double>(const double*, const double*, double, double*, int64_t, int64_t, hipStream_t);
 template hipError_t round_async<float>(const double*, float*, int64_t, hipStream_t);
