@@ -1,6 +1,6 @@
 """Benchmark of the morphocore_amd hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..7] [--no-cpu-baseline] [--no-extra]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..8] [--no-cpu-baseline] [--no-extra]
 
 K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
 millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
@@ -21,7 +21,9 @@ extension, or the C oracle, on a bounded sample on the host cores, in a child pr
 --config 1..5 are BASELINE.json's configs[0..4]. --config 6 and 7 are workloads of the fused
 compositions at configs[3]'s float64 shape, per-channel merges and one 3x3 element: the opening
 (nn.Opening's default form) and sigma_layer, each as one fused operator; their lines also carry the
-same step run as the reference's composition of operators ("composition_step").
+same step run as the reference's composition of operators ("composition_step"). --config 8 is
+configs[3] in float16 (16-bit storage, float32 arithmetic; the reference has no 16-bit path, so its
+CPU baseline runs float32 on the same values).
 
 --kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
 rocprofv3 counter runs.
@@ -64,7 +66,17 @@ CONFIGS = {
     7: dict(name="sigma_layer fwd+bwd fp64 (erosion and dilation blended, merge=identity), fused", kind="sigma", dtype="f64",
             x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
             sample=dict(x=(4, 128, 112, 112)), key="sigma_identity_f64"),
+    8: dict(name="dilation fwd+bwd fp16 merge=identity", kind="morpho", op="dilation", merge="identity", dtype="f16",
+            x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
+            sample=dict(x=(4, 128, 112, 112)), key="dilation_identity_f16"),
 }
+
+# Bench dtypes: torch dtype and bytes per element.
+DTYPES = {"f64": ("float64", 8), "f32": ("float32", 4), "f16": ("float16", 2), "bf16": ("bfloat16", 2)}
+
+
+def esize(cfg):
+    return DTYPES[cfg["dtype"]][1]
 
 
 def config_key(config):
@@ -99,7 +111,7 @@ def parse():
 # Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
 # after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
 # millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
-DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20)}
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20), 8: (200, 20)}
 
 
 def taps(cfg, x_shape=None):
@@ -110,12 +122,14 @@ def taps(cfg, x_shape=None):
 
 
 def make_inputs(cfg, torch, dev):
-    dtype = torch.float64 if cfg["dtype"] == "f64" else torch.float32
+    dtype = getattr(torch, DTYPES[cfg["dtype"]][0])
+    gdt = torch.float64 if dtype == torch.float64 else torch.float32  # 16-bit inputs: drawn in float32, then rounded
     g = torch.Generator().manual_seed(0)
     kind, low, scale = cfg["x_dist"]
-    x = torch.rand(*cfg["x"], generator=g, dtype=dtype) * scale + low if kind == "rand" else torch.randn(*cfg["x"], generator=g, dtype=dtype)
+    x = torch.rand(*cfg["x"], generator=g, dtype=gdt) * scale + low if kind == "rand" else torch.randn(*cfg["x"], generator=g, dtype=gdt)
+    x = x.to(dtype)
     nw = 3 if cfg["kind"] == "stack" else 1
-    ws = [torch.randn(*cfg["w"], generator=g, dtype=dtype) * cfg["w_std"] for _ in range(nw)]
+    ws = [(torch.randn(*cfg["w"], generator=g, dtype=gdt) * cfg["w_std"]).to(dtype) for _ in range(nw)]
     return x.to(dev), [w.to(dev) for w in ws], dtype
 
 
@@ -127,7 +141,8 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
     B, Cin, H, W = cfg["x"]
     Cout = cfg["w"][0]
     gen = torch.Generator(device=dev).manual_seed(1)
-    grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
+    grad = torch.randn((B, Cout, H, W), generator=gen, dtype=torch.float64 if dtype == torch.float64 else torch.float32,
+                       device=dev).to(dtype)
 
     # A step is a list of (forward, backward) phases: one per alpha of the smorph sweep (each alpha's
     # backward runs before the next alpha's forward, so one alpha's saved state is live at a time),
@@ -213,7 +228,7 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
     Cout, Cw, KH, KW = cfg["w"]
     geom = (B, Cin, Cout, Cw, H, W, KH, KW)
     t = taps(cfg)
-    esz = 8 if cfg["dtype"] == "f64" else 4
+    esz = esize(cfg)
     if cfg["kind"] == "pair":
         # The fused forward: x read once, the output and one tap byte per stage written once.
         first = 1 if cfg["first"] == "erosion" else 0
@@ -294,17 +309,17 @@ def step_work(cfg):
     B, Cin, H, W = cfg["x"]
     Cout = cfg["w"][0]
     if cfg["kind"] == "morpho" and cfg.get("bound") == "hbm":
-        esz = 8 if cfg["dtype"] == "f64" else 4
+        esz = esize(cfg)
         return 5 * B * Cin * H * W * esz, "bytes"
     if cfg["kind"] == "pair":
         # Forward: x read, output and two tap bytes written; backward: grad_out and two tap bytes
         # read, grad_x written.
-        esz = 8 if cfg["dtype"] == "f64" else 4
+        esz = esize(cfg)
         return B * Cin * H * W * (4 * esz + 4), "bytes"
     if cfg["kind"] == "sigma":
         # Forward: x read, output and two tap bytes written; backward: x, grad_out and two tap bytes
         # read, grad_x written.
-        esz = 8 if cfg["dtype"] == "f64" else 4
+        esz = esize(cfg)
         return B * Cin * H * W * (5 * esz + 4), "bytes"
     if cfg["kind"] == "morpho":
         return (None if B * Cout * H * W < (1 << 20) else (4 * t + 2 * B * Cout * Cin * H * W, "flop"))
@@ -408,6 +423,8 @@ def cpu_baseline(cfg, seconds):
         return {"value": None, "unit": "output-elements/s", "cores": threads, "kind": None, "sample": "failed: " + r.stderr[-300:]}
     res = json.loads(r.stdout.strip().splitlines()[-1])
     desc = f"x {tuple(sx)}, w {tuple(cfg['w'])}, fwd+bwd, {res['steps']} steps after one warm-up"
+    if cfg["dtype"] in ("f16", "bf16"):
+        desc += ", in float32 (the reference has no 16-bit path) on the same 16-bit values"
     if cfg["kind"] == "smorph":
         desc += ", alpha = 1 (one point of the sweep)"
     out = {"value": res["output_elements"] / res["seconds_per_step"], "unit": "output-elements/s", "cores": res["threads"],
@@ -513,7 +530,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64" if cfg["dtype"] == "f64" else "f32",
+        "dtype": cfg["dtype"],
         "data": "synthetic (seeded torch generators), inputs resident in HBM",
         "config": {"workload": f"{config_key(args.config)}: {cfg['name']}", "x": list(cfg["x"]), "w": list(cfg["w"]),
                    "parallelism": "none (1 GPU)"},

@@ -34,11 +34,12 @@
 namespace mca
 {
 
-template <typename T>
+// ST: the storage type of grad_output (float16 / bfloat16 gradients of float32 kernels, else T).
+template <typename T, typename ST = T>
 struct PackedParams
 {
     const int32_t* __restrict__ idx;
-    const T* __restrict__ gout;
+    const ST* __restrict__ gout;
     Acc* __restrict__ gin;  // double accumulator of grad_input (the output itself for float64)
     T* __restrict__ part;
     Geom g;
@@ -47,8 +48,8 @@ struct PackedParams
     int64_t chunk;
 };
 
-template <typename T, int OP>
-__global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedParams<T> p)
+template <typename T, int OP, typename ST = T>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedParams<T, ST> p)
 {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Acc* bins = reinterpret_cast<Acc*>(smem_raw);
@@ -75,7 +76,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
         const int64_t pix = n - b * plane;
         const int h = (int)(pix / g.W), wc = (int)(pix - (int64_t)h * g.W);
         const int64_t gi = (b * g.Cout + o) * plane + pix;
-        const T gv = p.gout[gi];
+        const T gv = (T)p.gout[gi];
         if (gv == T(0)) continue;
         const int32_t packed = p.idx[gi];
         const int c = packed >> 16, k = packed & 0xFFFF;
@@ -94,12 +95,12 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
     }
 }
 
-template <typename T>
+template <typename T, typename ST = T>
 struct TapsParams
 {
     const void* __restrict__ taps;
-    const T* __restrict__ gout;
-    T* __restrict__ gin;
+    const ST* __restrict__ gout;
+    ST* __restrict__ gin;
     T* __restrict__ part;
     Geom g;
     Tiling t;
@@ -466,8 +467,8 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_planes_kernel(const TapsPara
 // each grad_input pixel of the tile once: no zero fill, no atomics on grad_input. grad_weight sums
 // sign * g by saved tap in LDS bins with one copy per lane of a half wave (conflict free), one
 // partial slot per (batch element, tile). IDENTITY has no 1 / Cin scale.
-template <typename T, int OP, int KH, int KW, int RH>
-__global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const TapsParams<T> p)
+template <typename T, int OP, int KH, int KW, int RH, typename ST = T>
+__global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const TapsParams<T, ST> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1, WR = RH + KH - 1;
@@ -508,12 +509,12 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const Ta
     T pg[NS];
     int pt[NS];
     auto load = [&](int c) {
-        const T* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + c) * plane;
+        const ST* __restrict__ gp = p.gout + ((int64_t)b * g.Cout + c) * plane;
         const uint8_t* __restrict__ tp = static_cast<const uint8_t*>(p.taps) + ((int64_t)b * g.Cout + c) * plane;
 #pragma unroll
         for (int j = 0; j < NS; ++j)
         {
-            pg[j] = gp[off[j]];
+            pg[j] = (T)gp[off[j]];
             pt[j] = tp[off[j]];
         }
     };
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const Ta
                 gw[rr][kw] = gs[(wave * RH + rr) * COLS + lane + kw];
                 tw[rr][kw] = ts[(wave * RH + rr) * COLS + lane + kw];
             }
-        T* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + c) * plane;
+        ST* __restrict__ gplane = p.gin + ((int64_t)b * g.Cin + c) * plane;
         Acc* bl = bins + (lane & (NC - 1));
 #pragma unroll
         for (int r = 0; r < RH; ++r)
@@ -557,7 +558,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_ident_gather_kernel(const Ta
 #pragma unroll
                 for (int kw = 0; kw < KW; ++kw) s += tw[r + kh][kw] == kh * KW + kw ? (Acc)gw[r + kh][kw] : Acc(0);
             const int h = h0 + wave * RH + r;
-            if (h < g.H && wc < g.W) gplane[(int64_t)h * g.W + wc] = (T)s;
+            if (h < g.H && wc < g.W) gplane[(int64_t)h * g.W + wc] = (ST)(T)s;
             // grad_weight: this lane's own output pixel (h, wc), staged at (row r + PH, column PW).
             const int k = tw[r + PH][PW];
             if (k >= 0) lds_add(&bl[k * NC], (Acc)(OP == DILATION ? gw[r + PH][PW] : -gw[r + PH][PW]));
@@ -886,6 +887,67 @@ size_t half_backward_workspace(int merge, bool has_indices, const Geom& g)
     return bytes;
 }
 
+// The kernels that read grad_output once per output pixel and write grad_input once per input pixel
+// take the 16-bit data directly: the max / min scatter (double accumulator rounded into grad_input)
+// and the IDENTITY gather. grad_weight is summed in float32 partial slots and rounded at the end.
+template <typename ST, int OP>
+static hipError_t half_direct(int merge, const void* indices, const ST* grad_out, ST* grad_in, ST* grad_w, const Geom& g, unsigned char* ws,
+                              float* gw, hipStream_t stream)
+{
+    hipError_t err;
+    const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    size_t part_bytes;
+    int nslots;
+    partials<float>(merge, g, part_bytes, nslots);
+    float* part = reinterpret_cast<float*>(ws);
+    ws += align_up(part_bytes);
+    float* scratch = reinterpret_cast<float*>(ws);
+    ws += align_up(reduce_slots_scratch<float>(nslots, wnumel));
+    if (packed_winners(merge))
+    {
+        const PackedPlan s = plan_packed<float>(g);
+        const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
+        if (!s.lds_bins)
+            if ((err = fill_async<float>(part, (int64_t)s.nchunks * wnumel, 0.0f, stream)) != hipSuccess) return err;
+        Acc* gin_acc = reinterpret_cast<Acc*>(ws);
+        if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
+        PackedParams<float, ST> p{};
+        p.idx = static_cast<const int32_t*>(indices);
+        p.gout = grad_out;
+        p.gin = gin_acc;
+        p.part = part;
+        p.g = g;
+        p.nchunks = s.nchunks;
+        p.lds_bins = s.lds_bins ? 1 : 0;
+        p.chunk = s.chunk;
+        morpho_bwd_packed_kernel<float, OP, ST><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        if ((err = round_async<ST>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
+    }
+    else
+    {
+        const TapsPlan s = plan_taps<float>(merge, g);
+        TapsParams<float, ST> p{};
+        p.taps = indices;
+        p.gout = grad_out;
+        p.gin = grad_in;
+        p.part = part;
+        p.g = g;
+        p.t = s.t;
+        p.ig = s.ig;
+        p.nig = s.nig;
+        constexpr int RH = rows_per_wave<float>();
+        const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
+        if (g.KH == 3)
+            morpho_bwd_ident_gather_kernel<float, OP, 3, 3, RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
+        else
+            morpho_bwd_ident_gather_kernel<float, OP, 5, 5, RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+    if ((err = reduce_slots_async<float>(part, nslots, wnumel, gw, scratch, stream)) != hipSuccess) return err;
+    return convert_async<float, ST>(gw, grad_w, wnumel, stream);
+}
+
 template <typename ST>
 hipError_t half_backward(int op, int merge, bool replicate, float fill, const ST* x, const ST* w, const void* indices, const ST* grad_out,
                          ST* grad_in, ST* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
@@ -907,6 +969,10 @@ hipError_t half_backward(int op, int merge, bool replicate, float fill, const ST
     }
     const int64_t gout_n = (int64_t)g.B * g.Cout * g.plane(), gin_n = (int64_t)g.B * g.Cin * g.plane();
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    if (gout_n == 0) return morpho_backward<float>(op, merge, replicate, fill, nullptr, nullptr, indices, gout, gin, gw, g, ws, inner, stream);
+    if (packed_winners(merge) || plan_taps<float>(merge, g).gather)
+        return op == DILATION ? half_direct<ST, DILATION>(merge, indices, grad_out, grad_in, grad_w, g, ws, gw, stream)
+                              : half_direct<ST, EROSION>(merge, indices, grad_out, grad_in, grad_w, g, ws, gw, stream);
     if ((err = convert_async<ST, float>(grad_out, gout, gout_n, stream)) != hipSuccess) return err;
     // With the winners given, the float32 kernels read neither the input nor the element.
     if ((err = morpho_backward<float>(op, merge, replicate, fill, nullptr, nullptr, indices, gout, gin, gw, g, ws, inner, stream)) !=

@@ -139,6 +139,8 @@ template hipError_t convert_async<float, __bf16>(const float*, __bf16*, int64_t,
 template hipError_t noise_sample_async<float>(const float*, const float*, float, float*, int64_t, int64_t, hipStream_t);
 template hipError_t noise_sample_async<double>(const double*, const double*, double, double*, int64_t, int64_t, hipStream_t);
 template hipError_t round_async<float>(const double*, float*, int64_t, hipStream_t);
+template hipError_t round_async<_Float16>(const double*, _Float16*, int64_t, hipStream_t);
+template hipError_t round_async<__bf16>(const double*, __bf16*, int64_t, hipStream_t);
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
 template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
 template size_t reduce_slots_scratch<float>(int, int64_t);

@@ -26,9 +26,12 @@ PADDINGS = {"zero": 0, "geodesic": 1, "constant": 2, "replicate": 3}
 
 
 def _inputs(spec, torch):
+    # 16-bit workloads: the reference has no 16-bit path; it runs float32 on the same (rounded) values.
     dtype = torch.float64 if spec.get("dtype") == "f64" else torch.float32
     g = torch.Generator().manual_seed(0)
     x = (torch.rand(*spec["x"], generator=g, dtype=torch.float64) * spec.get("x_scale", 1.0) + spec.get("x_low", 0.0)).to(dtype)
+    if spec.get("dtype") in ("f16", "bf16"):
+        x = x.to(getattr(torch, "float16" if spec["dtype"] == "f16" else "bfloat16")).to(dtype)
     ws = [(torch.randn(*spec["w"], generator=g, dtype=torch.float64) * spec.get("w_std", 0.1)).to(dtype)
           for _ in range(3 if spec["kind"] == "stack" else 1)]
     return x, ws, dtype
