@@ -29,6 +29,9 @@
 // grad_input; grad_weight always receives sign * g (sign -1 for erosion).
 // When the forward pass did not save its winners, the forward kernel recomputes them into the
 // workspace first.
+#include <algorithm>
+#include <cstdlib>
+
 #include "launch.hpp"
 
 namespace mca
@@ -722,7 +725,29 @@ static void partials(int merge, const Geom& g, size_t& part_bytes, int& nslots)
     }
 }
 
-// Workspace layout: [partial slots | reduction scratch | (recomputed winners | scratch output)].
+// When the forward kept no per-pair taps (sum / mean / identity), the backward recomputes them for
+// this many batch elements at a time: as many as fit 1 GiB of taps and scratch output
+// (MORPHOCORE_AMD_RECOMPUTE_BYTES overrides it), at least one, so that the fallback's memory stays
+// bounded whatever the batch. (Max / min winners, one int32 per output pixel, are recomputed whole.)
+static size_t recompute_bytes()
+{
+    const char* v = std::getenv("MORPHOCORE_AMD_RECOMPUTE_BYTES");
+    return v && *v ? (size_t)std::strtoull(v, nullptr, 10) : (size_t(1) << 30);
+}
+
+template <typename T>
+static int recompute_batch(int merge, const Geom& g)
+{
+    if (packed_winners(merge)) return g.B;
+    Geom one = g;
+    one.B = 1;
+    const size_t per = indices_bytes(merge, one) + (size_t)one.Cout * one.plane() * sizeof(T);
+    const int64_t fit = per > 0 ? (int64_t)(recompute_bytes() / per) : g.B;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(fit, g.B));
+}
+
+// Workspace layout: [partial slots | reduction scratch | (recomputed winners | scratch output, for
+// recompute_batch batch elements)].
 template <typename T>
 size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
 {
@@ -730,7 +755,12 @@ size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
     int nslots;
     partials<T>(merge, g, part_bytes, nslots);
     size_t bytes = align_up(part_bytes) + align_up(reduce_slots_scratch<T>(nslots, (int64_t)g.Cout * g.Cw * g.taps()));
-    if (!has_indices) bytes += align_up(indices_bytes(merge, g)) + align_up((size_t)g.B * g.Cout * g.plane() * sizeof(T));
+    if (!has_indices)
+    {
+        Geom c = g;
+        c.B = recompute_batch<T>(merge, g);
+        bytes += align_up(indices_bytes(merge, c)) + align_up((size_t)c.B * c.Cout * c.plane() * sizeof(T));
+    }
     if (packed_winners(merge) && sizeof(T) != sizeof(Acc)) bytes += align_up((size_t)g.B * g.Cin * g.plane() * sizeof(Acc));
     return bytes;
 }
@@ -758,7 +788,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     ws += align_up(part_bytes);
     T* scratch = reinterpret_cast<T*>(ws);
     ws += align_up(reduce_slots_scratch<T>(nslots, wnumel));
-    if (!indices)
+    if (!indices && packed)
     {
         // The forward pass did not keep its winners: recompute them (and a scratch output).
         void* idx = ws;
@@ -797,59 +827,84 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     }
 
     const TapsPlan s = plan_taps<T>(merge, g);
-    TapsParams<T> p{};
-    p.taps = indices;
-    p.gout = grad_out;
-    p.gin = grad_in;
-    p.part = part;
-    p.g = g;
-    p.t = s.t;
-    p.ig = s.ig;
-    p.nig = s.nig;
-    p.oc = s.oc;
-    p.ncopy_log2 = __builtin_ctz((unsigned)s.ncopy);
-    p.kw_div = (65536u + (unsigned)g.KW - 1) / (unsigned)g.KW;
-    p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
-    constexpr int RH = rows_per_wave<T>();
-    const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
-    const bool wide = pair_tap_bytes(g) == 2;
-    if (s.gather)
+    // Without saved taps, batch chunks: each chunk's taps recomputed into the workspace, then routed
+    // into its own grad_input rows and partial slots (slots are per batch element and tile).
+    const int chunk = indices ? g.B : recompute_batch<T>(merge, g);
+    void* idx_ws = ws;
+    T* out_ws = nullptr;
+    if (!indices)
     {
-        switch (g.KH)
+        Geom c = g;
+        c.B = chunk;
+        out_ws = reinterpret_cast<T*>(ws + align_up(indices_bytes(merge, c)));
+    }
+    const int64_t plane = g.plane();
+    for (int b0 = 0; b0 < g.B; b0 += chunk)
+    {
+        Geom gc = g;
+        gc.B = std::min(chunk, g.B - b0);
+        const void* taps = indices;
+        if (!indices)
         {
-            case 3: morpho_bwd_ident_gather_kernel<T, OP, 3, 3, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
-            default: morpho_bwd_ident_gather_kernel<T, OP, 5, 5, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+            if ((err = morpho_forward<T>(OP, merge, replicate, fill, x + (int64_t)b0 * g.Cin * plane, w + (int64_t)b0 * g.wbs, out_ws, idx_ws,
+                                         gc, stream)) != hipSuccess)
+                return err;
+            taps = idx_ws;
         }
-    }
-    else if (s.planes)
-    {
-        if (s.t.rh == 4)
-            morpho_bwd_planes_kernel<T, OP, 4><<<blocks, BLOCK, s.lds, stream>>>(p);
+        TapsParams<T> p{};
+        p.taps = taps;
+        p.gout = grad_out + (int64_t)b0 * g.Cout * plane;
+        p.gin = grad_in + (int64_t)b0 * g.Cin * plane;
+        p.part = part + (int64_t)b0 * s.t.ntiles() * wnumel;
+        p.g = gc;
+        p.t = s.t;
+        p.ig = s.ig;
+        p.nig = s.nig;
+        p.oc = s.oc;
+        p.ncopy_log2 = __builtin_ctz((unsigned)s.ncopy);
+        p.kw_div = (65536u + (unsigned)g.KW - 1) / (unsigned)g.KW;
+        p.scale = merge == MERGE_AVERAGE ? T(1) / (T)g.Cin : T(1);
+        constexpr int RH = rows_per_wave<T>();
+        const unsigned blocks = (unsigned)((int64_t)gc.B * s.t.ntiles() * s.nig);
+        const bool wide = pair_tap_bytes(g) == 2;
+        if (s.gather)
+        {
+            switch (g.KH)
+            {
+                case 3: morpho_bwd_ident_gather_kernel<T, OP, 3, 3, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+                default: morpho_bwd_ident_gather_kernel<T, OP, 5, 5, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+            }
+        }
+        else if (s.planes)
+        {
+            if (s.t.rh == 4)
+                morpho_bwd_planes_kernel<T, OP, 4><<<blocks, BLOCK, s.lds, stream>>>(p);
+            else
+                morpho_bwd_planes_kernel<T, OP, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+        }
+        else if (merge == MERGE_IDENTITY)
+        {
+            if (wide)
+                morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
+            else
+                morpho_bwd_taps_kernel<T, OP, uint8_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
+        }
+        else if (s.ig == 2)
+        {
+            if (wide)
+                morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+            else
+                morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+        }
         else
-            morpho_bwd_planes_kernel<T, OP, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
+        {
+            if (wide)
+                morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
+            else
+                morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
+        }
+        if ((err = hipGetLastError()) != hipSuccess) return err;
     }
-    else if (merge == MERGE_IDENTITY)
-    {
-        if (wide)
-            morpho_bwd_taps_kernel<T, OP, uint16_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
-        else
-            morpho_bwd_taps_kernel<T, OP, uint8_t, true, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
-    }
-    else if (s.ig == 2)
-    {
-        if (wide)
-            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
-        else
-            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 2><<<blocks, BLOCK, s.lds, stream>>>(p);
-    }
-    else
-    {
-        if (wide)
-            morpho_bwd_taps_kernel<T, OP, uint16_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
-        else
-            morpho_bwd_taps_kernel<T, OP, uint8_t, false, RH, 1><<<blocks, BLOCK, s.lds, stream>>>(p);
-    }
-    if ((err = hipGetLastError()) != hipSuccess) return err;
     return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
 }
 

@@ -791,3 +791,34 @@ def test_saved_and_recomputed_winners_give_the_same_gradients(merge):
     # Accumulation order of float atomics may differ between runs: compare within the contract.
     assert normwise_error(_np(grads[0][1]), _np(grads[1][1])) <= 1e-6
     assert normwise_error(_np(grads[0][2]), _np(grads[1][2])) <= 1e-6
+
+
+@pytest.mark.parametrize("merge", ["sum", "mean", "identity"])
+@pytest.mark.parametrize("K", [3, 7])
+def test_recomputed_taps_in_batch_chunks(merge, K, monkeypatch):
+    """Without saved taps the backward recomputes them a few batch elements at a time
+    (MORPHOCORE_AMD_RECOMPUTE_BYTES bounds the buffer): one element per chunk gives the gradients of
+    the whole-batch recomputation, and both match the oracle."""
+    mca, _, _ = _mca()
+    dev = torch.device("cuda")
+    B, Cin, Cout, H, W = 5, 3, 4, 21, 70
+    if merge == "identity":
+        Cout = Cin
+    x = seeded(36, B, Cin, H, W)
+    w = seeded(37, *_weight_shape(merge, Cin, Cout, K, K), kind="randn", scale=0.1)
+    g = seeded(38, B, Cout, H, W, kind="randn")
+    grads = []
+    for budget in (None, "1"):
+        if budget is None:
+            monkeypatch.delenv("MORPHOCORE_AMD_RECOMPUTE_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("MORPHOCORE_AMD_RECOMPUTE_BYTES", budget)
+        xd = x.to(dev).requires_grad_(True)
+        wd = w.to(dev).requires_grad_(True)
+        out = mca.functional.dilation(xd, wd, merge, "replicate", save_indices=False)
+        out.backward(g.to(dev))
+        grads.append((_np(xd.grad), _np(wd.grad)))
+    gx, gw = O.morpho_backward(O.DILATION, O.MERGES[merge], O.REPLICATE, 0.0, x.numpy(), w.numpy(), g.numpy())
+    for got in grads:
+        assert normwise_error(got[0], gx) <= 1e-6 and normwise_error(got[1], gw) <= 1e-6
+    assert np.array_equal(grads[0][1], grads[1][1])
