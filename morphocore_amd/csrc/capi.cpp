@@ -45,6 +45,8 @@ int make_geom(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64
     if (!fits_int(B) || !fits_int(Cin) || !fits_int(Cout) || !fits_int(Cw) || !fits_int(H) || !fits_int(W) || !fits_int(KH) || !fits_int(KW))
         return fail("Tensor dimensions must be non negative and below 2^31");
     if (KH < 1 || KW < 1) return fail("The structuring element must have at least one tap");
+    // The kernels address a pixel within its plane with 32-bit offsets.
+    if (H * W > 0x7fffffff) return fail("Image planes of more than 2^31 - 1 pixels are not supported");
     if (merge == mca::MERGE_IDENTITY)
     {
         if (Cout != Cin) return fail("Identity mode requires weight.shape[0] == input.shape[1]");

@@ -209,3 +209,8 @@ def test_sigma_rejects_bad_arguments():
     assert "saved taps" in lib.mca_last_error().decode()
     assert lib.mca_morpho_sigma_backward_f32(0, inf, -inf, *common, t, t, None, None, None, None, None, *pg, None, need - 1, None) == 1
     assert "Workspace too small" in lib.mca_last_error().decode()
+
+
+def test_rejects_planes_beyond_32_bit_offsets():
+    assert _forward(2, (1, 1, 1, 1, 65536, 32768, 3, 3)) == 1
+    assert "2^31 - 1 pixels" in _native.lib().mca_last_error().decode()
