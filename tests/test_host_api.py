@@ -174,3 +174,73 @@ def test_composition_layers_construction():
     s = mca.nn.SigmaLayer(3, 4, 3)
     assert [tuple(p.shape) for p in s.parameters()] == [(4, 3, 3, 3), (4, 3)]
     assert set(mca.functional.__all__) >= {"opening", "closing", "sigma_layer"}
+
+
+class _RecordingOps:
+    """Stands in for torch.ops.morphocore in the functional layer: records each operator call and
+    returns a tensor of the output's shape (no kernel runs on the CPU)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        def op(x, *args):
+            self.calls.append((name, args))
+            w = args[0]
+            return torch.zeros(x.shape[0], w.shape[0], *x.shape[2:], dtype=x.dtype)
+        return op
+
+
+@pytest.mark.parametrize("kind", ["opening", "closing"])
+def test_fused_pair_routing(kind, monkeypatch):
+    """Per-channel merges go to the fused operator (erosion's element flipped, each stage's dropout
+    drawn first, noise only in training); dropout and noise together run the composition, whose draws
+    interleave; other merges always run the composition."""
+    import importlib
+
+    _pair, dil_mod, ero_mod = (importlib.import_module(f"morphocore_amd.functional.{m}") for m in ("_pair", "dilation", "erosion"))
+    rec = _RecordingOps()
+    monkeypatch.setattr(_pair, "ops", rec)
+    monkeypatch.setattr(ero_mod, "ops", rec)
+    monkeypatch.setattr(dil_mod, "ops", rec)
+    f = getattr(mca.functional, kind)
+    x = torch.zeros(2, 3, 8, 9)
+    w1 = torch.arange(27.0).reshape(3, 1, 3, 3)
+    w2 = -torch.arange(27.0).reshape(3, 1, 3, 3)
+    f(x, w1, w2, 'identity', 'geodesic', noise_scale=0.3)
+    name, args = rec.calls[-1]
+    assert name == "opening_closing" and len(rec.calls) == 1
+    first, second = (args[0], args[1])
+    if kind == "opening":
+        assert torch.equal(first, w1.flip((-2, -1))) and torch.equal(second, w2) and args[2] == 1
+    else:
+        assert torch.equal(first, w1) and torch.equal(second, w2.flip((-2, -1))) and args[2] == 0
+    assert args[-1] == 0.0  # noise only in training
+    rec.calls.clear()
+    f(x, w1, w2, 'identity', training=True, weight_dropout=0.5, noise_scale=0.3)
+    assert [c[0] for c in rec.calls] == (["erosion", "dilation"] if kind == "opening" else ["dilation", "erosion"])
+    rec.calls.clear()
+    f(x, w1, w2, 'identity', training=True, weight_dropout=0.5)
+    assert [c[0] for c in rec.calls] == ["opening_closing"]
+    rec.calls.clear()
+    f(x, torch.zeros(3, 3, 3, 3), w2, 'sum')
+    assert [c[0] for c in rec.calls] == (["erosion", "dilation"] if kind == "opening" else ["dilation", "erosion"])
+
+
+def test_fused_sigma_routing(monkeypatch):
+    import importlib
+
+    sig_mod, dil_mod, ero_mod = (importlib.import_module(f"morphocore_amd.functional.{m}") for m in ("sigma_layer", "dilation", "erosion"))
+    rec = _RecordingOps()
+    for m in (sig_mod, ero_mod, dil_mod):
+        monkeypatch.setattr(m, "ops", rec)
+    x = torch.zeros(2, 3, 8, 9)
+    w = torch.arange(27.0).reshape(3, 1, 3, 3)
+    a = torch.full((3, 1), 0.5)
+    mca.functional.sigma_layer(x, w, a, 'identity')
+    name, args = rec.calls[-1]
+    assert name == "sigma_identity" and torch.equal(args[0], w.flip((-2, -1))) and torch.equal(args[1], w)
+    assert torch.allclose(args[2], torch.sigmoid(a.mean(dim=1)))
+    rec.calls.clear()
+    mca.functional.sigma_layer(x, w, a.double(), 'identity')  # mixed dtypes: the composition
+    assert [c[0] for c in rec.calls] == ["erosion", "dilation"]
