@@ -618,6 +618,9 @@ static PackedPlan plan_packed(const Geom& g)
     return s;
 }
 
+// Rows per wave of the IDENTITY gather kernel.
+constexpr int GATHER_RH = 4;
+
 struct TapsPlan
 {
     Tiling t;
@@ -643,6 +646,10 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     if (ident && g.KH == g.KW && (g.KH == 3 || g.KH == 5))
     {
+        // 4 rows per wave for every dtype: 16-row tiles (float32 / 16-bit gathers 18-26% faster than
+        // with 8 rows, measured at configs[3]'s shape).
+        s.t = make_tiling(g, GATHER_RH);
+        s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
         // Up to 8 consecutive channels per workgroup, the next channel's loads in flight behind
         // each channel's gather.
         s.gather = true;
@@ -871,8 +878,8 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         {
             switch (g.KH)
             {
-                case 3: morpho_bwd_ident_gather_kernel<T, OP, 3, 3, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
-                default: morpho_bwd_ident_gather_kernel<T, OP, 5, 5, RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+                case 3: morpho_bwd_ident_gather_kernel<T, OP, 3, 3, GATHER_RH><<<blocks, BLOCK, 0, stream>>>(p); break;
+                default: morpho_bwd_ident_gather_kernel<T, OP, 5, 5, GATHER_RH><<<blocks, BLOCK, 0, stream>>>(p); break;
             }
         }
         else if (s.planes)
@@ -991,12 +998,11 @@ static hipError_t half_direct(int merge, const void* indices, const ST* grad_out
         p.t = s.t;
         p.ig = s.ig;
         p.nig = s.nig;
-        constexpr int RH = rows_per_wave<float>();
         const unsigned blocks = (unsigned)((int64_t)g.B * s.t.ntiles() * s.nig);
         if (g.KH == 3)
-            morpho_bwd_ident_gather_kernel<float, OP, 3, 3, RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
+            morpho_bwd_ident_gather_kernel<float, OP, 3, 3, GATHER_RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
         else
-            morpho_bwd_ident_gather_kernel<float, OP, 5, 5, RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
+            morpho_bwd_ident_gather_kernel<float, OP, 5, 5, GATHER_RH, ST><<<blocks, BLOCK, 0, stream>>>(p);
         if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if ((err = reduce_slots_async<float>(part, nslots, wnumel, gw, scratch, stream)) != hipSuccess) return err;
