@@ -1,6 +1,6 @@
 """Benchmark of the morphocore_amd hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..8] [--no-cpu-baseline] [--no-extra]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..9] [--no-cpu-baseline] [--no-extra]
 
 K and W default per config (DEFAULT_STEPS below): enough steps for steady clocks on the
 millisecond-scale configs, one or two on the half-second ones, so every default run ends in minutes.
@@ -23,7 +23,8 @@ compositions at configs[3]'s float64 shape, per-channel merges and one 3x3 eleme
 (nn.Opening's default form) and sigma_layer, each as one fused operator; their lines also carry the
 same step run as the reference's composition of operators ("composition_step"). --config 8 is
 configs[3] in float16 (16-bit storage, float32 arithmetic; the reference has no 16-bit path, so its
-CPU baseline runs float32 on the same values).
+CPU baseline runs float32 on the same values). --config 9 is smorph with the SMOOTH channel merge
+(smorph_scm, a beta per output channel) at configs[2]'s shape, alpha 1 and beta 1.
 
 --kernel-only and --copy-calibration launch only the dominant kernel, or a plain device copy, for
 rocprofv3 counter runs.
@@ -69,6 +70,9 @@ CONFIGS = {
     8: dict(name="dilation fwd+bwd fp16 merge=identity", kind="morpho", op="dilation", merge="identity", dtype="f16",
             x=(32, 128, 112, 112), w=(128, 1, 3, 3), x_dist=("rand", -1.0, 2.0), w_std=0.1, bound="hbm",
             sample=dict(x=(4, 128, 112, 112)), key="dilation_identity_f16"),
+    9: dict(name="smorph_scm fwd+bwd fp32 (SMOOTH merge, alpha 1, beta 1)", kind="scm", dtype="f32", x=(8, 64, 256, 256),
+            w=(64, 64, 7, 7), x_dist=("randn", 0.0, 1.0), w_std=0.1, bound="valu", sample=dict(x=(1, 64, 64, 64)),
+            key="smorph_scm_f32"),
 }
 
 # Bench dtypes: torch dtype and bytes per element.
@@ -111,7 +115,7 @@ def parse():
 # Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
 # after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
 # millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
-DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20), 8: (200, 20)}
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20), 8: (200, 20), 9: (2, 1)}
 
 
 def taps(cfg, x_shape=None):
@@ -178,6 +182,12 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
         phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
         n_out = B * Cout * H * W
         params = [xr] + wr
+    elif cfg["kind"] == "scm":
+        alpha = torch.full((Cout, Cin), 1.0, dtype=dtype, device=dev, requires_grad=True)
+        beta = torch.full((Cout,), 1.0, dtype=dtype, device=dev, requires_grad=True)
+        phases = [((lambda: [F.smorph(xr, wr[0], alpha, beta)]), lambda outs: torch.autograd.backward(outs, [grad]))]
+        n_out = B * Cout * H * W
+        params = [xr] + wr + [alpha, beta]
     elif cfg["kind"] in ("sigma", "sigma_composition"):
         alpha = torch.full((Cout, 1), 0.3, dtype=dtype, device=dev, requires_grad=True)
         if cfg["kind"] == "sigma":
@@ -244,6 +254,23 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
 
         what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
+    if cfg["kind"] == "scm":
+        # The SMOOTH merge's backward (generic kernel), the larger part of its step: 18 flop per tap
+        # (SURVEY's smorph convention) plus the soft merge's per-pixel work, not counted.
+        a_p = torch.full((Cout * Cin,), 1.0, dtype=dtype, device=dev)
+        beta = torch.full((Cout,), 1.0, dtype=dtype, device=dev)
+        wt = ws[0]
+        out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
+        mst = torch.empty((2, B, Cout, H, W), dtype=dtype, device=dev)
+        native.smorph_scm_forward(x, wt, a_p, beta, out, mst, geom)
+        gen = torch.Generator(device=dev).manual_seed(2)
+        grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
+        gx, gw, ga, gb = torch.empty_like(x), torch.empty_like(wt), torch.empty_like(a_p), torch.empty_like(beta)
+
+        def launch():
+            native.smorph_scm_backward(x, wt, a_p, beta, out, mst, grad, gx, gw, ga, gb, geom)
+
+        return launch, 18 * t, "flop", "smorph_scm backward, alpha 1, beta 1 (mca_smorph_scm_backward_f32: kernels + reductions)"
     if cfg["kind"] == "sigma":
         # The fused forward: x read once, the output and one tap byte per operation written once.
         pg = (B, Cin, H, W, KH, KW)
@@ -325,6 +352,8 @@ def step_work(cfg):
         return (None if B * Cout * H * W < (1 << 20) else (4 * t + 2 * B * Cout * Cin * H * W, "flop"))
     if cfg["kind"] == "smorph":
         return 26 * t * len(cfg["alphas"]), "flop"
+    if cfg["kind"] == "scm":
+        return 26 * t, "flop"
     return 2 * t + 26 * t + 2 * t, "flop"  # stack: dilation, smorph, erosion (index scatters not counted)
 
 

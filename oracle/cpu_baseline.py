@@ -8,7 +8,7 @@ prints one JSON object:
   {"seconds_per_step": s, "output_elements": n, "kind": "reference"|"port", "threads": t, "steps": k}
 
 Usage: python oracle/cpu_baseline.py '<json spec>' where the spec holds
-  kind: "morpho" | "smorph" | "stack" | "pair" | "sigma", op: "dilation"|"erosion" (pair: the first stage), merge, padding,
+  kind: "morpho" | "smorph" | "stack" | "pair" | "sigma" | "scm", op: "dilation"|"erosion" (pair: the first stage), merge, padding,
   dtype: "f32"|"f64",
   x: [B,C,H,W], w: [Cout,Cw,KH,KW], alpha (smorph), threads, min_seconds.
 """
@@ -59,6 +59,13 @@ def run_reference(spec, threads):
             t = torch.tanh(a).unsqueeze(-1).unsqueeze(-1) if a.dim() == 2 else torch.tanh(a).view(-1, 1, 1, 1)
             wt = t * ((1 - t) / 2 * wr[0].flip(dims=(-2, -1)) + (1 + t) / 2 * wr[0])
             out = ops.smorph(xr, wt, a, merge)
+        elif spec["kind"] == "scm":
+            # smorph with a beta: the SMOOTH channel merge (functional/smorph.py:72-73).
+            a = torch.full((x.shape[1], x.shape[1]), 1.0, dtype=dtype, requires_grad=True)
+            beta = torch.full((wr[0].shape[0],), 1.0, dtype=dtype, requires_grad=True)
+            t = torch.tanh(a).unsqueeze(-1).unsqueeze(-1)
+            wt = t * ((1 - t) / 2 * wr[0].flip(dims=(-2, -1)) + (1 + t) / 2 * wr[0])
+            out = ops.smorph_scm(xr, wt, a, beta)
         elif spec["kind"] == "pair":
             # The reference's opening / closing with per-channel merges and one shared element
             # (functional/opening.py:96-101).
