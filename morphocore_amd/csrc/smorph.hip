@@ -492,7 +492,7 @@ size_t smorph_backward_workspace(int merge, const Geom& g)
 template <typename T, int MK, bool STATS>
 static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t stream)
 {
-    if constexpr (sizeof(T) == 4 && MK != MK_SMOOTH)
+    if constexpr (sizeof(T) == 4)
         if (smorph_static_supported<T>(p.g)) return launch_smorph_fwd_static(MK, STATS, p, stream);
     constexpr int RH = rows_per_wave<T>();
     const int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout;
@@ -695,7 +695,8 @@ hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* b
     p.alpha = alpha;
     p.pout = reinterpret_cast<T*>(workspace);
     p.g = g;
-    p.t = make_tiling(g, rows_per_wave<T>());
+    // The float32 static kernels (one row per wave) write the pair outputs where they exist.
+    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
     hipError_t err = launch_smorph_fwd<T, MK_SMOOTH, false>(p, stream);
     if (err != hipSuccess) return err;
     smorph_soft_merge_kernel<T><<<elementwise_grid(n), BLOCK, 0, stream>>>(p.pout, beta, out, sstats, g);

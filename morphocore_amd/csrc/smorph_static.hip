@@ -395,6 +395,11 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         {
             m = fmaf(Wsum, inv, m);
         }
+        else if constexpr (MK == MK_SMOOTH)
+        {
+            // Every pair's output, merged afterwards by the soft merge (smorph.hip).
+            if (in) p.pout[(((int64_t)b * g.Cout + o) * g.Cin + i) * plane + (int64_t)h * g.W + wc] = Wsum * inv;
+        }
         else
         {
             m = Wsum * inv;
@@ -403,7 +408,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         __syncthreads();
     }
 
-    if (!in) return;
+    if (!in || MK == MK_SMOOTH) return;
     float v = m;
     if constexpr (MK == MK_SUM && !STATS)
     {
@@ -1156,6 +1161,9 @@ static hipError_t fwd_size(int mk, bool stats, const SmorphFwdParams<float>& p, 
         case MK_SUM: smorph_fwd_static<MK_SUM, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MAX: smorph_fwd_static<MK_MAX, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MIN: smorph_fwd_static<MK_MIN, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SMOOTH:
+            if constexpr (!SAVE) smorph_fwd_static<MK_SMOOTH, KS, KS, false, false><<<blocks, BLOCK, 0, stream>>>(p);
+            break;
         default: smorph_fwd_static<MK_IDENT, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
