@@ -422,7 +422,7 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     SmorphBwdPlan s{};
     // The static kernels (smorph_static.hip) use one output row per wave (two from saved statistics)
     // and static LDS.
-    const bool stat = merge != MERGE_SMOOTH && smorph_static_supported<T>(g);
+    const bool stat = smorph_static_supported<T>(g);
     s.t = make_tiling(g, stat ? (saved ? 2 : 1) : rows_per_wave<T>());
     s.ncopy = 16;
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
@@ -725,9 +725,14 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     T* part_b = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
     T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes));
     const int nslots = g.B * s.nstrips;
-    if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
-    if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
-    if ((err = fill_async<T>(part_b, (int64_t)nslots * g.Cin * g.Cout, T(0), stream)) != hipSuccess) return err;
+    const bool stat = smorph_static_supported<T>(g);
+    // The static kernel that keeps its partials in LDS stores every slot entry itself.
+    if (!(stat && smorph_bwd_lds_partials(g, false, true)))
+    {
+        if ((err = fill_async<T>(part_w, (int64_t)nslots * wnumel, T(0), stream)) != hipSuccess) return err;
+        if ((err = fill_async<T>(part_a, (int64_t)nslots * s.npairs, T(0), stream)) != hipSuccess) return err;
+        if ((err = fill_async<T>(part_b, (int64_t)nslots * g.Cin * g.Cout, T(0), stream)) != hipSuccess) return err;
+    }
 
     SmorphBwdParams<T> p{};
     p.x = x;
@@ -748,10 +753,21 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     p.ncopy = s.ncopy;
     p.npairs = s.npairs;
     p.scale = T(1);
-    constexpr int RH = rows_per_wave<T>();
-    const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
-    smorph_bwd_kernel<T, MK_SMOOTH, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+    bool launched = false;
+    if constexpr (sizeof(T) == 4)
+        if (stat)
+        {
+            // The float32 static kernel, recomputing each pair's statistics (one row per wave).
+            if ((err = launch_smorph_bwd_static(MK_SMOOTH, p, stream)) != hipSuccess) return err;
+            launched = true;
+        }
+    if (!launched)
+    {
+        constexpr int RH = rows_per_wave<T>();
+        const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
+        smorph_bwd_kernel<T, MK_SMOOTH, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
     if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
     if ((err = reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream)) != hipSuccess) return err;
     // grad_beta[o]: the partial rows [slot][i] summed in (slot, i) order.

@@ -223,16 +223,18 @@ inline bool smorph_static_supported(const Geom& g)
         return g.KH == g.KW && (g.KH == 3 || g.KH == 5 || g.KH == 7 || g.KH == 11) && g.plane() <= 0x7fffffff;
 }
 
-// The static backward up to 5x5 sums each workgroup's grad_weight / grad_alpha partials over its
-// tiles in LDS (at most this many values: output channels x (taps + 1)) and stores them once, every
-// entry of its slot; otherwise it adds each tile's sums to the zero-filled slot with atomics. (At
-// 7x7 the 12.8 KiB they need would hold the kernel to four workgroups per CU; it runs five.)
-constexpr int SMORPH_LDS_PARTIALS = 64 * 26;
+// The static backward up to 5x5 sums each workgroup's grad_weight / grad_alpha (and, for the SMOOTH
+// merge, grad_beta) partials over its tiles in LDS (at most this many values: output channels x
+// (taps + 1 or 2)) and stores them once, every entry of its slot; otherwise it adds each tile's sums
+// to the zero-filled slot with atomics. (At 7x7 the 12.8 KiB they need would hold the kernel to four
+// workgroups per CU; it runs five. The two-row kernel at 5x5 keeps seven per CU with 64 x 26 values,
+// not with 64 x 27.)
+__host__ __device__ constexpr int smorph_lds_partials(bool smooth) { return smooth ? 64 * 27 : 64 * 26; }
 
-__host__ __device__ inline bool smorph_bwd_lds_partials(const Geom& g, bool identity)
+__host__ __device__ inline bool smorph_bwd_lds_partials(const Geom& g, bool identity, bool smooth = false)
 {
     const int K = g.KH * g.KW;
-    return K <= 25 && (identity ? 1 : g.Cout) * (K + 1) <= SMORPH_LDS_PARTIALS;
+    return K <= 25 && (identity ? 1 : g.Cout) * (K + (smooth ? 2 : 1)) <= smorph_lds_partials(smooth);
 }
 
 // Pair statistics the float32 static forward can save for the backward: ref (the window's extremum),

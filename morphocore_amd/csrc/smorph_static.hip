@@ -441,10 +441,18 @@ struct PairStats
 // (the LDS tile), to the grad_weight bin of tap k and to grad_alpha (returned: the sum of
 // p_k (v_k - ref)(v_k - out) over the taps). gv is g * scale (0 outside the image); for MAX / MIN it
 // is divided by the pixel's winner count, and a pair not within 1e-6 of the merge target outv routes
-// with g' = 0.
+// with g' = 0. For SMOOTH, outv is the merged output, sm the soft merge's beta, ref and 1 / sum at the
+// pixel: g' = g q (1 + beta (c - outv)) with q = exp(beta (c - ref)) / sum the pair's share, and
+// grad_beta's term q (c - ref)(c - outv) g goes to bterm (smorph_cpu_kernels.hxx:231-266).
+struct SmoothPixel
+{
+    float beta, ref, inv;
+};
+
 template <int MK, int KH, int KW, bool MASKED>
 __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* wl, float a, float gv, float cnt, float outv, bool in,
-                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane)
+                                                 const TapMask<KH, KW>& tm, Acc* gxb, Acc* bl, int lane, const SmoothPixel& sm,
+                                                 float& bterm)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1;
@@ -494,6 +502,14 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
         // g' = 0, so its c are 0, or NaN where its own values are not finite.
         gv = gv / (cnt > 0.0f ? cnt : 1.0f);
         gv = is_winner(st.outp, outv) ? gv : 0.0f;
+    }
+    if constexpr (MK == MK_SMOOTH)
+    {
+        // Every in-image pixel adds its term, also with a zero gradient (a NaN pair reaches grad_beta).
+        const float c = st.outp;
+        const float q = exp_ref((c - sm.ref) * sm.beta, lo) * sm.inv;
+        bterm = in ? q * (c - sm.ref) * (c - outv) * gv : 0.0f;
+        gv = gv * fmaf(sm.beta * q, c - outv, q);
     }
     // A lane outside the image (where S may be 0 and out NaN) gets g' = 0 and a finite centre, and
     // its c are cleared.
@@ -570,10 +586,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int TH = NWAVES, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
     constexpr int NC = smorph_bin_copies(K);
+    // Bins after the K taps: grad_alpha, then grad_beta for SMOOTH.
+    constexpr int NB = MK == MK_SMOOTH ? 2 : 1;
     __shared__ float tile[ROWS * COLS];
     __shared__ Acc gtile[ROWS * COLS];
-    __shared__ __align__(32) Acc bins[(K + 1) * NC];  // grad_weight bins of the K taps, then grad_alpha; NC copies each
-    // Structuring element and alpha of the current / next pair, rows padded to 16 bytes (128-bit reads).
+    __shared__ __align__(32) Acc bins[(K + NB) * NC];  // grad_weight bins of the K taps, then the NB others; NC copies each
+    // Structuring element, alpha and (SMOOTH) beta of the current / next pair, rows padded to 16 bytes
+    // (128-bit reads; K is odd, so K + 2 entries fit).
     __shared__ __align__(16) float wl[2][(K + 4) & ~3];
     const Geom g = p.g;
     const Tiling t = p.t;
@@ -601,15 +620,19 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
             wl[buf][threadIdx.x] = p.w[((int64_t)o * g.Cw + wi) * K + threadIdx.x];
         else if (threadIdx.x == K)
             wl[buf][K] = p.alpha[pair_index(o)];
+        else if (MK == MK_SMOOTH && threadIdx.x == K + 1)
+            wl[buf][K + 1] = p.beta[o];
     };
 
-    // This workgroup's grad_weight / grad_alpha partials summed over its tiles (pair o - o_begin, tap
-    // k or K for alpha), stored once at the end, when they fit.
-    constexpr int NPART = K <= 25 ? SMORPH_LDS_PARTIALS : 1;
+    // This workgroup's grad_weight / grad_alpha / grad_beta partials summed over its tiles (pair
+    // o - o_begin, tap k, K for alpha, K + 1 for beta), stored once at the end, when they fit.
+    constexpr int NPART = K <= 25 ? smorph_lds_partials(MK == MK_SMOOTH) : 1;
     __shared__ float partials[NPART];
-    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
+    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT, MK == MK_SMOOTH);
     for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
-    for (int j = threadIdx.x; j < (K + 1) * NC; j += BLOCK) bins[j] = Acc(0);
+    for (int j = threadIdx.x; j < (K + NB) * NC; j += BLOCK) bins[j] = Acc(0);
+    // grad_beta partials: row (slot, i) of Cout values.
+    float* __restrict__ part_b = MK == MK_SMOOTH ? p.part_b + ((int64_t)slot * g.Cin + i) * g.Cout : nullptr;
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
     const float* xb = tile + (wave + KH - 1) * COLS + lane + KW - 1;
@@ -634,10 +657,11 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
             gtile[idx] = Acc(0);
         }
         stage_weights(o_begin, 0);
-        // The output gradient (and, for MAX / MIN, the merged output and winner count) of this lane's
-        // pixel, one output channel ahead.
+        // The output gradient (and, for MAX / MIN, the merged output and winner count; for SMOOTH, the
+        // merged output and the soft merge's ref and 1 / sum) of this lane's pixel, one output channel
+        // ahead.
         const int64_t pix = (int64_t)min(h, g.H - 1) * g.W + min(wc, g.W - 1);
-        float gv_n = 0.0f, cnt_n = 0.0f, out_n = 0.0f;
+        float gv_n = 0.0f, cnt_n = 0.0f, out_n = 0.0f, sref_n = 0.0f, sinv_n = 0.0f;
         auto load_g = [&](int o) {
             o = min(o, o_end - 1);
             const int64_t oi = ((int64_t)b * g.Cout + o) * plane + pix;
@@ -647,6 +671,12 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
                 cnt_n = p.counts[oi];
                 out_n = p.out[oi];
             }
+            if constexpr (MK == MK_SMOOTH)
+            {
+                out_n = p.out[oi];
+                sref_n = p.sstats[oi];
+                sinv_n = p.sstats[(int64_t)g.B * g.Cout * plane + oi];
+            }
         };
         load_g(o_begin);
         __syncthreads();
@@ -654,22 +684,25 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         {
             const int buf = (o - o_begin) & 1;
             const float gv = in ? gv_n * p.scale : 0.0f, cnt = cnt_n, outv = out_n;
+            SmoothPixel sm{0.0f, sref_n, sinv_n};
             load_g(o + 1);
             const float* w = wl[buf];
             const float a = w[K];
-            float asum;
+            if constexpr (MK == MK_SMOOTH) sm.beta = w[K + 1];
+            float asum, bterm = 0.0f;
             if (interior)
-                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, false>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane, sm, bterm);
             else
-                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane);
+                asum = smorph_bwd_pair<MK, KH, KW, true>(xb, w, a, gv, cnt, outv, in, tm, gxb, bl, lane, sm, bterm);
             lds_add(&bl[K * NC], (Acc)asum);
+            if constexpr (MK == MK_SMOOTH) lds_add(&bl[(K + 1) * NC], (Acc)bterm);
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
             // Sum the NC copies of each bin: 8 threads per bin each add NC / 8 adjacent copies (16-byte
             // LDS reads) and clear them, a butterfly over the 8 finishes; the sums go to this
-            // workgroup's slot. (K + 1) * 8 is a multiple of 8, so every group of 8 lanes is whole.
+            // workgroup's slot. (K + NB) * 8 is a multiple of 8, so every group of 8 lanes is whole.
             constexpr int PER = NC / 8;  // copies per thread
-            for (int j = threadIdx.x; j < (K + 1) * 8; j += BLOCK)
+            for (int j = threadIdx.x; j < (K + NB) * 8; j += BLOCK)
             {
                 Acc v;
                 if constexpr (PER == 4)
@@ -692,11 +725,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
                 {
                     const int k = j >> 3;
                     if (lds_partials)
-                        partials[(o - o_begin) * (K + 1) + k] += (float)v;  // one owner per entry
+                        partials[(o - o_begin) * (K + NB) + k] += (float)v;  // one owner per entry
                     else if (k < K)
                         global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
-                    else
+                    else if (k == K)
                         global_add(&part_a[pair_index(o)], (float)v);
+                    else
+                        global_add(&part_b[o], (float)v);
                 }
             }
             __syncthreads();
@@ -717,14 +752,16 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         // Every entry of this workgroup's share of the slot (zeros for a strip without tiles): the
         // host skips the slot's zero fill.
         __syncthreads();
-        const int n = (o_end - o_begin) * (K + 1);
+        const int n = (o_end - o_begin) * (K + NB);
         for (int j = threadIdx.x; j < n; j += BLOCK)
         {
-            const int ol = j / (K + 1), k = j - ol * (K + 1), o = o_begin + ol;
+            const int ol = j / (K + NB), k = j - ol * (K + NB), o = o_begin + ol;
             if (k < K)
                 part_w[((int64_t)o * g.Cw + wi) * K + k] = partials[j];
-            else
+            else if (k == K)
                 part_a[pair_index(o)] = partials[j];
+            else
+                part_b[o] = partials[j];
         }
     }
 }
@@ -934,7 +971,7 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
         else if (threadIdx.x == K)
             wl[buf][K] = p.alpha[pair_index(o)];
     };
-    constexpr int NPART = K <= 25 ? SMORPH_LDS_PARTIALS : 1;
+    constexpr int NPART = K <= 25 ? smorph_lds_partials(false) : 1;
     __shared__ float partials[NPART];
     const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
     for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
@@ -1196,6 +1233,7 @@ static hipError_t bwd_size(int mk, const SmorphBwdParams<float>& p, hipStream_t 
         case MK_SUM: smorph_bwd_static<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MAX: smorph_bwd_static<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MIN: smorph_bwd_static<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SMOOTH: smorph_bwd_static<MK_SMOOTH, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         default: smorph_bwd_static<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
@@ -1217,6 +1255,8 @@ static hipError_t bwd2_size(int mk, const SmorphBwdParams<float>& p, hipStream_t
 
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
+    // The SMOOTH merge recomputes (no saved-statistics kernel).
+    if (mk == MK_SMOOTH && p.pstats) return hipErrorInvalidValue;
     // From saved statistics: the two-row kernel (64 x 8 tiles); recomputing: the one-row kernel.
     if (p.t.rh != (p.pstats ? 2 : 1)) return hipErrorInvalidValue;
     switch (p.g.KH)

@@ -85,6 +85,20 @@ def test_scm_shared_alpha_large_element_and_one_channel(dtype):
     _check(x1, w1, torch.full((2, 1), -2.0, dtype=dtype), torch.tensor([4.0, -4.0], dtype=dtype), g1)
 
 
+@pytest.mark.parametrize("K,Cout", [(3, 160), (5, 64), (5, 65), (7, 3), (11, 2)])
+def test_scm_float32_static_partials(K, Cout):
+    """The float32 static backward's grad_weight / grad_alpha / grad_beta partials: summed in LDS (5x5
+    with 64 output channels, 64 x 27 values, the most that fit) or added with atomics (3x3 with 160
+    output channels, 5x5 with 65, 7x7 and 11x11), over border and interior tiles."""
+    B, Cin, H, W = 1, 2, 21, 140
+    x = seeded(71 + K, B, Cin, H, W, kind="randn")
+    w = seeded(72 + K, Cout, Cin, K, K, kind="randn", scale=0.1)
+    alpha = seeded(73 + K, Cout, Cin, kind="randn", scale=2.0)
+    beta = seeded(74 + K, Cout, kind="randn", scale=2.0)
+    g = seeded(75 + K, B, Cout, H, W, kind="randn")
+    _check(x, w, alpha, beta, g)
+
+
 def test_scm_nan_input_propagates_like_the_reference():
     """An in-image NaN reaches its pairs' outputs, the merged output and the gradients as in the
     oracle (positions of NaN identical, finite values within the tolerance)."""
