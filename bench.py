@@ -255,8 +255,8 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "scm":
-        # The SMOOTH merge's backward (generic kernel), the larger part of its step: 18 flop per tap
-        # (SURVEY's smorph convention) plus the soft merge's per-pixel work, not counted.
+        # The SMOOTH merge's backward (float32 static recomputing kernel at 7x7), the larger part of its step: 18 flop per tap
+        # (the smorph tap convention) plus the soft merge's per-pixel work, not counted.
         a_p = torch.full((Cout * Cin,), 1.0, dtype=dtype, device=dev)
         beta = torch.full((Cout,), 1.0, dtype=dtype, device=dev)
         wt = ws[0]

@@ -4,7 +4,10 @@
 // output gradient to its packed (channel, tap): grad_input by global double atomics (one per output
 // pixel; a pixel can collect up to Cout * KH * KW of them, which float32 sums would round past the
 // 1e-6 tolerance), rounded once to float32 afterwards, grad_weight into LDS bins that become this
-// workgroup's partial slot.
+// workgroup's partial slot. Small problems (whose time is launches) gather grad_input instead, in
+// further workgroups of the same launch: each input pixel sums, in double and in (output channel,
+// tap) order, the gradients of the output pixels whose winner it is, written once (no zero fill, no
+// atomics, no rounding pass), and keep at most 32 slots (one reduction launch).
 // Reference semantics: morpho_op_cpu_backward.hxx:39-88 (run_single_winner).
 //
 // ADD / AVERAGE / IDENTITY: every channel pair routes g * scale to its own first extremal tap
@@ -43,13 +46,49 @@ struct PackedParams
 {
     const int32_t* __restrict__ idx;
     const ST* __restrict__ gout;
-    Acc* __restrict__ gin;  // double accumulator of grad_input (the output itself for float64)
+    Acc* __restrict__ gin;  // double accumulator of grad_input (the output itself for float64); null: gathered
+    ST* __restrict__ gin_gather;  // grad_input written by the gathering workgroups
     T* __restrict__ part;
     Geom g;
     int nchunks;
     int lds_bins;
     int64_t chunk;
+    int wblocks;  // workgroups of the scatter; the ones after it gather grad_input (gin null)
 };
+
+// grad_input of input pixel n = ((b * Cin + c) * H + iy) * W + ix: the sum of the output gradients of
+// the pixels (o, h, w) whose packed winner is (c, tap k) with (h + pad_h - kh, w + pad_w - kw) =
+// (iy, ix), in double, over o and then k in order (morpho_op_cpu_backward.hxx:39-88 adds the same
+// terms per output pixel).
+template <typename T, typename ST>
+__device__ __forceinline__ void packed_gather_pixel(const PackedParams<T, ST>& p, int64_t n)
+{
+    const Geom& g = p.g;
+    const int64_t plane = g.plane();
+    const int64_t bc = n / plane;
+    const int64_t pix = n - bc * plane;
+    const int b = (int)(bc / g.Cin), c = (int)(bc - (int64_t)b * g.Cin);
+    const int iy = (int)(pix / g.W), ix = (int)(pix - (int64_t)iy * g.W);
+    const int ph = g.pad_h(), pw = g.pad_w();
+    Acc s = Acc(0);
+    for (int o = 0; o < g.Cout; ++o)
+    {
+        const int64_t base = ((int64_t)b * g.Cout + o) * plane;
+        for (int kh = 0; kh < g.KH; ++kh)
+        {
+            const int h = iy - ph + kh;
+            if (h < 0 || h >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw)
+            {
+                const int wc = ix - pw + kw;
+                if (wc < 0 || wc >= g.W) continue;
+                const int64_t q = base + (int64_t)h * g.W + wc;
+                if (p.idx[q] == ((c << 16) | (kh * g.KW + kw))) s += (Acc)(T)p.gout[q];
+            }
+        }
+    }
+    p.gin_gather[n] = (ST)s;
+}
 
 template <typename T, int OP, typename ST = T>
 __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedParams<T, ST> p)
@@ -58,6 +97,12 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
     Acc* bins = reinterpret_cast<Acc*>(smem_raw);
     const Geom g = p.g;
     const int work = xcd_work_index(blockIdx.x, gridDim.x);
+    if (work >= p.wblocks)
+    {
+        const int64_t n = (int64_t)(work - p.wblocks) * BLOCK + threadIdx.x;
+        if (n < (int64_t)g.B * g.Cin * g.plane()) packed_gather_pixel(p, n);
+        return;
+    }
     const int chunk = work % p.nchunks;
     const int o = work / p.nchunks;
     const int K = g.KH * g.KW, ph = g.pad_h(), pw = g.pad_w();
@@ -85,7 +130,7 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
         const int c = packed >> 16, k = packed & 0xFFFF;
         const int kh = k / g.KW, kw = k - kh * g.KW;
         const int iy = h + ph - kh, ix = wc + pw - kw;
-        if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], (Acc)gv);
+        if (p.gin && iy >= 0 && iy < g.H && ix >= 0 && ix < g.W) global_add(&p.gin[(b * g.Cin + c) * plane + (int64_t)iy * g.W + ix], (Acc)gv);
         if (p.lds_bins)
             lds_add(&bins[(int64_t)c * K + k], (Acc)(sign * gv));
         else
@@ -594,9 +639,15 @@ struct PackedPlan
     int nchunks;
     int64_t chunk;
     bool lds_bins;
+    bool gather;  // grad_input gathered (small problems)
+    int gblocks;  // gathering workgroups
     size_t part_bytes;
     size_t lds;
 };
+
+// Gathered grad_input reads Cout * KH * KW winners per input pixel: taken while that is at most this
+// many reads in all (a few microseconds), where launches, not the scatter's work, set the time.
+constexpr int64_t PACKED_GATHER_READS = int64_t(1) << 25;
 
 template <typename T>
 static PackedPlan plan_packed(const Geom& g)
@@ -604,9 +655,13 @@ static PackedPlan plan_packed(const Geom& g)
     PackedPlan s{};
     const int64_t total = (int64_t)g.B * g.plane();
     const int64_t wnumel = (int64_t)g.Cout * g.Cin * g.taps();
+    const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
+    s.gather = gin_n > 0 && gin_n * g.Cout * g.taps() <= PACKED_GATHER_READS;
+    s.gblocks = s.gather ? (int)((gin_n + BLOCK - 1) / BLOCK) : 0;
     int64_t nchunks = (4096 + g.Cout - 1) / g.Cout;
     const int64_t max_chunks = (total + BLOCK - 1) / BLOCK;
     if (nchunks > max_chunks) nchunks = max_chunks;
+    if (s.gather && nchunks > REDUCE_GROUP) nchunks = REDUCE_GROUP;  // one reduction launch
     while (nchunks > 1 && (size_t)nchunks * wnumel * sizeof(T) > ((size_t)256 << 20)) nchunks /= 2;
     if (nchunks < 1) nchunks = 1;
     s.nchunks = (int)nchunks;
@@ -768,7 +823,8 @@ size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
         c.B = recompute_batch<T>(merge, g);
         bytes += align_up(indices_bytes(merge, c)) + align_up((size_t)c.B * c.Cout * c.plane() * sizeof(T));
     }
-    if (packed_winners(merge) && sizeof(T) != sizeof(Acc)) bytes += align_up((size_t)g.B * g.Cin * g.plane() * sizeof(Acc));
+    if (packed_winners(merge) && sizeof(T) != sizeof(Acc) && !plan_packed<T>(g).gather)
+        bytes += align_up((size_t)g.B * g.Cin * g.plane() * sizeof(Acc));
     return bytes;
 }
 
@@ -779,11 +835,12 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     hipError_t err;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     const bool packed = packed_winners(merge);
-    // The gather kernel writes every grad_input pixel itself; the others accumulate onto zeros.
-    const bool gather = !packed && (int64_t)g.B * g.Cout * g.plane() > 0 && plan_taps<T>(merge, g).gather;
+    const bool nonempty = (int64_t)g.B * g.Cout * g.plane() > 0;
+    // The gather kernels write every grad_input pixel themselves; the others accumulate onto zeros.
+    const bool gather = nonempty && (packed ? plan_packed<T>(g).gather : plan_taps<T>(merge, g).gather);
     const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
     // float32 max / min round their double grad_input accumulator into every pixel at the end.
-    const bool rounded = packed && sizeof(T) != sizeof(Acc) && (int64_t)g.B * g.Cout * g.plane() > 0;
+    const bool rounded = packed && sizeof(T) != sizeof(Acc) && nonempty;
     if (!gather && !rounded)
         if ((err = fill_async<T>(grad_in, gin_n, T(0), stream)) != hipSuccess) return err;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return fill_async<T>(grad_w, wnumel, T(0), stream);
@@ -810,26 +867,33 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         const PackedPlan s = plan_packed<T>(g);
         if (!s.lds_bins)
             if ((err = fill_async<T>(part, (int64_t)s.nchunks * wnumel, T(0), stream)) != hipSuccess) return err;
-        // float32: grad_input summed in a double buffer of the workspace, rounded once at the end.
-        Acc* gin_acc = reinterpret_cast<Acc*>(grad_in);
+        // float32: grad_input summed in a double buffer of the workspace, rounded once at the end
+        // (gathered: written directly).
+        Acc* gin_acc = s.gather ? nullptr : reinterpret_cast<Acc*>(grad_in);
         if constexpr (sizeof(T) != sizeof(Acc))
         {
-            gin_acc = reinterpret_cast<Acc*>(ws);
-            if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
+            if (!s.gather)
+            {
+                gin_acc = reinterpret_cast<Acc*>(ws);
+                if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
+            }
         }
         PackedParams<T> p{};
         p.idx = static_cast<const int32_t*>(indices);
         p.gout = grad_out;
         p.gin = gin_acc;
+        p.gin_gather = grad_in;
         p.part = part;
         p.g = g;
         p.nchunks = s.nchunks;
         p.lds_bins = s.lds_bins ? 1 : 0;
         p.chunk = s.chunk;
-        morpho_bwd_packed_kernel<T, OP><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
+        p.wblocks = s.nchunks * g.Cout;
+        morpho_bwd_packed_kernel<T, OP><<<(unsigned)((int64_t)p.wblocks + s.gblocks), BLOCK, s.lds, stream>>>(p);
         if ((err = hipGetLastError()) != hipSuccess) return err;
         if constexpr (sizeof(T) != sizeof(Acc))
-            if ((err = round_async<T>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
+            if (!s.gather)
+                if ((err = round_async<T>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
         return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
     }
 
@@ -971,20 +1035,24 @@ static hipError_t half_direct(int merge, const void* indices, const ST* grad_out
         const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
         if (!s.lds_bins)
             if ((err = fill_async<float>(part, (int64_t)s.nchunks * wnumel, 0.0f, stream)) != hipSuccess) return err;
-        Acc* gin_acc = reinterpret_cast<Acc*>(ws);
-        if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
+        Acc* gin_acc = s.gather ? nullptr : reinterpret_cast<Acc*>(ws);
+        if (!s.gather)
+            if ((err = fill_async<Acc>(gin_acc, gin_n, Acc(0), stream)) != hipSuccess) return err;
         PackedParams<float, ST> p{};
         p.idx = static_cast<const int32_t*>(indices);
         p.gout = grad_out;
         p.gin = gin_acc;
+        p.gin_gather = grad_in;
         p.part = part;
         p.g = g;
         p.nchunks = s.nchunks;
         p.lds_bins = s.lds_bins ? 1 : 0;
         p.chunk = s.chunk;
-        morpho_bwd_packed_kernel<float, OP, ST><<<(unsigned)((int64_t)s.nchunks * g.Cout), BLOCK, s.lds, stream>>>(p);
+        p.wblocks = s.nchunks * g.Cout;
+        morpho_bwd_packed_kernel<float, OP, ST><<<(unsigned)((int64_t)p.wblocks + s.gblocks), BLOCK, s.lds, stream>>>(p);
         if ((err = hipGetLastError()) != hipSuccess) return err;
-        if ((err = round_async<ST>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
+        if (!s.gather)
+            if ((err = round_async<ST>(gin_acc, grad_in, gin_n, stream)) != hipSuccess) return err;
     }
     else
     {

@@ -563,7 +563,7 @@ def test_smorph_functional_matches_blend():
 
 
 # ------------------------------------------------------------------------------------------------
-# The BASELINE configurations, at sizes the oracle finishes in seconds
+# The benchmark configurations (configs[0..4]), at sizes the oracle finishes in seconds
 # ------------------------------------------------------------------------------------------------
 
 def test_config1_dilation_max_full_size():
@@ -669,7 +669,7 @@ def test_config5_stack_reduced():
 
 
 # ------------------------------------------------------------------------------------------------
-# Full BASELINE sizes: size-independent properties
+# Full benchmark sizes: size-independent properties
 # ------------------------------------------------------------------------------------------------
 
 def test_config2_full_size_properties():
