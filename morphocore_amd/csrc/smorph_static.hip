@@ -823,15 +823,17 @@ struct RoutePixel
     bool in;
 };
 
-template <int MK, int KH, int KW, bool MASKED, bool ZA>
+// MASKED: the tile reaches past the image, so some taps read outside it (tile rows skipped by the
+// uniform `rows` bits, tap columns masked by `pen`). GATE: some of the wave's pixels lie outside the
+// image (another pixel's ref, so their e may be infinite): their c is cleared. Border tiles of an image
+// whose sides are multiples of the tile's (64 x 8) have no such pixel and skip that select per tap.
+template <int MK, int KH, int KW, bool MASKED, bool ZA, bool GATE = MASKED>
 __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* wl, float a, const RoutePixel& A, const RoutePixel& B,
                                                   unsigned rows, const float (&pen)[KW], Acc* gw, Acc* bl, Acc* btail,
                                                   const int (&hcell)[HaloRows<KH + 1, KW>::regs], Acc* gtile)
 {
 #pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
     constexpr int K = KH * KW, COLS = TILE_W + KW - 1, NC = smorph_bin_copies(K);
-    // Lanes outside the image (another pixel's ref, so e may be infinite): c cleared.
-    constexpr bool GATE = MASKED;
     float lo = ExpConsts<float>::min_input;
     asm volatile("" : "+v"(lo));  // the exponential's clamp in a register: register-only comparisons
     float asumA = 0.0f, asumB = 0.0f;
@@ -1000,6 +1002,8 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
         const int hA = h0 + RH * wave, wc = w0 + lane;
         const bool inA = hA < g.H && wc < g.W, inB = hA + 1 < g.H && wc < g.W;
         const bool interior = y0 >= 0 && y0 + ROWS <= g.H && x0 >= 0 && x0 + COLS <= g.W;
+        // Some pixel of this wave's two rows lies outside the image (uniform over the wave).
+        const bool gate = __builtin_amdgcn_uicmp((unsigned)!(inA && inB), 0u, 33) != 0;
         unsigned rows = 0;
 #pragma unroll
         for (int j = 0; j <= KH; ++j)
@@ -1081,6 +1085,9 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             if (interior)
                 asum = za ? smorph_bwd_pair2<MK, KH, KW, false, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
                           : smorph_bwd_pair2<MK, KH, KW, false, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
+            else if (!gate)
+                asum = za ? smorph_bwd_pair2<MK, KH, KW, true, true, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
+                          : smorph_bwd_pair2<MK, KH, KW, true, false, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             else
                 asum = za ? smorph_bwd_pair2<MK, KH, KW, true, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
                           : smorph_bwd_pair2<MK, KH, KW, true, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
