@@ -1,0 +1,171 @@
+"""Seeded sweep of the operators over random geometries, against the oracle.
+
+Each case draws its batch, channel counts, plane size (ragged tiles, planes narrower or shorter than a
+tile or than the element, one channel), element size (square and rectangular, even and odd), merge,
+padding, dtype (dilation / erosion also float16 and bfloat16) and saving choice, then runs the operator through torch.ops.morphocore (the product
+path) and compares with the oracle: dilation / erosion forwards bit for bit, smorph forwards and every
+gradient within 1e-6 (float32) / 1e-12 (float64) norm-wise (a shared alpha's gradient, a sum over the
+pairs that can cancel, relative to the sum of its terms' magnitudes). The sweep exercises the launch plans
+(tilings, workspace layouts, saved-statistics slots, small-grid shapes) on shapes no hand-written
+case picks.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import TOL, normwise_error
+
+pytestmark = pytest.mark.gpu
+
+MERGES = ["max", "min", "sum", "mean", "identity"]
+PADDINGS = ["zero", "geodesic", "constant", "replicate"]
+SIZES = [(1, 1), (1, 3), (2, 2), (3, 3), (3, 5), (4, 2), (5, 5), (5, 3), (7, 7), (2, 5), (11, 11)]
+
+
+def _geometry(rng, dtypes=(torch.float32, torch.float64)):
+    KH, KW = SIZES[int(rng.integers(0, len(SIZES)))]
+    large = KH * KW > 49
+    # One case in four takes a larger plane (several strips and tile rows per plane) with few channels.
+    wide = rng.integers(0, 4) == 0
+    hmax, wmax = (120, 260) if wide else ((40, 90) if large else (90, 150))
+    cmax = 4 if wide or large else 10
+    return dict(B=int(rng.integers(1, 4)), Cin=int(rng.integers(1, cmax)), Cout=int(rng.integers(1, cmax)),
+                H=int(rng.integers(1, hmax)), W=int(rng.integers(1, wmax)), KH=KH, KW=KW,
+                dtype=dtypes[int(rng.integers(0, len(dtypes)))], seed=int(rng.integers(0, 1 << 30)))
+
+
+def _morpho_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        c = _geometry(rng, (torch.float32, torch.float64, torch.float16, torch.bfloat16))
+        c.update(op=int(rng.integers(0, 2)), merge=MERGES[int(rng.integers(0, 5))], padding=PADDINGS[int(rng.integers(0, 4))],
+                 pv=float(rng.normal()), save=bool(rng.integers(0, 2)))
+        if c["merge"] == "identity":
+            c["Cout"] = c["Cin"]
+        yield c
+
+
+def _smorph_cases(n, seed, merges):
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        c = _geometry(rng)
+        c.update(merge=merges[int(rng.integers(0, len(merges)))], shared=bool(rng.integers(0, 2)),
+                 alpha_scale=float(rng.choice([0.0, 1.0, 5.0, 20.0])), save=bool(rng.integers(0, 2)))
+        if c["merge"] == "identity":
+            c["Cout"] = c["Cin"]
+        yield c
+
+
+def _ids(c):
+    return f"{c['B']}x{c['Cin']}x{c['Cout']}x{c['H']}x{c['W']}k{c['KH']}x{c['KW']}"
+
+
+def _gen(c):
+    g = torch.Generator().manual_seed(c["seed"])
+    return lambda *s, scale=1.0: (torch.randn(*s, generator=g, dtype=torch.float64) * scale).to(c["dtype"])  # noqa: E731
+
+
+HALF = (torch.float16, torch.bfloat16)
+# 16-bit gradients are rounded once from float32 sums the oracle forms in another order: within about
+# one unit in their last place (as tests/test_gpu_half.py).
+GTOL = {torch.float32: TOL[torch.float32], torch.float64: TOL[torch.float64], torch.float16: 1e-3, torch.bfloat16: 8e-3}
+
+
+def _check(got, want, dtype, what):
+    err = normwise_error(got.detach().cpu().numpy(), want)
+    assert err <= TOL[dtype], f"{what}: {err}"
+
+
+@pytest.mark.parametrize("c", list(_morpho_cases(200, 7101)), ids=_ids)
+def test_morpho_sweep(c):
+    import morphocore_amd  # noqa: F401  (registers torch.ops.morphocore)
+
+    dev = torch.device("cuda")
+    mk = _gen(c)
+    cw = 1 if c["merge"] == "identity" else c["Cin"]
+    x = mk(c["B"], c["Cin"], c["H"], c["W"])
+    w = mk(c["Cout"], cw, c["KH"], c["KW"], scale=0.3)
+    gout = mk(c["B"], c["Cout"], c["H"], c["W"])
+    merge, padding = O.MERGES[c["merge"]], O.PADDINGS[c["padding"]]
+    fn = torch.ops.morphocore.dilation if c["op"] == O.DILATION else torch.ops.morphocore.erosion
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    out = fn(xd, wd, merge, padding, c["pv"], c["save"], 0.0)
+    out.backward(gout.to(dev))
+    # 16-bit tensors: the float32 oracle on the same (exactly converted) values and the float32 padding
+    # value, each result rounded once.
+    half = c["dtype"] in HALF
+    xs, ws, gs = ((t.float() if half else t).numpy() for t in (x, w, gout))
+    pv = c["pv"]
+    ref, _ = O.morpho_forward(c["op"], merge, padding, pv, xs, ws)
+    rounded = (lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(c["dtype"]).float().numpy()) if half else (lambda a: a)  # noqa: E731
+    assert np.array_equal(out.detach().float().cpu().numpy() if half else out.detach().cpu().numpy(), rounded(ref)), "forward differs"
+    gx, gw = O.morpho_backward(c["op"], merge, padding, pv, xs, ws, gs)
+    for name, got, want in (("grad_input", xd.grad, gx), ("grad_weight", wd.grad, gw)):
+        err = normwise_error(got.detach().float().cpu().numpy() if half else got.detach().cpu().numpy(), rounded(want))
+        assert err <= GTOL[c["dtype"]], f"{name}: {err}"
+
+
+def _smorph_run(c, monkeypatch, scm):
+    import morphocore_amd  # noqa: F401
+
+    monkeypatch.setenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT", "-1" if c["save"] else "0")
+    dev = torch.device("cuda")
+    mk = _gen(c)
+    cw = 1 if c["merge"] == "identity" else c["Cin"]
+    x = mk(c["B"], c["Cin"], c["H"], c["W"])
+    w = mk(c["Cout"], cw, c["KH"], c["KW"], scale=0.3)
+    pairs = c["Cout"] if c["merge"] == "identity" else c["Cout"] * c["Cin"]
+    alpha = (mk(1) if c["shared"] else mk(pairs)) * c["alpha_scale"]
+    alpha = alpha.reshape(()) if c["shared"] else alpha.reshape((c["Cout"],) if c["merge"] == "identity" else (c["Cout"], c["Cin"]))
+    gout = mk(c["B"], c["Cout"], c["H"], c["W"])
+    xd, wd, ad = (t.to(dev).requires_grad_(True) for t in (x, w, alpha))
+    beta = None
+    if scm:
+        beta = mk(c["Cout"], scale=3.0)
+        bd = beta.to(dev).requires_grad_(True)
+        out = torch.ops.morphocore.smorph_scm(xd, wd, ad, bd)
+        out.backward(gout.to(dev))
+        ref = O.smorph_scm_forward(x.numpy(), w.numpy(), alpha.numpy(), beta.numpy())
+        want = O.smorph_scm_backward(x.numpy(), w.numpy(), alpha.numpy(), beta.numpy(), gout.numpy())
+        got = (xd.grad, wd.grad, ad.grad, bd.grad)
+    else:
+        merge = O.MERGES[c["merge"]]
+        out = torch.ops.morphocore.smorph(xd, wd, ad, merge)
+        out.backward(gout.to(dev))
+        ref = O.smorph_forward(merge, x.numpy(), w.numpy(), alpha.numpy())
+        want = O.smorph_backward(merge, x.numpy(), w.numpy(), alpha.numpy(), gout.numpy())
+        got = (xd.grad, wd.grad, ad.grad)
+    _check(out, ref, c["dtype"], "forward")
+    for name, a, b in zip(("grad_input", "grad_weight", "grad_alpha", "grad_beta"), got, want):
+        if name == "grad_alpha" and c["shared"]:
+            # A shared alpha receives the sum of every pair's gradient (smorph.cpp:96-98), which can
+            # cancel far below its terms (float32's own sum then moves by more than 1e-6 of the
+            # result: the oracle's differs from its float64 counterpart by up to ~5e-5 on these
+            # inputs); its error is measured against the sum of the terms' magnitudes instead.
+            per_pair = _per_pair_alpha_grads(c, x, w, alpha, gout, beta if scm else None)
+            err = abs(float(a) - float(b)) / max(float(np.abs(per_pair).sum(dtype=np.float64)), 1e-30)
+            assert err <= TOL[c["dtype"]], f"{name} (shared): {err}"
+            continue
+        _check(a, b, c["dtype"], name)
+
+
+def _per_pair_alpha_grads(c, x, w, alpha, gout, beta):
+    """The oracle's gradient of every pair's own alpha, all equal to the shared value."""
+    merge = O.SMOOTH if beta is not None else O.MERGES[c["merge"]]
+    pairs = (c["Cout"],) if c["merge"] == "identity" and beta is None else (c["Cout"], c["Cin"])
+    ap = np.full(pairs, float(alpha), dtype=x.numpy().dtype)
+    if beta is not None:
+        return O.smorph_scm_backward(x.numpy(), w.numpy(), ap, beta.numpy(), gout.numpy())[2]
+    return O.smorph_backward(merge, x.numpy(), w.numpy(), ap, gout.numpy())[2]
+
+
+@pytest.mark.parametrize("c", list(_smorph_cases(120, 7202, MERGES)), ids=_ids)
+def test_smorph_sweep(c, monkeypatch):
+    _smorph_run(c, monkeypatch, scm=False)
+
+
+@pytest.mark.parametrize("c", list(_smorph_cases(40, 7303, ["sum"])), ids=_ids)
+def test_smorph_scm_sweep(c, monkeypatch):
+    _smorph_run(c, monkeypatch, scm=True)
