@@ -296,10 +296,12 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
                             e = exp_ref((v - ref[r]) * a, lo);
                         const T pg = e * scaled[r];
                         const T centered = v - outp[r];
-                        const T c = fma(a * pg, centered, pg);
+                        // c = pg (1 + a centered) and the alpha term pg (v - ref) centered share pg centered.
+                        const T q = pg * centered;
+                        const T c = fma(a, q, pg);
                         lds_add(&gtile[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)c);
                         lds_add(&bins[k * p.ncopy + copy], (Acc)c);
-                        asum[r] = asum[r] + pg * (v - ref[r]) * centered;
+                        asum[r] = fma(q, v - ref[r], asum[r]);
                     }
                 }
             T as = T(0);

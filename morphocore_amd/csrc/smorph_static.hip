@@ -550,7 +550,9 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
             }
             const float pg = ekr * scaled;
             const float centered = vk - outc;
-            float c = fmaf(a * pg, centered, pg);
+            // c = pg (1 + a centered) and the alpha term pg (v - ref) centered share pg centered.
+            const float q = pg * centered;
+            float c = fmaf(a, q, pg);
             if constexpr (GATE) c = in ? c : 0.0f;
             if (kw == 0)
             {
@@ -563,7 +565,7 @@ __device__ __forceinline__ float smorph_bwd_pair(const float* xb, const float* w
                 racc = wave_shift_up(racc) + c;
             }
             lds_add(&bl[k * smorph_bin_copies(K)], (Acc)c);
-            asum = fmaf(pg * (vk - ref), centered, asum);
+            asum = fmaf(q, vk - ref, asum);
             // Keeps the compiler from deferring the alpha terms to the end of the pair, which would
             // hold every tap's factors in registers.
             asm volatile("" : "+v"(asum));
@@ -859,9 +861,11 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
             ek = __builtin_amdgcn_exp2f(MASKED ? (vk - P.ref) * a2 - pen[kw] : (vk - P.ref) * a2);  // exp_route, log2(e) folded
         const float pg = ek * P.scaled;
         const float centered = vk - P.outc;
-        float c = fmaf(a * pg, centered, pg);
+        // c = pg (1 + a centered) and the alpha term pg (v - ref) centered share pg centered.
+        const float q = pg * centered;
+        float c = fmaf(a, q, pg);
         if constexpr (GATE) c = P.in ? c : 0.0f;
-        asum = fmaf(pg * (vk - P.ref), centered, asum);
+        asum = fmaf(q, vk - P.ref, asum);
         // Keeps the compiler from deferring the alpha terms, which would hold every tap's factors
         // in registers.
         asm volatile("" : "+v"(asum));
