@@ -234,6 +234,42 @@ public:
 
     bool admit(int64_t nbytes, c10::DeviceIndex device)
     {
+        std::lock_guard<std::mutex> lock(m_);
+        return admit_locked(nbytes, device);
+    }
+
+    // A float32 buffer of nbytes for the statistics when the policy admits it, tracked from then on;
+    // an undefined tensor otherwise (also when the allocation fails: the backward then recomputes).
+    // The check, the allocation and the tracking are one critical section, so that forwards running
+    // in several threads cannot together exceed the budget.
+    Tensor allocate(int64_t nbytes, const c10::TensorOptions& options)
+    {
+        const c10::DeviceIndex device = options.device().index();
+        std::lock_guard<std::mutex> lock(m_);
+        if (!admit_locked(nbytes, device)) return Tensor();
+        Tensor t;
+        try
+        {
+            t = torch::empty({nbytes / 4}, options.dtype(torch::kFloat32));
+        }
+        catch (const c10::OutOfMemoryError&)
+        {
+            return Tensor();  // fragmented memory
+        }
+        live_.push_back(Entry{t.storage().getWeakStorageImpl(), static_cast<int64_t>(t.nbytes()), device});
+        return t;
+    }
+
+private:
+    struct Entry
+    {
+        c10::weak_intrusive_ptr<c10::StorageImpl> storage;
+        int64_t nbytes;
+        c10::DeviceIndex device;
+    };
+
+    bool admit_locked(int64_t nbytes, c10::DeviceIndex device)
+    {
         if (nbytes <= 0) return false;
         size_t free_b = 0, total_b = 0;
         {
@@ -246,23 +282,8 @@ public:
         const int64_t avail = static_cast<int64_t>(free_b) + (cached_unused > 0 ? cached_unused : 0);
         const int64_t budget = env_bytes("MORPHOCORE_AMD_SAVED_STATS_BUDGET", static_cast<int64_t>(total_b) / 10 * 4);
         const int64_t limit = env_bytes("MORPHOCORE_AMD_SAVED_STATS_LIMIT", -1);
-        std::lock_guard<std::mutex> lock(m_);
         return stats_policy(nbytes, prune_and_sum(device), budget, avail, limit);
     }
-
-    void track(const Tensor& t)
-    {
-        std::lock_guard<std::mutex> lock(m_);
-        live_.push_back(Entry{t.storage().getWeakStorageImpl(), static_cast<int64_t>(t.nbytes()), t.device().index()});
-    }
-
-private:
-    struct Entry
-    {
-        c10::weak_intrusive_ptr<c10::StorageImpl> storage;
-        int64_t nbytes;
-        c10::DeviceIndex device;
-    };
 
     int64_t prune_and_sum(c10::DeviceIndex device)
     {
@@ -747,18 +768,7 @@ public:
         if (x.scalar_type() == c10::kFloat)
         {
             const int64_t nbytes = needs_grad ? (int64_t)mca_smorph_stats_bytes_f32((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW) : 0;
-            if (nbytes > 0 && SavedStats::get().admit(nbytes, x.device().index()))
-            {
-                try
-                {
-                    stats = torch::empty({nbytes / 4}, x.options().dtype(torch::kFloat32));
-                    SavedStats::get().track(stats);
-                }
-                catch (const c10::OutOfMemoryError&)
-                {
-                    stats = Tensor();  // fragmented memory: the backward recomputes them
-                }
-            }
+            if (nbytes > 0) stats = SavedStats::get().allocate(nbytes, x.options());
             if (stats.defined())
                 check_rc(mca_smorph_forward_stats_f32((int)merge, x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(),
                                                       out.data_ptr<float>(), stats.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH,
