@@ -37,7 +37,7 @@ def _grads(outs, params, g):
     return [p.grad.detach().clone() for p in params]
 
 
-@pytest.mark.parametrize("case", list(_cases(40, 2024)), ids=lambda c: f"{c['B']}x{c['C']}x{c['H']}x{c['W']}k{c['K']}p{c['padding']}")
+@pytest.mark.parametrize("case", list(_cases(100, 2024)), ids=lambda c: f"{c['B']}x{c['C']}x{c['H']}x{c['W']}k{c['K']}p{c['padding']}")
 @pytest.mark.parametrize("first", [0, 1], ids=["closing", "opening"])
 def test_opening_closing_sweep(case, first):
     import morphocore_amd  # noqa: F401
@@ -62,7 +62,7 @@ def test_opening_closing_sweep(case, first):
         assert normwise_error(u.cpu().numpy(), v.cpu().numpy()) <= TOL[case["dtype"]]
 
 
-@pytest.mark.parametrize("case", list(_cases(40, 4048)), ids=lambda c: f"{c['B']}x{c['C']}x{c['H']}x{c['W']}k{c['K']}p{c['padding']}")
+@pytest.mark.parametrize("case", list(_cases(100, 4048)), ids=lambda c: f"{c['B']}x{c['C']}x{c['H']}x{c['W']}k{c['K']}p{c['padding']}")
 def test_sigma_identity_sweep(case):
     import morphocore_amd  # noqa: F401
 
