@@ -56,12 +56,16 @@ struct PackedParams
     int wblocks;  // workgroups of the scatter; the ones after it gather grad_input (gin null)
 };
 
-// grad_input of input pixel n = ((b * Cin + c) * H + iy) * W + ix: the sum of the output gradients of
-// the pixels (o, h, w) whose packed winner is (c, tap k) with (h + pad_h - kh, w + pad_w - kw) =
-// (iy, ix), in double, over o and then k in order (morpho_op_cpu_backward.hxx:39-88 adds the same
-// terms per output pixel).
+// Output-channel slots of a gathering workgroup: GATHER_SLOTS threads share each input pixel, slot s
+// taking the output channels s, s + GATHER_SLOTS, ...; BLOCK / GATHER_SLOTS pixels per workgroup.
+constexpr int GATHER_SLOTS = 16;
+
+// Slot `slot`'s share of the grad_input of input pixel n = ((b * Cin + c) * H + iy) * W + ix: the sum
+// of the output gradients of the pixels (o, h, w), o = slot mod GATHER_SLOTS, whose packed winner is
+// (c, tap k) with (h + pad_h - kh, w + pad_w - kw) = (iy, ix), in double, over o and then k in order
+// (morpho_op_cpu_backward.hxx:39-88 adds the same terms per output pixel).
 template <typename T, typename ST>
-__device__ __forceinline__ void packed_gather_pixel(const PackedParams<T, ST>& p, int64_t n)
+__device__ __forceinline__ Acc packed_gather_pixel(const PackedParams<T, ST>& p, int64_t n, int slot)
 {
     const Geom& g = p.g;
     const int64_t plane = g.plane();
@@ -71,7 +75,7 @@ __device__ __forceinline__ void packed_gather_pixel(const PackedParams<T, ST>& p
     const int iy = (int)(pix / g.W), ix = (int)(pix - (int64_t)iy * g.W);
     const int ph = g.pad_h(), pw = g.pad_w();
     Acc s = Acc(0);
-    for (int o = 0; o < g.Cout; ++o)
+    for (int o = slot; o < g.Cout; o += GATHER_SLOTS)
     {
         const int64_t base = ((int64_t)b * g.Cout + o) * plane;
         for (int kh = 0; kh < g.KH; ++kh)
@@ -87,7 +91,7 @@ __device__ __forceinline__ void packed_gather_pixel(const PackedParams<T, ST>& p
             }
         }
     }
-    p.gin_gather[n] = (ST)s;
+    return s;
 }
 
 template <typename T, int OP, typename ST = T>
@@ -99,8 +103,20 @@ __global__ __launch_bounds__(BLOCK) void morpho_bwd_packed_kernel(const PackedPa
     const int work = xcd_work_index(blockIdx.x, gridDim.x);
     if (work >= p.wblocks)
     {
-        const int64_t n = (int64_t)(work - p.wblocks) * BLOCK + threadIdx.x;
-        if (n < (int64_t)g.B * g.Cin * g.plane()) packed_gather_pixel(p, n);
+        // Gathering workgroup: each pixel's slots, then their sum in slot order (deterministic).
+        __shared__ Acc slot_sums[BLOCK];
+        constexpr int PIX = BLOCK / GATHER_SLOTS;
+        const int lp = threadIdx.x % PIX, slot = threadIdx.x / PIX;
+        const int64_t n = (int64_t)(work - p.wblocks) * PIX + lp;
+        const bool in = n < (int64_t)g.B * g.Cin * g.plane();
+        slot_sums[threadIdx.x] = in ? packed_gather_pixel(p, n, slot) : Acc(0);
+        __syncthreads();
+        if (in && slot == 0)
+        {
+            Acc s = Acc(0);
+            for (int k = 0; k < GATHER_SLOTS; ++k) s += slot_sums[k * PIX + lp];
+            p.gin_gather[n] = (ST)s;
+        }
         return;
     }
     const int chunk = work % p.nchunks;
@@ -657,7 +673,7 @@ static PackedPlan plan_packed(const Geom& g)
     const int64_t wnumel = (int64_t)g.Cout * g.Cin * g.taps();
     const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
     s.gather = gin_n > 0 && gin_n * g.Cout * g.taps() <= PACKED_GATHER_READS;
-    s.gblocks = s.gather ? (int)((gin_n + BLOCK - 1) / BLOCK) : 0;
+    s.gblocks = s.gather ? (int)((gin_n + BLOCK / GATHER_SLOTS - 1) / (BLOCK / GATHER_SLOTS)) : 0;
     int64_t nchunks = (4096 + g.Cout - 1) / g.Cout;
     const int64_t max_chunks = (total + BLOCK - 1) / BLOCK;
     if (nchunks > max_chunks) nchunks = max_chunks;
