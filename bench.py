@@ -255,22 +255,26 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "scm":
-        # The SMOOTH merge's backward (float32 static recomputing kernel at 7x7), the larger part of its step: 18 flop per tap
-        # (the smorph tap convention) plus the soft merge's per-pixel work, not counted.
+        # The SMOOTH merge's backward, the larger part of its step, from the forward's saved pair statistics as the
+        # operator runs it (float32 static two-row kernel at 7x7): 18 flop per tap (the smorph tap convention) plus
+        # the soft merge's per-pixel work, not counted.
         a_p = torch.full((Cout * Cin,), 1.0, dtype=dtype, device=dev)
         beta = torch.full((Cout,), 1.0, dtype=dtype, device=dev)
         wt = ws[0]
         out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
         mst = torch.empty((2, B, Cout, H, W), dtype=dtype, device=dev)
-        native.smorph_scm_forward(x, wt, a_p, beta, out, mst, geom)
+        nbytes = native.smorph_scm_stats_bytes(dtype, geom)
+        pst = torch.empty((nbytes // 4,), dtype=torch.float32, device=dev) if nbytes else None
+        native.smorph_scm_forward(x, wt, a_p, beta, out, mst, geom, pair_stats=pst)
         gen = torch.Generator(device=dev).manual_seed(2)
         grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
         gx, gw, ga, gb = torch.empty_like(x), torch.empty_like(wt), torch.empty_like(a_p), torch.empty_like(beta)
 
         def launch():
-            native.smorph_scm_backward(x, wt, a_p, beta, out, mst, grad, gx, gw, ga, gb, geom)
+            native.smorph_scm_backward(x, wt, a_p, beta, out, mst, grad, gx, gw, ga, gb, geom, pair_stats=pst)
 
-        return launch, 18 * t, "flop", "smorph_scm backward, alpha 1, beta 1 (mca_smorph_scm_backward_f32: kernels + reductions)"
+        entry = "mca_smorph_scm_backward_stats_f32" if pst is not None else "mca_smorph_scm_backward_f32"
+        return launch, 18 * t, "flop", f"smorph_scm backward, alpha 1, beta 1, from the forward's saved pair statistics ({entry}: kernels + reductions)"
     if cfg["kind"] == "sigma":
         # The fused forward: x read once, the output and one tap byte per operation written once.
         pg = (B, Cin, H, W, KH, KW)

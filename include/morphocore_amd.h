@@ -217,6 +217,26 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
                                 double* grad_alpha, double* grad_beta, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
                                 int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Smorph with the SMOOTH channel merge and saved pair statistics (float32; square 3x3, 5x5, 7x7 and
+ * 11x11 elements). No reference counterpart: the reference's backward recomputes each pair's softmax
+ * statistics (smorph_kernels.cuh:512-523 with smorph_scm.cpp:36-96). The forward stores, for every
+ * channel pair at every output pixel, the window's extremum, 1 / S and W / S (three float32 arrays of
+ * B * Cout * Cin * H * W values, mca_smorph_scm_stats_bytes_f32 bytes, 0 when the configuration has no
+ * such path), the last being the pair outputs the soft merge reads (no workspace); it also writes
+ * merge_stats as mca_smorph_scm_forward_f32 does. The backward reads both instead of recomputing (the
+ * workspace of mca_smorph_scm_backward_f32). Output bit for bit that of mca_smorph_scm_forward_f32;
+ * gradients within the float32 tolerance of mca_smorph_scm_backward_f32's (the same terms added in
+ * another order). */
+size_t mca_smorph_scm_stats_bytes_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW);
+int mca_smorph_scm_forward_stats_f32(const float* input, const float* weight, const float* alpha, const float* beta, float* output,
+                                     float* merge_stats, float* pair_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                     int64_t W, int64_t KH, int64_t KW, void* stream);
+int mca_smorph_scm_backward_stats_f32(const float* input, const float* weight, const float* alpha, const float* beta, const float* output,
+                                      const float* merge_stats, const float* pair_stats, const float* grad_output, float* grad_input,
+                                      float* grad_weight, float* grad_alpha, float* grad_beta, int64_t B, int64_t Cin, int64_t Cout,
+                                      int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
 /* Per-sample structuring elements of weight noise in one pass: out[b][j] = weight[j] + (uniform[b][j] * 2
  * - 1) * scale for b < batch, j < n, with the roundings of the four elementwise operations the
  * reference composes it from (morphocore/functional/csrc/cpp/morpho_op_wrap.hxx:55-64: torch::rand's

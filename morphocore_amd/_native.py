@@ -49,6 +49,9 @@ EXPORTS = (
     "mca_smorph_scm_backward_workspace_size_f64",
     "mca_smorph_scm_backward_f32",
     "mca_smorph_scm_backward_f64",
+    "mca_smorph_scm_stats_bytes_f32",
+    "mca_smorph_scm_forward_stats_f32",
+    "mca_smorph_scm_backward_stats_f32",
     "mca_noise_sample_weights_f32",
     "mca_noise_sample_weights_f64",
     "mca_morpho_pair_supported",
@@ -167,6 +170,12 @@ def lib() -> ctypes.CDLL:
     so.mca_smorph_forward_stats_f32.restype = _I
     so.mca_smorph_backward_stats_f32.argtypes = [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P] + _GEOM + [_P, _SZ, _P]
     so.mca_smorph_backward_stats_f32.restype = _I
+    so.mca_smorph_scm_stats_bytes_f32.argtypes = list(_GEOM)
+    so.mca_smorph_scm_stats_bytes_f32.restype = _SZ
+    so.mca_smorph_scm_forward_stats_f32.argtypes = [_P] * 7 + _GEOM + [_P]
+    so.mca_smorph_scm_forward_stats_f32.restype = _I
+    so.mca_smorph_scm_backward_stats_f32.argtypes = [_P] * 12 + _GEOM + [_P, _SZ, _P]
+    so.mca_smorph_scm_backward_stats_f32.restype = _I
     _lib = so
     return so
 
@@ -279,19 +288,40 @@ def smorph_backward(merge, x, weight, alpha_pairs, out, grad_out, grad_in, grad_
              *geom, _ptr(ws), ws.numel(), _stream(x)))
 
 
-def smorph_scm_forward(x, weight, alpha_pairs, beta, out, merge_stats, geom):
+def smorph_scm_stats_bytes(dtype, geom) -> int:
+    """Bytes of the pair statistics the smorph_scm forward can save for its backward (C ABI
+    mca_smorph_scm_stats_bytes_f32); 0 when the configuration has no such path."""
+    if dtype != torch.float32:
+        return 0
+    return int(lib().mca_smorph_scm_stats_bytes_f32(*geom))
+
+
+def smorph_scm_forward(x, weight, alpha_pairs, beta, out, merge_stats, geom, pair_stats=None):
     """Enqueue smorph with the SMOOTH merge (C ABI mca_smorph_scm_forward_*), workspace from torch;
-    `merge_stats` (2 * B * Cout * H * W values, or None) receives the soft merge's ref and 1 / sum."""
+    `merge_stats` (2 * B * Cout * H * W values, or None) receives the soft merge's ref and 1 / sum.
+    With `pair_stats` (float32, smorph_scm_stats_bytes bytes) the pair statistics are saved too
+    (mca_smorph_scm_forward_stats_f32, no workspace)."""
     so, sfx = lib(), _sfx(x)
+    if pair_stats is not None:
+        _check(so.mca_smorph_scm_forward_stats_f32(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats),
+                                                   _ptr(pair_stats), *geom, _stream(x)))
+        return
     ws = _workspace(getattr(so, f"mca_smorph_scm_forward_workspace_size_{sfx}")(*geom), x.device)
     f = getattr(so, f"mca_smorph_scm_forward_{sfx}")
     _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), *geom, _ptr(ws), ws.numel(), _stream(x)))
 
 
-def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out, grad_in, grad_w, grad_alpha, grad_beta, geom):
-    """Enqueue the smorph_scm backward (C ABI mca_smorph_scm_backward_*), workspace from torch."""
+def smorph_scm_backward(x, weight, alpha_pairs, beta, out, merge_stats, grad_out, grad_in, grad_w, grad_alpha, grad_beta, geom,
+                        pair_stats=None):
+    """Enqueue the smorph_scm backward (C ABI mca_smorph_scm_backward_*, or
+    mca_smorph_scm_backward_stats_f32 with the forward's saved `pair_stats`), workspace from torch."""
     so, sfx = lib(), _sfx(x)
     ws = _workspace(getattr(so, f"mca_smorph_scm_backward_workspace_size_{sfx}")(*geom), x.device)
+    if pair_stats is not None:
+        _check(so.mca_smorph_scm_backward_stats_f32(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats),
+                                                    _ptr(pair_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w), _ptr(grad_alpha),
+                                                    _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))
+        return
     f = getattr(so, f"mca_smorph_scm_backward_{sfx}")
     _check(f(_ptr(x), _ptr(weight), _ptr(alpha_pairs), _ptr(beta), _ptr(out), _ptr(merge_stats), _ptr(grad_out), _ptr(grad_in), _ptr(grad_w),
              _ptr(grad_alpha), _ptr(grad_beta), *geom, _ptr(ws), ws.numel(), _stream(x)))

@@ -201,24 +201,27 @@ int check_workspace(size_t given, size_t need, const void* workspace)
     return MCA_OK;
 }
 
+// `pair_stats` (float32 only, checked by the callers): the pair statistics saved by the forward (no
+// workspace then) and read by the backward, or null.
 template <typename T>
 int scm_forward_impl(const T* input, const T* weight, const T* alpha, const T* beta, T* output, T* merge_stats, int64_t B, int64_t Cin,
                      int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes,
-                     void* stream)
+                     void* stream, float* pair_stats = nullptr)
 {
     mca::Geom g{};
     int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
     if (rc != MCA_OK) return rc;
     if ((rc = check_lds(mca::smorph_scm_lds<T>(g, false))) != MCA_OK) return rc;
-    if ((rc = check_workspace(workspace_bytes, mca::smorph_scm_forward_workspace<T>(g), workspace)) != MCA_OK) return rc;
-    return hip_status(
-        mca::smorph_scm_forward<T>(input, weight, alpha, beta, output, merge_stats, g, workspace, workspace_bytes, (hipStream_t)stream));
+    if (!pair_stats && (rc = check_workspace(workspace_bytes, mca::smorph_scm_forward_workspace<T>(g), workspace)) != MCA_OK) return rc;
+    return hip_status(mca::smorph_scm_forward<T>(input, weight, alpha, beta, output, merge_stats, g, workspace, workspace_bytes,
+                                                 (hipStream_t)stream, pair_stats));
 }
 
 template <typename T>
 int scm_backward_impl(const T* input, const T* weight, const T* alpha, const T* beta, const T* output, const T* merge_stats,
                       const T* grad_output, T* grad_input, T* grad_weight, T* grad_alpha, T* grad_beta, int64_t B, int64_t Cin, int64_t Cout,
-                      int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream)
+                      int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes, void* stream,
+                      const float* pair_stats = nullptr)
 {
     mca::Geom g{};
     int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
@@ -227,7 +230,7 @@ int scm_backward_impl(const T* input, const T* weight, const T* alpha, const T* 
     if (!merge_stats && (int64_t)g.B * g.Cout * g.plane() > 0) return fail("merge_stats must not be null");
     if ((rc = check_workspace(workspace_bytes, mca::smorph_scm_backward_workspace<T>(g), workspace)) != MCA_OK) return rc;
     return hip_status(mca::smorph_scm_backward<T>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight,
-                                                  grad_alpha, grad_beta, g, workspace, workspace_bytes, (hipStream_t)stream));
+                                                  grad_alpha, grad_beta, g, workspace, workspace_bytes, (hipStream_t)stream, pair_stats));
 }
 
 // Device address of `scratch` on `device` (which must be the current device), looked up once per
@@ -631,6 +634,42 @@ int mca_smorph_scm_backward_f64(const double* input, const double* weight, const
 {
     return scm_backward_impl<double>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight, grad_alpha,
                                      grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream);
+}
+
+size_t mca_smorph_scm_stats_bytes_f32(int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW)
+{
+    mca::Geom g{};
+    if (make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g) != MCA_OK) return 0;
+    return (size_t)mca::smorph_stats_values(mca::MERGE_SMOOTH, g) * 3 * sizeof(float);
+}
+
+int mca_smorph_scm_forward_stats_f32(const float* input, const float* weight, const float* alpha, const float* beta, float* output,
+                                     float* merge_stats, float* pair_stats, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64_t H,
+                                     int64_t W, int64_t KH, int64_t KW, void* stream)
+{
+    mca::Geom g{};
+    int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_stats(mca::MERGE_SMOOTH, g, pair_stats)) != MCA_OK) return rc;
+    // An empty output has no statistics (a null pair_stats is allowed): nothing to compute.
+    if (!pair_stats) return MCA_OK;
+    return scm_forward_impl<float>(input, weight, alpha, beta, output, merge_stats, B, Cin, Cout, Cw, H, W, KH, KW, nullptr, 0, stream,
+                                   pair_stats);
+}
+
+int mca_smorph_scm_backward_stats_f32(const float* input, const float* weight, const float* alpha, const float* beta, const float* output,
+                                      const float* merge_stats, const float* pair_stats, const float* grad_output, float* grad_input,
+                                      float* grad_weight, float* grad_alpha, float* grad_beta, int64_t B, int64_t Cin, int64_t Cout,
+                                      int64_t Cw, int64_t H, int64_t W, int64_t KH, int64_t KW, void* workspace, size_t workspace_bytes,
+                                      void* stream)
+{
+    mca::Geom g{};
+    int rc = make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g);
+    if (rc != MCA_OK) return rc;
+    if ((rc = check_stats(mca::MERGE_SMOOTH, g, pair_stats)) != MCA_OK) return rc;
+    // An empty output (null pair_stats): the recomputing path, which only clears the gradients.
+    return scm_backward_impl<float>(input, weight, alpha, beta, output, merge_stats, grad_output, grad_input, grad_weight, grad_alpha,
+                                    grad_beta, B, Cin, Cout, Cw, H, W, KH, KW, workspace, workspace_bytes, stream, pair_stats);
 }
 
 int mca_noise_sample_weights_f32(const float* weight, const float* uniform, float scale, float* out, int64_t batch, int64_t n, void* stream)

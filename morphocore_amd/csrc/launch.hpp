@@ -92,6 +92,9 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
 // Smorph with the SMOOTH channel merge (smorph_scm; generic kernels, float32 and float64).
 // Forward workspace: every pair output, [B, Cout, Cin, H, W]. `sstats` (2 * B * Cout * H * W values:
 // the soft merge's ref, then 1 / sum), written by the forward (may be null) and read by the backward.
+// `pstats`: the pair statistics (as smorph_forward's `stats`, smorph_stats_count(MERGE_SMOOTH) values
+// per array; float32 static configurations only), saved by the forward, whose pair outputs are then
+// the W / S array (no workspace), and read by the backward; null: the backward recomputes them.
 template <typename T>
 size_t smorph_scm_forward_workspace(const Geom& g);
 template <typename T>
@@ -100,11 +103,11 @@ template <typename T>
 size_t smorph_scm_lds(const Geom& g, bool backward);
 template <typename T>
 hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* beta, T* out, T* sstats, const Geom& g, void* workspace,
-                              size_t workspace_bytes, hipStream_t stream);
+                              size_t workspace_bytes, hipStream_t stream, float* pstats = nullptr);
 template <typename T>
 hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* beta, const T* out, const T* sstats, const T* grad_out,
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream);
+                               hipStream_t stream, const float* pstats = nullptr);
 
 // Opening / closing with IDENTITY merges fused into one pass (morpho_fused.hip). g: Cin == Cout == C,
 // Cw == 1; first_op: the first stage's op.

@@ -667,7 +667,7 @@ size_t smorph_scm_forward_workspace(const Geom& g)
 template <typename T>
 size_t smorph_scm_backward_workspace(const Geom& g)
 {
-    return smorph_plan_workspace<T>(plan_smorph_bwd<T>(MERGE_SMOOTH, g), g);
+    return smorph_backward_workspace<T>(MERGE_SMOOTH, g);
 }
 
 template <typename T>
@@ -686,17 +686,24 @@ static unsigned elementwise_grid(int64_t n)
 
 template <typename T>
 hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* beta, T* out, T* sstats, const Geom& g, void* workspace,
-                              size_t workspace_bytes, hipStream_t stream)
+                              size_t workspace_bytes, hipStream_t stream, float* pstats)
 {
-    if (workspace_bytes < smorph_scm_forward_workspace<T>(g)) return hipErrorInvalidValue;
+    if (pstats && !(sizeof(T) == 4 && smorph_static_supported<T>(g))) return hipErrorInvalidValue;
+    if (!pstats && workspace_bytes < smorph_scm_forward_workspace<T>(g)) return hipErrorInvalidValue;
     const int64_t n = (int64_t)g.B * g.Cout * g.plane();
     if (n == 0) return hipSuccess;
     SmorphFwdParams<T> p{};
     p.x = x;
     p.w = w;
     p.alpha = alpha;
-    p.pout = reinterpret_cast<T*>(workspace);
     p.g = g;
+    if constexpr (sizeof(T) == 4)
+    {
+        // Saving: the W / S array holds the pair outputs, [B, Cout, Cin, H, W] as the workspace would.
+        p.pstats = pstats;
+        p.nstat = smorph_stats_count<T>(MERGE_SMOOTH, g);
+    }
+    p.pout = pstats ? reinterpret_cast<T*>(pstats + 2 * p.nstat) : reinterpret_cast<T*>(workspace);
     // The float32 static kernels (one row per wave) write the pair outputs where they exist.
     p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
     hipError_t err = launch_smorph_fwd<T, MK_SMOOTH, false>(p, stream);
@@ -708,10 +715,13 @@ hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* b
 template <typename T>
 hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* beta, const T* out, const T* sstats, const T* grad_out,
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream)
+                               hipStream_t stream, const float* pstats)
 {
     hipError_t err;
-    const SmorphBwdPlan s = plan_smorph_bwd<T>(MERGE_SMOOTH, g);
+    if (pstats && !(sizeof(T) == 4 && smorph_static_supported<T>(g))) return hipErrorInvalidValue;
+    if (workspace_bytes < smorph_scm_backward_workspace<T>(g)) return hipErrorInvalidValue;
+    const SmorphBwdPlan s = plan_smorph_bwd<T>(MERGE_SMOOTH, g, pstats != nullptr);
+    // The layout below is this plan's; never lay it out past the buffer.
     if (workspace_bytes < smorph_plan_workspace<T>(s, g)) return hipErrorInvalidValue;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
@@ -759,7 +769,10 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     if constexpr (sizeof(T) == 4)
         if (stat)
         {
-            // The float32 static kernel, recomputing each pair's statistics (one row per wave).
+            // The float32 static kernels: from the saved pair statistics (two rows per wave), or
+            // recomputing them (one row per wave).
+            p.pstats = pstats;
+            p.nstat = smorph_stats_count<T>(MERGE_SMOOTH, g);
             if ((err = launch_smorph_bwd_static(MK_SMOOTH, p, stream)) != hipSuccess) return err;
             launched = true;
         }
@@ -780,9 +793,10 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     template size_t smorph_scm_forward_workspace<T>(const Geom&);                                                                        \
     template size_t smorph_scm_backward_workspace<T>(const Geom&);                                                                       \
     template size_t smorph_scm_lds<T>(const Geom&, bool);                                                                                \
-    template hipError_t smorph_scm_forward<T>(const T*, const T*, const T*, const T*, T*, T*, const Geom&, void*, size_t, hipStream_t); \
+    template hipError_t smorph_scm_forward<T>(const T*, const T*, const T*, const T*, T*, T*, const Geom&, void*, size_t, hipStream_t,  \
+                                              float*);                                                                               \
     template hipError_t smorph_scm_backward<T>(const T*, const T*, const T*, const T*, const T*, const T*, const T*, T*, T*, T*, T*,   \
-                                               const Geom&, void*, size_t, hipStream_t);
+                                               const Geom&, void*, size_t, hipStream_t, const float*);
 
 MCA_INSTANTIATE_SCM(float)
 MCA_INSTANTIATE_SCM(double)

@@ -397,8 +397,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW >
         }
         else if constexpr (MK == MK_SMOOTH)
         {
-            // Every pair's output, merged afterwards by the soft merge (smorph.hip).
-            if (in) p.pout[(((int64_t)b * g.Cout + o) * g.Cin + i) * plane + (int64_t)h * g.W + wc] = Wsum * inv;
+            // Every pair's output, merged afterwards by the soft merge (smorph.hip); with SAVE the
+            // saved W / S values above are those outputs (the same index), read from there.
+            if (!SAVE && in) p.pout[(((int64_t)b * g.Cout + o) * g.Cin + i) * plane + (int64_t)h * g.W + wc] = Wsum * inv;
         }
         else
         {
@@ -798,15 +799,15 @@ __host__ __device__ constexpr int smorph_pack_value(int row) { return ((row & 1)
 
 // Packed bins: the K tap values in the order the two-row backward emits them (tile row j = 1 .. KH,
 // then kw: tap (KH - j) KW + kw) in groups of four, group q of 64 doubles, 16-lane row r holding
-// emission 4 q + smorph_pack_value(r), 16 copies; then the last emission (K % 4 == 1) and alpha,
-// unpacked, 16 copies each (a 32-double tail keeps the 11x11 kernel's LDS within five workgroups per
-// CU).
-template <int K>
+// emission 4 q + smorph_pack_value(r), 16 copies; then the last emission (K % 4 == 1), alpha and for
+// SMOOTH (NB = 2) beta, unpacked, 16 copies each (a tail of 32 or 48 doubles keeps the 11x11
+// kernel's LDS within five workgroups per CU).
+template <int K, int NB = 1>
 struct PackedBins
 {
     static constexpr bool on = K > 25;
     static constexpr int groups = K / 4;
-    static constexpr int size = groups * WAVE + 2 * 16;
+    static constexpr int size = groups * WAVE + (1 + NB) * 16;
 };
 
 // Rows of right-halo values (KW - 1 each) that one register holds, and the registers for NR rows.
@@ -943,12 +944,15 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
     constexpr int RH = 2, TH = NWAVES * RH, ROWS = TH + KH - 1, COLS = TILE_W + KW - 1;
     constexpr int NC = smorph_bin_copies(K);
+    // Values after the K taps: grad_alpha, then grad_beta for SMOOTH.
+    constexpr int NB = MK == MK_SMOOTH ? 2 : 1;
     constexpr bool PACK = PackedBins<K>::on;
-    constexpr int NBINS = PACK ? PackedBins<K>::size : (K + 1) * NC;
+    constexpr int NBINS = PACK ? PackedBins<K, NB>::size : (K + NB) * NC;
     __shared__ float tile[ROWS * COLS];
     __shared__ Acc gtile[ROWS * COLS];
-    // grad_weight bins of the K taps, then grad_alpha: NC copies each, or PACK's groups of four.
+    // grad_weight bins of the K taps, then the NB others: NC copies each, or PACK's groups of four.
     __shared__ __align__(32) Acc bins[NBINS];
+    // Structuring element, alpha and (SMOOTH) beta of the current / next pair.
     __shared__ __align__(16) float wl[2][(K + 4) & ~3];
     const Geom g = p.g;
     const Tiling t = p.t;
@@ -976,12 +980,16 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             wl[buf][threadIdx.x] = p.w[((int64_t)o * g.Cw + wi) * K + threadIdx.x];
         else if (threadIdx.x == K)
             wl[buf][K] = p.alpha[pair_index(o)];
+        else if (MK == MK_SMOOTH && threadIdx.x == K + 1)
+            wl[buf][K + 1] = p.beta[o];
     };
-    constexpr int NPART = K <= 25 ? smorph_lds_partials(false) : 1;
+    constexpr int NPART = K <= 25 ? smorph_lds_partials(MK == MK_SMOOTH) : 1;
     __shared__ float partials[NPART];
-    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT);
+    const bool lds_partials = smorph_bwd_lds_partials(g, MK == MK_IDENT, MK == MK_SMOOTH);
     for (int j = threadIdx.x; j < NPART; j += BLOCK) partials[j] = 0.0f;
     for (int j = threadIdx.x; j < NBINS; j += BLOCK) bins[j] = Acc(0);
+    // grad_beta partials: row (slot, i) of Cout values.
+    float* __restrict__ part_b = MK == MK_SMOOTH ? p.part_b + ((int64_t)slot * g.Cin + i) * g.Cout : nullptr;
     const int tile_begin = strip * p.tps;
     const int tile_end = min(tile_begin + p.tps, t.ntiles());
     const float* xw = tile + RH * wave * COLS + lane + KW - 1;  // tile row 2 wave, this lane's tap-0 column
@@ -1032,11 +1040,13 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             gtile[idx] = Acc(0);
         }
         stage_weights(o_begin, 0);
-        // Output gradient, saved statistics (and for MAX / MIN the merged output and winner count)
-        // of both pixels, one output channel ahead.
+        // Output gradient, saved statistics (and for MAX / MIN the merged output and winner count;
+        // for SMOOTH the merged output and the soft merge's ref and 1 / sum) of both pixels, one
+        // output channel ahead.
         const int64_t pixA = (int64_t)min(hA, g.H - 1) * g.W + min(wc, g.W - 1);
         const int64_t pixB = (int64_t)min(hA + 1, g.H - 1) * g.W + min(wc, g.W - 1);
         float gA_n = 0.0f, gB_n = 0.0f, cA_n = 0.0f, cB_n = 0.0f, oA_n = 0.0f, oB_n = 0.0f;
+        SmoothPixel mA_n{0.0f, 0.0f, 0.0f}, mB_n{0.0f, 0.0f, 0.0f};
         PairStats sA_n{0.0f, 0.0f, 0.0f}, sB_n{0.0f, 0.0f, 0.0f};
         auto load_g = [&](int o) {
             o = min(o, o_end - 1);
@@ -1047,8 +1057,19 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             {
                 cA_n = p.counts[ob + pixA];
                 cB_n = p.counts[ob + pixB];
+            }
+            if constexpr (MK == MK_MAX || MK == MK_MIN || MK == MK_SMOOTH)
+            {
                 oA_n = p.out[ob + pixA];
                 oB_n = p.out[ob + pixB];
+            }
+            if constexpr (MK == MK_SMOOTH)
+            {
+                const int64_t nout = (int64_t)g.B * g.Cout * plane;
+                mA_n.ref = p.sstats[ob + pixA];
+                mA_n.inv = p.sstats[nout + ob + pixA];
+                mB_n.ref = p.sstats[ob + pixB];
+                mB_n.inv = p.sstats[nout + ob + pixB];
             }
             const float* q = p.pstats + (((int64_t)b * g.Cout + o) * cpair + (MK == MK_IDENT ? 0 : i)) * plane;
             sA_n.ref = __builtin_nontemporal_load(q + pixA);
@@ -1058,7 +1079,9 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             sB_n.inv = __builtin_nontemporal_load(q + p.nstat + pixB);
             sB_n.outp = __builtin_nontemporal_load(q + 2 * p.nstat + pixB);
         };
-        auto route_pixel = [&](bool in, float gv, float cnt, float outv, const PairStats& st) {
+        // bterm (SMOOTH): the pixel's grad_beta term.
+        auto route_pixel = [&](bool in, float gv, float cnt, float outv, const PairStats& st, const SmoothPixel& sm, float& bterm) {
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fmaf)
             RoutePixel r;
             gv = in ? gv * p.scale : 0.0f;
             if constexpr (MK == MK_MAX || MK == MK_MIN)
@@ -1067,6 +1090,16 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
                 // values are not finite), as the reference.
                 gv = gv / (cnt > 0.0f ? cnt : 1.0f);
                 gv = is_winner(st.outp, outv) ? gv : 0.0f;
+            }
+            if constexpr (MK == MK_SMOOTH)
+            {
+                // g' = g q (1 + beta (c - out)) with q = exp(beta (c - ref)) / sum the pair's share of
+                // the soft merge, and grad_beta's term q (c - ref)(c - out) g, also with a zero gradient
+                // (a NaN pair reaches grad_beta), as the recomputing kernel (smorph_bwd_pair).
+                const float c = st.outp;
+                const float q = exp_ref((c - sm.ref) * sm.beta) * sm.inv;
+                bterm = in ? q * (c - sm.ref) * (c - outv) * gv : 0.0f;
+                gv = gv * fmaf(sm.beta * q, c - outv, q);
             }
             r.ref = st.ref;
             r.scaled = in ? gv * st.inv : 0.0f;
@@ -1079,10 +1112,12 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
         for (int o = o_begin; o < o_end; ++o)
         {
             const int buf = (o - o_begin) & 1;
-            const RoutePixel A = route_pixel(inA, gA_n, cA_n, oA_n, sA_n);
-            const RoutePixel B = route_pixel(inB, gB_n, cB_n, oB_n, sB_n);
-            load_g(o + 1);
             const float* w = wl[buf];
+            float btA = 0.0f, btB = 0.0f;
+            if constexpr (MK == MK_SMOOTH) mA_n.beta = mB_n.beta = w[K + 1];
+            const RoutePixel A = route_pixel(inA, gA_n, cA_n, oA_n, sA_n, mA_n, btA);
+            const RoutePixel B = route_pixel(inB, gB_n, cB_n, oB_n, sB_n, mB_n, btB);
+            load_g(o + 1);
             const float a = w[K];
             float asum;
             const bool za = alpha_is_zero(a);
@@ -1096,15 +1131,34 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
                 asum = za ? smorph_bwd_pair2<MK, KH, KW, true, true>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile)
                           : smorph_bwd_pair2<MK, KH, KW, true, false>(xw, w, a, A, B, rows, pen, gw, bl, btail, hcell, gtile);
             if constexpr (!PACK) lds_add(&bl[K * NC], (Acc)asum);
+            if constexpr (MK == MK_SMOOTH)
+            {
+                const float bterm = btA + btB;
+                if constexpr (PACK)
+                    lds_add(&btail[32], (Acc)bterm);
+                else
+                    lds_add(&bl[(K + 1) * NC], (Acc)bterm);
+            }
             if (o + 1 < o_end) stage_weights(o + 1, buf ^ 1);
             __syncthreads();
+            // Partial of value k (tap k < K, K alpha, K + 1 beta) of pair o into this workgroup's slot.
+            auto put = [&](int k, Acc v) {
+                if (lds_partials)
+                    partials[(o - o_begin) * (K + NB) + k] += (float)v;  // one owner per entry
+                else if (k < K)
+                    global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
+                else if (k == K)
+                    global_add(&part_a[pair_index(o)], (float)v);
+                else
+                    global_add(&part_b[o], (float)v);
+            };
             if constexpr (PACK)
             {
                 // Sum the 16 copies of each value (4 threads per value, 4 adjacent copies each, a
                 // butterfly over the 4) into this workgroup's slot: the packed groups, then the tail.
                 // The thread count is a multiple of 4.
                 constexpr int NG = PackedBins<K>::groups;
-                for (int j = threadIdx.x; j < NG * 16 + 2 * 4; j += BLOCK)
+                for (int j = threadIdx.x; j < NG * 16 + (1 + NB) * 4; j += BLOCK)
                 {
                     double4* q = reinterpret_cast<double4*>(&bins[j * 4]);
                     const double4 c4 = *q;
@@ -1112,18 +1166,13 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
                     Acc v = (c4.x + c4.y) + (c4.z + c4.w);
                     v += __shfl_xor(v, 1, 4);
                     v += __shfl_xor(v, 2, 4);
-                    // Emission index: in the groups, or the tail's K - 1 (the last tap) and K (alpha).
+                    // Emission index: in the groups, or the tail's K - 1 (the last tap), K (alpha) and
+                    // K + 1 (beta).
                     const int e = j < NG * 16 ? (j >> 4) * 4 + smorph_pack_value((j >> 2) & 3) : K - 1 + ((j - NG * 16) >> 2);
-                    if ((j & 3) == 0 && e <= K)
+                    if ((j & 3) == 0 && e < K + NB)
                     {
-                        // Emission e < K is tap (KH - 1 - e / KW) KW + e % KW; e == K is alpha.
-                        const int k = e < K ? (KH - 1 - e / KW) * KW + e % KW : K;
-                        if (lds_partials)
-                            partials[(o - o_begin) * (K + 1) + k] += (float)v;
-                        else if (k < K)
-                            global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
-                        else
-                            global_add(&part_a[pair_index(o)], (float)v);
+                        // Emission e < K is tap (KH - 1 - e / KW) KW + e % KW; the others keep their index.
+                        put(e < K ? (KH - 1 - e / KW) * KW + e % KW : e, v);
                     }
                 }
                 __syncthreads();
@@ -1132,7 +1181,7 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
             // Sum the NC copies of each bin (8 threads per bin, NC / 8 adjacent copies each, a butterfly
             // over the 8) into this workgroup's slot, as the one-row kernel does.
             constexpr int PER = NC / 8;
-            for (int j = threadIdx.x; j < (K + 1) * 8; j += BLOCK)
+            for (int j = threadIdx.x; j < (K + NB) * 8; j += BLOCK)
             {
                 Acc v;
                 if constexpr (PER == 4)
@@ -1151,16 +1200,7 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
                 }
 #pragma unroll
                 for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
-                if ((j & 7) == 0)
-                {
-                    const int k = j >> 3;
-                    if (lds_partials)
-                        partials[(o - o_begin) * (K + 1) + k] += (float)v;
-                    else if (k < K)
-                        global_add(&part_w[((int64_t)o * g.Cw + wi) * K + k], (float)v);
-                    else
-                        global_add(&part_a[pair_index(o)], (float)v);
-                }
+                if ((j & 7) == 0) put(j >> 3, v);
             }
             __syncthreads();
         }
@@ -1176,14 +1216,16 @@ smorph_bwd_saved2(const SmorphBwdParams<float> p)
     if (lds_partials)
     {
         __syncthreads();
-        const int n = (o_end - o_begin) * (K + 1);
+        const int n = (o_end - o_begin) * (K + NB);
         for (int j = threadIdx.x; j < n; j += BLOCK)
         {
-            const int ol = j / (K + 1), k = j - ol * (K + 1), o = o_begin + ol;
+            const int ol = j / (K + NB), k = j - ol * (K + NB), o = o_begin + ol;
             if (k < K)
                 part_w[((int64_t)o * g.Cw + wi) * K + k] = partials[j];
-            else
+            else if (k == K)
                 part_a[pair_index(o)] = partials[j];
+            else
+                part_b[o] = partials[j];
         }
     }
 }
@@ -1209,9 +1251,7 @@ static hipError_t fwd_size(int mk, bool stats, const SmorphFwdParams<float>& p, 
         case MK_SUM: smorph_fwd_static<MK_SUM, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MAX: smorph_fwd_static<MK_MAX, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MIN: smorph_fwd_static<MK_MIN, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
-        case MK_SMOOTH:
-            if constexpr (!SAVE) smorph_fwd_static<MK_SMOOTH, KS, KS, false, false><<<blocks, BLOCK, 0, stream>>>(p);
-            break;
+        case MK_SMOOTH: smorph_fwd_static<MK_SMOOTH, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
         default: smorph_fwd_static<MK_IDENT, KS, KS, false, SAVE><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
@@ -1259,6 +1299,7 @@ static hipError_t bwd2_size(int mk, const SmorphBwdParams<float>& p, hipStream_t
         case MK_SUM: smorph_bwd_saved2<MK_SUM, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MAX: smorph_bwd_saved2<MK_MAX, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         case MK_MIN: smorph_bwd_saved2<MK_MIN, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
+        case MK_SMOOTH: smorph_bwd_saved2<MK_SMOOTH, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
         default: smorph_bwd_saved2<MK_IDENT, KS, KS><<<blocks, BLOCK, 0, stream>>>(p); break;
     }
     return hipGetLastError();
@@ -1266,8 +1307,6 @@ static hipError_t bwd2_size(int mk, const SmorphBwdParams<float>& p, hipStream_t
 
 hipError_t launch_smorph_bwd_static(int mk, const SmorphBwdParams<float>& p, hipStream_t stream)
 {
-    // The SMOOTH merge recomputes (no saved-statistics kernel).
-    if (mk == MK_SMOOTH && p.pstats) return hipErrorInvalidValue;
     // From saved statistics: the two-row kernel (64 x 8 tiles); recomputing: the one-row kernel.
     if (p.t.rh != (p.pstats ? 2 : 1)) return hipErrorInvalidValue;
     switch (p.g.KH)

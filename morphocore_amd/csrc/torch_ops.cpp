@@ -860,7 +860,9 @@ Tensor smorph(const Tensor& input, const Tensor& weight, const Tensor& alpha, in
 }
 
 // SmorphSCM (smorph_scm.cpp:13-96): smorph with the SMOOTH channel merge, one beta per output channel.
-// The forward keeps the soft merge's ref and 1 / sum per output pixel for the backward.
+// The forward keeps the soft merge's ref and 1 / sum per output pixel for the backward, and in float32
+// (when the saved-statistics budget admits them) each pair's ref, 1 / S and W / S, which spare the
+// backward their recomputation.
 class SmorphScmFunction : public torch::autograd::Function<SmorphScmFunction>
 {
 public:
@@ -882,18 +884,35 @@ public:
         }
         Tensor out = torch::empty({g.B, g.Cout, g.H, g.W}, x.options());
         Tensor mstats = needs_grad ? torch::empty({2, g.B, g.Cout, g.H, g.W}, x.options()) : Tensor();
-        const size_t n = f32 ? mca_smorph_scm_forward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)
-                             : mca_smorph_scm_forward_workspace_size_f64(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
-        Tensor ws = byte_buffer((int64_t)n, x);
-        if (f32)
-            check_rc(mca_smorph_scm_forward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
-                                                out.data_ptr<float>(), mstats.defined() ? mstats.data_ptr<float>() : nullptr, g.B, g.Cin, g.Cout,
-                                                g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        // float32 with a backward to follow: the pair statistics too, when the budget admits them
+        // (they then also stand in for the pair-output workspace).
+        Tensor pstats;
+        if (f32 && needs_grad)
+        {
+            const int64_t nbytes = (int64_t)mca_smorph_scm_stats_bytes_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            if (nbytes > 0) pstats = SavedStats::get().allocate(nbytes, x.options());
+        }
+        if (pstats.defined())
+        {
+            check_rc(mca_smorph_scm_forward_stats_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                      out.data_ptr<float>(), mstats.data_ptr<float>(), pstats.data_ptr<float>(), g.B, g.Cin,
+                                                      g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, stream_of(x)));
+        }
         else
-            check_rc(mca_smorph_scm_forward_f64(x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), bt.data_ptr<double>(),
-                                                out.data_ptr<double>(), mstats.defined() ? mstats.data_ptr<double>() : nullptr, g.B, g.Cin,
-                                                g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
-        ctx->save_for_backward({out, alpha, beta, x, w, mstats});
+        {
+            const size_t n = f32 ? mca_smorph_scm_forward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)
+                                 : mca_smorph_scm_forward_workspace_size_f64(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
+            Tensor ws = byte_buffer((int64_t)n, x);
+            if (f32)
+                check_rc(mca_smorph_scm_forward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                    out.data_ptr<float>(), mstats.defined() ? mstats.data_ptr<float>() : nullptr, g.B, g.Cin,
+                                                    g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+            else
+                check_rc(mca_smorph_scm_forward_f64(x.data_ptr<double>(), w.data_ptr<double>(), ap.data_ptr<double>(), bt.data_ptr<double>(),
+                                                    out.data_ptr<double>(), mstats.defined() ? mstats.data_ptr<double>() : nullptr, g.B, g.Cin,
+                                                    g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        }
+        ctx->save_for_backward({out, alpha, beta, x, w, mstats, pstats});
         return out;
     }
 
@@ -906,6 +925,7 @@ public:
         const Tensor& x = saved[3];
         const Tensor& w = saved[4];
         const Tensor& mstats = saved[5];
+        const Tensor& pstats = saved[6];
         TORCH_CHECK(mstats.defined(), "smorph_scm: the forward ran without gradients and kept no merge statistics");
         const Tensor grad_output = grad_outputs[0].contiguous();
         TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
@@ -921,11 +941,19 @@ public:
         {
             const size_t n = mca_smorph_scm_backward_workspace_size_f32(g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW);
             Tensor ws = byte_buffer((int64_t)n, x);
-            check_rc(mca_smorph_scm_backward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
-                                                 out.data_ptr<float>(), mstats.data_ptr<float>(), grad_output.data_ptr<float>(),
-                                                 grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(), grad_pairs.data_ptr<float>(),
-                                                 grad_beta.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW, ws.data_ptr(),
-                                                 (size_t)ws.numel(), stream_of(x)));
+            if (pstats.defined())
+                check_rc(mca_smorph_scm_backward_stats_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                           out.data_ptr<float>(), mstats.data_ptr<float>(), pstats.data_ptr<float>(),
+                                                           grad_output.data_ptr<float>(), grad_input.data_ptr<float>(),
+                                                           grad_weight.data_ptr<float>(), grad_pairs.data_ptr<float>(),
+                                                           grad_beta.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW,
+                                                           ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+            else
+                check_rc(mca_smorph_scm_backward_f32(x.data_ptr<float>(), w.data_ptr<float>(), ap.data_ptr<float>(), bt.data_ptr<float>(),
+                                                     out.data_ptr<float>(), mstats.data_ptr<float>(), grad_output.data_ptr<float>(),
+                                                     grad_input.data_ptr<float>(), grad_weight.data_ptr<float>(), grad_pairs.data_ptr<float>(),
+                                                     grad_beta.data_ptr<float>(), g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW,
+                                                     ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
         }
         else
         {

@@ -20,7 +20,7 @@ def declared_symbols():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _native.lib()
     symbols = declared_symbols()
-    assert len(symbols) == 50
+    assert len(symbols) == 53
     for name in symbols:
         assert hasattr(lib, name), name
     assert sorted(_native.EXPORTS) == symbols
@@ -121,10 +121,35 @@ def test_smorph_stats_bytes_and_rejection():
     assert rc == 0, lib.mca_last_error().decode()
 
 
+def test_smorph_scm_stats_bytes_and_rejection():
+    """The SMOOTH merge's saved-statistics entry points: as many values as the SUM merge's (three per
+    channel pair and output pixel) for the static sizes, none otherwise; a configuration without
+    them, or a null buffer, is an argument error before any device work; an empty batch needs none."""
+    lib = _native.lib()
+    B, Cin, Cout, H, W = 2, 3, 4, 16, 16
+    for k in (3, 5, 7, 11):
+        assert lib.mca_smorph_scm_stats_bytes_f32(B, Cin, Cout, Cin, H, W, k, k) == 12 * B * Cout * Cin * H * W
+    assert lib.mca_smorph_scm_stats_bytes_f32(B, Cin, Cout, Cin, H, W, 4, 4) == 0
+    assert lib.mca_smorph_scm_stats_bytes_f32(B, Cin, Cout, Cin, H, W, 3, 5) == 0
+    assert lib.mca_smorph_scm_stats_bytes_f32(B, Cin, Cout, 1, H, W, 3, 3) == 0  # Cw != Cin
+    nulls = (None,) * 7
+    rc = lib.mca_smorph_scm_forward_stats_f32(*nulls, B, Cin, Cout, Cin, H, W, 4, 4, None)
+    assert rc == 1 and "No saved smorph statistics" in lib.mca_last_error().decode()
+    rc = lib.mca_smorph_scm_forward_stats_f32(*nulls, B, Cin, Cout, Cin, H, W, 3, 3, None)
+    assert rc == 1 and "stats must not be null" in lib.mca_last_error().decode()
+    rc = lib.mca_smorph_scm_backward_stats_f32(*(None,) * 12, B, Cin, Cout, Cin, H, W, 3, 3, None, 0, None)
+    assert rc == 1 and "stats must not be null" in lib.mca_last_error().decode()
+    assert _native.smorph_scm_stats_bytes(__import__("torch").float64, (B, Cin, Cout, Cin, H, W, 3, 3)) == 0
+    assert lib.mca_smorph_scm_stats_bytes_f32(0, Cin, Cout, Cin, H, W, 3, 3) == 0
+    rc = lib.mca_smorph_scm_forward_stats_f32(*nulls, 0, Cin, Cout, Cin, H, W, 3, 3, None)
+    assert rc == 0, lib.mca_last_error().decode()
+
+
 def _smorph_saved_plan_bytes(merge, B, Cin, Cout, H, W, K):
     """Workspace bytes of the float32 smorph backward from saved statistics (two output rows per
-    wave: 64 x 8 tiles), for a square static element: slot partials of grad_weight and grad_alpha,
-    MAX / MIN counts and merge target, and the two-stage slot reduction's scratch."""
+    wave: 64 x 8 tiles), for a square static element: slot partials of grad_weight and grad_alpha
+    (and for SMOOTH, merge 4, of grad_beta: Cin rows of Cout values per slot), MAX / MIN counts and
+    merge target, and the two-stage slot reduction's scratch."""
     align = lambda v: (v + 255) // 256 * 256  # noqa: E731
     ntiles = -(-W // 64) * -(-H // 8)
     nstrips = min(max(-(-8192 // (B * Cin)), 1), ntiles)
@@ -135,18 +160,25 @@ def _smorph_saved_plan_bytes(merge, B, Cin, Cout, H, W, K):
     nslots = B * -(-ntiles // tps)
     counts = 2 * B * Cout * H * W * 4 if merge in (0, 1) else 0
     scratch = -(-nslots // 32) * max(wnumel, npairs) * 4 if nslots > 32 else 0
-    return align(nslots * wnumel * 4) + align(nslots * npairs * 4) + align(counts) + align(scratch)
+    part_b = nslots * npairs * 4 if merge == 4 else 0
+    if merge == 4 and nslots * Cin > 32:
+        scratch = max(scratch, -(-(nslots * Cin) // 32) * Cout * 4)
+    return align(nslots * wnumel * 4) + align(nslots * npairs * 4) + align(part_b) + align(counts) + align(scratch)
 
 
-@pytest.mark.parametrize("merge", [0, 2, 3])
+@pytest.mark.parametrize("merge", [0, 2, 3, 4])
 @pytest.mark.parametrize("geom", [(4, 64, 100, 100, 3), (4, 64, 100, 100, 7), (2, 16, 300, 300, 5), (1, 8, 160, 200, 11)])
 def test_smorph_workspace_covers_the_saved_statistics_plan(merge, geom):
     """The workspace size the caller allocates must also hold the layout of the backward from saved
     statistics, whose rounding of tiles per strip can give more slots than the recomputing plan
-    (4 x 64 x 100 x 100: 26 strips against 25). Regression test of an out-of-bounds layout."""
+    (4 x 64 x 100 x 100: 26 strips against 25). Regression test of an out-of-bounds layout; merge 4
+    is the SMOOTH merge's (smorph_scm) backward."""
     B, C, H, W, K = geom
     lib = _native.lib()
-    have = lib.mca_smorph_backward_workspace_size_f32(merge, B, C, C, C, H, W, K, K)
+    if merge == 4:
+        have = lib.mca_smorph_scm_backward_workspace_size_f32(B, C, C, C, H, W, K, K)
+    else:
+        have = lib.mca_smorph_backward_workspace_size_f32(merge, B, C, C, C, H, W, K, K)
     assert have >= _smorph_saved_plan_bytes(merge, B, C, C, H, W, K)
 
 
