@@ -255,16 +255,19 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         what = f"fused {cfg['first']} -> identity pair forward (mca_morpho_pair_forward, one kernel)"
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "scm":
-        # The SMOOTH merge's backward, the larger part of its step, from the forward's saved pair statistics as the
-        # operator runs it (float32 static two-row kernel at 7x7): 18 flop per tap (the smorph tap convention) plus
-        # the soft merge's per-pixel work, not counted.
+        # The SMOOTH merge's backward, the larger part of its step, as the operator runs it: from the forward's saved
+        # pair statistics when it would save them (float32 static two-row kernel at 7x7; 10 flop per tap, as the
+        # smorph backward from saved statistics), else recomputing them (18). The soft merge's per-pixel work is not
+        # counted.
+        from morphocore_amd import _C
+
         a_p = torch.full((Cout * Cin,), 1.0, dtype=dtype, device=dev)
         beta = torch.full((Cout,), 1.0, dtype=dtype, device=dev)
         wt = ws[0]
         out = torch.empty((B, Cout, H, W), dtype=dtype, device=dev)
         mst = torch.empty((2, B, Cout, H, W), dtype=dtype, device=dev)
         nbytes = native.smorph_scm_stats_bytes(dtype, geom)
-        pst = torch.empty((nbytes // 4,), dtype=torch.float32, device=dev) if nbytes else None
+        pst = torch.empty((nbytes // 4,), dtype=torch.float32, device=dev) if _C.saved_stats_admit(nbytes, dev.index or 0) else None
         native.smorph_scm_forward(x, wt, a_p, beta, out, mst, geom, pair_stats=pst)
         gen = torch.Generator(device=dev).manual_seed(2)
         grad = torch.randn((B, Cout, H, W), generator=gen, dtype=dtype, device=dev)
@@ -273,8 +276,10 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         def launch():
             native.smorph_scm_backward(x, wt, a_p, beta, out, mst, grad, gx, gw, ga, gb, geom, pair_stats=pst)
 
-        entry = "mca_smorph_scm_backward_stats_f32" if pst is not None else "mca_smorph_scm_backward_f32"
-        return launch, 18 * t, "flop", f"smorph_scm backward, alpha 1, beta 1, from the forward's saved pair statistics ({entry}: kernels + reductions)"
+        if pst is not None:
+            return launch, 10 * t, "flop", ("smorph_scm backward, alpha 1, beta 1, from the forward's saved pair statistics "
+                                            "(mca_smorph_scm_backward_stats_f32: kernels + reductions)")
+        return launch, 18 * t, "flop", "smorph_scm backward, alpha 1, beta 1 (mca_smorph_scm_backward_f32: kernels + reductions)"
     if cfg["kind"] == "sigma":
         # The fused forward: x read once, the output and one tap byte per operation written once.
         pg = (B, Cin, H, W, KH, KW)
