@@ -256,9 +256,9 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         return launch, (2 * B * Cin * H * W * esz + 2 * B * Cin * H * W + 2 * ws[0].numel() * esz), "bytes", what
     if cfg["kind"] == "scm":
         # The SMOOTH merge's backward, the larger part of its step, as the operator runs it: from the forward's saved
-        # pair statistics when it would save them (float32 static two-row kernel at 7x7; 10 flop per tap, as the
-        # smorph backward from saved statistics), else recomputing them (18). The soft merge's per-pixel work is not
-        # counted.
+        # pair statistics when it would save them (float32 static two-row kernel at 7x7), else recomputing them; 18
+        # flop per tap either way (the smorph backward's algorithmic work), 10 executed from saved statistics. The
+        # soft merge's per-pixel work is not counted.
         from morphocore_amd import _C
 
         a_p = torch.full((Cout * Cin,), 1.0, dtype=dtype, device=dev)
@@ -277,7 +277,8 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
             native.smorph_scm_backward(x, wt, a_p, beta, out, mst, grad, gx, gw, ga, gb, geom, pair_stats=pst)
 
         if pst is not None:
-            return launch, 10 * t, "flop", ("smorph_scm backward, alpha 1, beta 1, from the forward's saved pair statistics "
+            launch.executed_work = 10 * t
+            return launch, 18 * t, "flop", ("smorph_scm backward, alpha 1, beta 1, from the forward's saved pair statistics "
                                             "(mca_smorph_scm_backward_stats_f32: kernels + reductions)")
         return launch, 18 * t, "flop", "smorph_scm backward, alpha 1, beta 1 (mca_smorph_scm_backward_f32: kernels + reductions)"
     if cfg["kind"] == "sigma":
@@ -327,11 +328,12 @@ def dominant(cfg, torch, native, x, ws, dtype, dev):
         native.smorph_backward(merge, x, w, alpha, out, grad, gx, gw, ga, geom, stats=stats)
 
     if stats is not None:
-        # Without the recomputation of S and W (8 flop per tap), a backward tap is its exponential
-        # and its routing: 10 flop.
+        # The backward's algorithmic work is 18 flop per tap (recomputation of ref, S and W 8, exponential 1,
+        # routing 9); from the saved statistics the kernel executes the exponential and the routing only: 10.
         what = (f"smorph backward, merge {cfg.get('merge', 'sum')}, alpha {a:g}, from the forward's saved pair statistics "
                 "(mca_smorph_backward_stats_f32: kernel + zero-fill + slot reduction)")
-        return launch, 10 * t, "flop", what
+        launch.executed_work = 10 * t
+        return launch, 18 * t, "flop", what
     what = f"smorph backward, merge {cfg.get('merge', 'sum')}, alpha {a:g} (mca_smorph_backward: kernel + zero-fill + slot reduction)"
     return launch, 18 * t, "flop", what
 
@@ -541,6 +543,7 @@ def main():
     x, ws, dtype = r["x"].detach(), [w.detach() for w in r["ws"]], r["dtype"]
     launch, dwork, dunit, what = dominant(cfg, torch, _native, x, ws, dtype, dev)
     kms, kn = time_launches(torch, launch)
+    executed = getattr(launch, "executed_work", None)
     del launch
     if dunit == "bytes":
         achieved = dwork / (kms * 1e-3) / 1e9
@@ -549,6 +552,10 @@ def main():
         peak = PEAK_FP64_TFLOPS if cfg["dtype"] == "f64" else PEAK_FP32_TFLOPS
         achieved = dwork / (kms * 1e-3) / 1e12
         roof = {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak}
+        if executed is not None:
+            # The work the kernel executes (algorithmic work less what the saved statistics spare it).
+            roof["executed_work_per_launch"] = executed
+            roof["frac_executed"] = executed / (kms * 1e-3) / 1e12 / peak
     roof["traffic"] = measured_traffic(args.config)
     roof.update({"kernel": what, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": dwork, "work_unit": dunit})
     ceiling = instruction_ceiling(args.config, cfg, roof, dwork)
