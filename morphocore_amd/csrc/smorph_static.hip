@@ -937,8 +937,13 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     return asum;
 }
 
+// Waves per SIMD requested: seven up to 5x5, six at 7x7, five at 11x11; SMOOTH (two more pixel
+// values and the soft merge's share per pair) five from 5x5 on: 87 registers without spills at 5x5,
+// where seven were out of reach (91 registers), and at 7x7 3 registers spilled instead of 18 at six
+// (measured on MI355X: 1% faster at 7x7, the same at 5x5).
 template <int MK, int KH, int KW>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(KH * KW > 49 ? 5 : (KH * KW > 25 ? 6 : 7), 8))) void
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
+    KH * KW > 49 ? 5 : ((MK == MK_SMOOTH && KH * KW >= 25) ? 5 : (KH * KW > 25 ? 6 : 7)), 8))) void
 smorph_bwd_saved2(const SmorphBwdParams<float> p)
 {
     constexpr int K = KH * KW, PH = KH / 2, PW = KW / 2;
