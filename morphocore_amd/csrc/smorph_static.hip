@@ -853,8 +853,13 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     // alpha log2(e) once per pair, in a vector register: each tap's exponential is 2^((v - ref) a2).
     float a2 = a * 1.44269504088896340736f;
     asm volatile("" : "+v"(a2));
-    auto route_tap = [&](const RoutePixel& P, float x, int k, int kw, float& asum) {
-        const float vk = x + wl[k];
+    // 11x11: each tap's two element values are read from LDS one tap ahead of their use, so that the
+    // read's latency overlaps the previous tap's arithmetic (the asm statement below ends each tap's
+    // scheduling region, which otherwise leaves every read just before its use, then a wait):
+    // measured 5% faster on MI355X at 11x11, 0.5% slower at 7x7 (more spills there).
+    constexpr bool WAHEAD = KW > 7;
+    auto route_tap = [&](const RoutePixel& P, float x, float wk, int kw, float& asum) {
+        const float vk = x + wk;
         float ek;
         if constexpr (ZA)
             ek = exp_ref_zero_alpha(MASKED ? (vk - P.ref) * a - pen[kw] : (vk - P.ref) * a, lo);
@@ -881,14 +886,34 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw) xr[kw] = xw[j * COLS - kw];
         float racc = 0.0f;
+        float wAn = 0.0f, wBn = 0.0f;  // WAHEAD: the element values of the next tap
+        if (WAHEAD && rv)
+        {
+            if (j < KH) wAn = wl[khA * KW];
+            if (j > 0) wBn = wl[khB * KW];
+        }
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
         {
             float cA = 0.0f, cB = 0.0f;
             if (rv)
             {
-                if (j < KH) cA = route_tap(A, xr[kw], khA * KW + kw, kw, asumA);
-                if (j > 0) cB = route_tap(B, xr[kw], khB * KW + kw, kw, asumB);
+                if constexpr (WAHEAD)
+                {
+                    const float wA = wAn, wB = wBn;
+                    if (kw + 1 < KW)
+                    {
+                        if (j < KH) wAn = wl[khA * KW + kw + 1];
+                        if (j > 0) wBn = wl[khB * KW + kw + 1];
+                    }
+                    if (j < KH) cA = route_tap(A, xr[kw], wA, kw, asumA);
+                    if (j > 0) cB = route_tap(B, xr[kw], wB, kw, asumB);
+                }
+                else
+                {
+                    if (j < KH) cA = route_tap(A, xr[kw], wl[khA * KW + kw], kw, asumA);
+                    if (j > 0) cB = route_tap(B, xr[kw], wl[khB * KW + kw], kw, asumB);
+                }
                 const float cs = j == 0 ? cA : (j == KH ? cB : cA + cB);
                 // Row sums per tile column across the wave (DPP wave_shr Horner over kw); what leaves
                 // lane 63 at step kw is the right halo column 63 + KW - kw: lane KW - 1 - kw keeps it.
