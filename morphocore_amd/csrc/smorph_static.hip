@@ -853,10 +853,12 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
     // alpha log2(e) once per pair, in a vector register: each tap's exponential is 2^((v - ref) a2).
     float a2 = a * 1.44269504088896340736f;
     asm volatile("" : "+v"(a2));
-    // 11x11: each tap's two element values are read from LDS one tap ahead of their use, so that the
-    // read's latency overlaps the previous tap's arithmetic (the asm statement below ends each tap's
+    // 11x11: each tap's two element values are read from LDS two taps ahead of their use, so that the
+    // read's latency overlaps the previous taps' arithmetic (the asm statement below ends each tap's
     // scheduling region, which otherwise leaves every read just before its use, then a wait):
-    // measured 5% faster on MI355X at 11x11, 0.5% slower at 7x7 (more spills there).
+    // measured on MI355X 5% faster at 11x11 one tap ahead, 1.2% more two taps ahead; one tap ahead
+    // was 0.5% slower at 7x7 (more spills there), and pinning the reads at the start of the tap with a
+    // scheduling barrier 3.8% slower at 11x11.
     constexpr bool WAHEAD = KW > 7;
     auto route_tap = [&](const RoutePixel& P, float x, float wk, int kw, float& asum) {
         const float vk = x + wk;
@@ -886,11 +888,19 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw) xr[kw] = xw[j * COLS - kw];
         float racc = 0.0f;
-        float wAn = 0.0f, wBn = 0.0f;  // WAHEAD: the element values of the next tap
+        float wAn = 0.0f, wBn = 0.0f, wAm = 0.0f, wBm = 0.0f;  // WAHEAD: the element values of the next two taps
         if (WAHEAD && rv)
         {
-            if (j < KH) wAn = wl[khA * KW];
-            if (j > 0) wBn = wl[khB * KW];
+            if (j < KH)
+            {
+                wAn = wl[khA * KW];
+                wAm = wl[khA * KW + 1];
+            }
+            if (j > 0)
+            {
+                wBn = wl[khB * KW];
+                wBm = wl[khB * KW + 1];
+            }
         }
 #pragma unroll
         for (int kw = 0; kw < KW; ++kw)
@@ -901,10 +911,12 @@ __device__ __forceinline__ float smorph_bwd_pair2(const float* xw, const float* 
                 if constexpr (WAHEAD)
                 {
                     const float wA = wAn, wB = wBn;
-                    if (kw + 1 < KW)
+                    wAn = wAm;
+                    wBn = wBm;
+                    if (kw + 2 < KW)
                     {
-                        if (j < KH) wAn = wl[khA * KW + kw + 1];
-                        if (j > 0) wBn = wl[khB * KW + kw + 1];
+                        if (j < KH) wAm = wl[khA * KW + kw + 2];
+                        if (j > 0) wBm = wl[khB * KW + kw + 2];
                     }
                     if (j < KH) cA = route_tap(A, xr[kw], wA, kw, asumA);
                     if (j > 0) cB = route_tap(B, xr[kw], wB, kw, asumB);
