@@ -185,3 +185,37 @@ def test_config4_full_size_identity_f64():
     _check_grad_input_regions(
         gx, x, ones,
         lambda xc, gc: O.morpho_backward(O.DILATION, O.MERGES["identity"], O.PADDINGS["replicate"], 0.0, xc, wn, gc)[0], 1, 16, 0.0)
+
+
+def test_scm_full_size():
+    """smorph_scm at configs[2]'s full size (bench.py --config 9): (8, 64, 256, 256), w~ (64, 64, 7, 7)
+    ~N(0, 0.1), alpha 1, beta per output channel: forward and grad_input regions against the oracle
+    on crops; with an all-ones output gradient the soft merge's weights q_i (1 + beta (c_i - out)) sum
+    to 1 over the input channels, and each pair's routing weights to 1 over its taps, so grad_weight[o]
+    sums to B*H*W and grad_input to B*Cout*H*W."""
+    print("smorph_scm full size", flush=True)
+    dev = torch.device("cuda")
+    B, C, H, W, K = 8, 64, 256, 256, 7
+    P = K // 2
+    x = seeded(60, B, C, H, W, kind="randn").to(dev)
+    wt = seeded(61, C, C, K, K, kind="randn", scale=0.1).to(dev)
+    alpha = torch.full((C, C), 1.0, device=dev)
+    beta = (torch.linspace(-3.0, 3.0, C)).to(dev)
+    g = seeded(62, B, C, H, W, kind="randn").to(dev)
+    xr = x.clone().requires_grad_(True)
+    out = torch.ops.morphocore.smorph_scm(xr, wt, alpha, beta)
+    out.backward(g)
+    an, wn, bn = _np(alpha), _np(wt), _np(beta)
+    _check_forward_regions(out, x, lambda xc: O.smorph_scm_forward(xc, wn, an, bn), P, 8, 1e-6)
+    _check_grad_input_regions(xr.grad, x, g, lambda xc, gc: O.smorph_scm_backward(xc, wn, an, bn, gc)[0], P, 8, 1e-6)
+    del out, xr
+    xr = x.clone().requires_grad_(True)
+    wr = wt.clone().requires_grad_(True)
+    out = torch.ops.morphocore.smorph_scm(xr, wr, alpha, beta)
+    out.backward(torch.ones_like(out))
+    per_o = wr.grad.double().sum(dim=(1, 2, 3))
+    n = B * H * W
+    err = float((per_o - n).abs().max()) / n
+    assert err <= 1e-6, f"grad_weight[o] sums: {err}"
+    total = float(xr.grad.double().sum())
+    assert abs(total - n * C) / (n * C) <= 1e-6, f"grad_input sum: {total}"
