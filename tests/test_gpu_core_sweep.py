@@ -166,6 +166,6 @@ def test_smorph_sweep(c, monkeypatch):
     _smorph_run(c, monkeypatch, scm=False)
 
 
-@pytest.mark.parametrize("c", list(_smorph_cases(40, 7303, ["sum"])), ids=_ids)
+@pytest.mark.parametrize("c", list(_smorph_cases(80, 7303, ["sum"])), ids=_ids)
 def test_smorph_scm_sweep(c, monkeypatch):
     _smorph_run(c, monkeypatch, scm=True)
