@@ -4,6 +4,7 @@ import torch.nn as nn
 from ..functional._pair import EROSION, fused_pair
 from .dilation import Dilation
 from .erosion import Erosion
+from ._plain import calls_forward_plainly
 
 _SHARED = ('padding_mode', 'padding_value', 'save_indices', 'weight_dropout', 'noise_scale', 'training')
 
@@ -49,9 +50,11 @@ class Opening(nn.Module):
             self.dilation.weight = self.erosion.weight
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # Both stages per channel with the same settings: one fused operator call (same values and draws).
+        # Both stages per channel with the same settings: one fused operator call (same values and draws),
+        # unless a hook or an override of a sub-module's forward expects the two calls.
         a, b = self.erosion, self.dilation
-        if a.channel_merge_mode == 'identity' and all(getattr(a, k) == getattr(b, k) for k in _SHARED):
+        if (a.channel_merge_mode == 'identity' and all(getattr(a, k) == getattr(b, k) for k in _SHARED)
+                and calls_forward_plainly(a, Erosion) and calls_forward_plainly(b, Dilation)):
             out = fused_pair(x, a.weight, b.weight, EROSION, a.padding_mode, a.save_indices, a.padding_value, a.weight_dropout, a.training,
                              a.noise_scale)
             if out is not None:

@@ -159,6 +159,29 @@ def test_dropout_mask_matches_the_reference_loop(shape, p):
         assert bool(rows.any(dim=1).all())
 
 
+def test_dropout_mask_of_a_permuted_weight():
+    """A weight that is not contiguous (a permuted view: rand_like keeps its strides) gets its one
+    survivor per pair on the mask itself, at the tap the reference's loop draws, counted in the
+    view's own (row, column) order; every pair keeps a tap."""
+    from morphocore_amd.functional._dropout import dropout_keep
+
+    base = torch.randn(6, 2, 5, 3)
+    w = base.permute(0, 1, 3, 2)  # (6, 2, 3, 5), not contiguous
+    assert not w.is_contiguous()
+    for seed in range(4):
+        torch.manual_seed(seed)
+        ref = torch.rand_like(w) > 0.999
+        for i in range(w.shape[0]):
+            for j in range(w.shape[1]):
+                if not ref[i, j].any():
+                    flat = torch.randint(0, ref[i, j].numel(), (1,)).item()
+                    ref[i, j, flat // w.shape[3], flat % w.shape[3]] = True
+        torch.manual_seed(seed)
+        got = dropout_keep(w, 0.999)
+        assert torch.equal(got, ref)
+        assert bool(got.reshape(12, -1).any(dim=1).all())
+
+
 def test_composition_layers_construction():
     """Opening / Closing share one structuring element by default, which needs equal channel counts
     and the identity merge (reference nn/opening.py:104-140 messages); SigmaLayer has weight and
@@ -244,3 +267,53 @@ def test_fused_sigma_routing(monkeypatch):
     rec.calls.clear()
     mca.functional.sigma_layer(x, w, a.double(), 'identity')  # mixed dtypes: the composition
     assert [c[0] for c in rec.calls] == ["erosion", "dilation"]
+
+
+@pytest.mark.parametrize("kind", ["Opening", "Closing"])
+def test_fused_layer_keeps_sub_module_hooks(kind, monkeypatch):
+    """nn.Opening / nn.Closing take the fused operator only when calling the two sub-modules would run
+    nothing but their own forward: a forward hook, a pre-hook, a global hook or a subclass of a
+    stage makes the layer call both sub-modules, as the reference's layers always do."""
+    import importlib
+
+    _pair, dil_mod, ero_mod = (importlib.import_module(f"morphocore_amd.functional.{m}") for m in ("_pair", "dilation", "erosion"))
+    rec = _RecordingOps()
+    for m in (_pair, dil_mod, ero_mod):
+        monkeypatch.setattr(m, "ops", rec)
+    x = torch.zeros(2, 3, 8, 9)
+    layer = getattr(mca.nn, kind)(3, 3, 3)
+    first, second = (layer.erosion, layer.dilation) if kind == "Opening" else (layer.dilation, layer.erosion)
+    order = ["erosion", "dilation"] if kind == "Opening" else ["dilation", "erosion"]
+    layer(x)
+    assert [c[0] for c in rec.calls] == ["opening_closing"]
+    seen = []
+    for register in (lambda m: m.register_forward_hook(lambda *a: seen.append("hook")),
+                     lambda m: m.register_forward_pre_hook(lambda *a: seen.append("pre"))):
+        for m in (first, second):
+            rec.calls.clear()
+            h = register(m)
+            layer(x)
+            h.remove()
+            assert [c[0] for c in rec.calls] == order
+    assert len(seen) == 4
+    rec.calls.clear()
+    h = torch.nn.modules.module.register_module_forward_hook(lambda *a: None)
+    try:
+        layer(x)
+    finally:
+        h.remove()
+    assert [c[0] for c in rec.calls] == order
+
+    class Sub(type(second)):
+        def forward(self, x):
+            return super().forward(x) + 1.0
+
+    sub = Sub(3, 3, 3, channel_merge_mode="identity")
+    sub.weight = second.weight
+    if kind == "Opening":
+        layer.dilation = sub
+    else:
+        layer.erosion = sub
+    rec.calls.clear()
+    layer(x)
+    assert [c[0] for c in rec.calls] == order
