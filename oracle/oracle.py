@@ -248,7 +248,9 @@ def smorph_scm_backward(x, w_tilde, alpha, beta, grad_out):
 
 def smorph_w_tilde(w, alpha, merge_name):
     """w~ = tanh a * ((1 - tanh a)/2 * flip(w) + (1 + tanh a)/2 * w) (functional/smorph.py:56-70),
-    computed with torch on the CPU exactly as the reference's Python does."""
+    computed with torch on the CPU exactly as the reference's Python does. Pinned by closed forms
+    (tests/test_oracle.py: alpha 0 and +-20, tanh alpha = +-1/2 by hand, every alpha shape, the
+    derivatives in w and alpha), which planted mistakes fail."""
     import torch
 
     wt = torch.as_tensor(w)

@@ -398,3 +398,141 @@ def test_smorph_scm_gradients_match_finite_differences():
     gx, gw, ga, gb = O.smorph_scm_backward(x, w, alpha, beta, g)
     for got, arr in ((gx, x), (gw, w), (ga, alpha), (gb, beta)):
         np.testing.assert_allclose(got, _finite_difference(loss, arr, 1e-6), rtol=1e-5, atol=1e-7)
+
+
+# ----------------------------------------------------------------------------------------------
+# The smorph structuring-element blend w~ (functional/smorph.py:56-70), which the oracle computes
+# with torch exactly as the reference's Python and every smorph test through functional.smorph
+# uses as its expected value: pinned by closed forms derived apart from the formula.
+# ----------------------------------------------------------------------------------------------
+
+# An asymmetric 2x3 element with exact (small integer) entries.
+_W23 = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]])
+# alpha with tanh(alpha) = 1/2 exactly (in float64 and, rounded, in float32): the blend is then
+# 1/2 (1/4 flip(w) + 3/4 w) = flip(w) / 8 + 3 w / 8, worked out by hand for _W23 ...
+_ALPHA_HALF = {np.float64: 0.5493061443340549, np.float32: 0.54930615}
+_W23_HALF = np.array([[1.125, 1.375, 1.625], [1.875, 2.125, 2.375]])
+# ... and with tanh(alpha) = -1/2: -1/2 (3/4 flip(w) + 1/4 w) = -flip(_W23_HALF).
+_W23_MINUS_HALF = np.array([[-2.375, -2.125, -1.875], [-1.625, -1.375, -1.125]])
+
+
+def _w_tilde_failures(fn, dtype):
+    """Checks of a w~ function fn(w, alpha, merge_name) -> array; returns the names of those that fail."""
+    failed = []
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((3, 2, 3, 4)).astype(dtype)
+    fw = w[:, :, ::-1, ::-1]
+    # alpha = 0: tanh 0 = 0 zeroes the blend.
+    if not np.array_equal(fn(w, np.zeros((3, 2), dtype), "sum"), np.zeros_like(w)):
+        failed.append("alpha 0")
+    # alpha = +-20: tanh rounds to +-1 in both dtypes, so w~ = w and w~ = -flip(w) exactly.
+    if not np.array_equal(fn(w, np.full((3, 2), 20.0, dtype), "sum"), w):
+        failed.append("alpha +20")
+    if not np.array_equal(fn(w, np.full((3, 2), -20.0, dtype), "sum"), -fw):
+        failed.append("alpha -20")
+    # tanh alpha = +-1/2 on the asymmetric element, against the hand-computed values.
+    w23 = _W23.astype(dtype).reshape(1, 1, 2, 3)
+    a = _ALPHA_HALF[dtype]
+    if not np.array_equal(fn(w23, np.full((1, 1), a, dtype), "sum")[0, 0], _W23_HALF.astype(dtype)):
+        failed.append("tanh 1/2")
+    if not np.array_equal(fn(w23, np.full((1, 1), -a, dtype), "sum")[0, 0], _W23_MINUS_HALF.astype(dtype)):
+        failed.append("tanh -1/2")
+    # Shapes: a per-pair (Cout, Cin) alpha, a 0-d shared one, and the identity merge's (C,) and (C, 1),
+    # each entry from {0, 20, -20} so that every block has its own closed form.
+    choice = rng.integers(0, 3, (3, 2))
+    vals = np.array([0.0, 20.0, -20.0], dtype)
+    closed = lambda k, blk, fblk: (np.zeros_like(blk), blk, -fblk)[k]  # noqa: E731
+    got = fn(w, vals[choice], "sum")
+    if not all(np.array_equal(got[o, i], closed(choice[o, i], w[o, i], fw[o, i])) for o in range(3) for i in range(2)):
+        failed.append("per-pair alpha")
+    if not np.array_equal(fn(w, np.array(-20.0, dtype), "max"), -fw):
+        failed.append("shared 0-d alpha")
+    wi = w[:, :1]
+    fwi = wi[:, :, ::-1, ::-1]
+    for shape in ((3,), (3, 1)):
+        got = fn(wi, vals[choice[:, 0]].reshape(shape), "identity")
+        if not all(np.array_equal(got[c, 0], closed(choice[c, 0], wi[c, 0], fwi[c, 0])) for c in range(3)):
+            failed.append(f"identity alpha {shape}")
+    # Derivatives, by central differences in float64, against the closed forms
+    # d w~_j / d w_k = t (1 + t) / 2 [k = j] + t (1 - t) / 2 [k = flip(j)] and
+    # d w~ / d alpha = (1 - t^2) ((1 - 2 t) / 2 flip(w) + (1 + 2 t) / 2 w).
+    if dtype == np.float64:
+        w1 = w[:1, :1].copy()
+        alpha = 0.37
+        t = math.tanh(alpha)
+        eps = 1e-6
+        fd = (fn(w1, np.full((1, 1), alpha + eps), "sum") - fn(w1, np.full((1, 1), alpha - eps), "sum")) / (2 * eps)
+        want = (1 - t * t) * ((1 - 2 * t) / 2 * w1[:, :, ::-1, ::-1] + (1 + 2 * t) / 2 * w1)
+        if np.max(np.abs(fd - want)) > 1e-8:
+            failed.append("d/d alpha")
+        KH, KW = w1.shape[2:]
+        for kh, kw in ((0, 0), (1, 2), (2, 1)):
+            d = np.zeros_like(w1)
+            d[0, 0, kh, kw] = eps
+            fd = (fn(w1 + d, np.full((1, 1), alpha), "sum") - fn(w1 - d, np.full((1, 1), alpha), "sum")) / (2 * eps)
+            want = np.zeros_like(w1)
+            want[0, 0, kh, kw] += t * (1 + t) / 2
+            want[0, 0, KH - 1 - kh, KW - 1 - kw] += t * (1 - t) / 2
+            if np.max(np.abs(fd - want)) > 1e-8:
+                failed.append(f"d/d w[{kh},{kw}]")
+    return failed
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_smorph_w_tilde_closed_forms(dtype):
+    """oracle.smorph_w_tilde against closed forms: alpha = 0, +-20, tanh alpha = +-1/2 by hand on an
+    asymmetric element, the per-pair / shared / identity alpha shapes, and its derivatives in w and
+    alpha by central differences."""
+    assert _w_tilde_failures(O.smorph_w_tilde, dtype) == []
+
+
+def test_smorph_w_tilde_planted_mistakes_are_caught():
+    """Plausible mistakes in the blend each fail at least one of the closed-form checks: the two
+    weights swapped, the flip missing or along one axis only, the leading tanh missing, the identity
+    alpha broadcast along the input channels."""
+    import torch
+
+    def variant(mistake):
+        def fn(w, alpha, merge_name):
+            wt, at = torch.as_tensor(np.ascontiguousarray(w)), torch.as_tensor(np.asarray(alpha))
+            if mistake == "identity broadcast" and merge_name == "identity":
+                ta = torch.tanh(at).reshape(1, -1, 1, 1)
+            elif merge_name == "identity" or at.dim() == 1:
+                ta = torch.tanh(at).view(-1, 1, 1, 1)
+            else:
+                ta = torch.tanh(at).unsqueeze(-1).unsqueeze(-1)
+            t1, t2 = (1 + ta) / 2, (1 - ta) / 2
+            if mistake == "swap":
+                t1, t2 = t2, t1
+            flipped = {"no flip": wt, "flip rows": wt.flip(dims=(-2,))}.get(mistake, wt.flip(dims=(-2, -1)))
+            blend = t2 * flipped + t1 * wt
+            return (blend if mistake == "no tanh" else ta * blend).numpy()
+        return fn
+
+    for mistake in ("swap", "no flip", "flip rows", "no tanh", "identity broadcast"):
+        assert _w_tilde_failures(variant(mistake), np.float64), mistake
+
+
+@pytest.mark.parametrize("merge,alpha_shape", [("sum", (3, 2)), ("max", ()), ("identity", (3,)), ("identity", (3, 1)), ("mean", (3,))])
+def test_functional_smorph_passes_the_oracle_w_tilde(merge, alpha_shape, monkeypatch):
+    """The product's functional.smorph hands its operator the same w~ as oracle.smorph_w_tilde, bit for
+    bit (the operator itself is replaced by a recorder: no kernel runs on the CPU)."""
+    import importlib
+
+    import torch
+
+    smod = importlib.import_module("morphocore_amd.functional.smorph")
+    seen = {}
+
+    class Rec:
+        def smorph(self, x, w, alpha, merge_code):
+            seen["w"] = w
+            return x
+
+    monkeypatch.setattr(smod, "ops", Rec())
+    g = torch.Generator().manual_seed(3)
+    cw = 1 if merge == "identity" else 2
+    w = torch.randn(3, cw, 3, 5, generator=g, dtype=torch.float64)
+    alpha = torch.randn(alpha_shape, generator=g, dtype=torch.float64) * 2
+    smod.smorph(torch.zeros(1, cw if merge != "identity" else 3, 4, 4, dtype=torch.float64), w, alpha, channel_merge_mode=merge)
+    assert np.array_equal(seen["w"].numpy(), O.smorph_w_tilde(w.numpy(), alpha.numpy(), merge))
