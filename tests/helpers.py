@@ -1,4 +1,6 @@
 """Shared helpers of the tests: seeded inputs and the norm-wise error the gradient checks use."""
+import os
+
 import numpy as np
 import torch
 
@@ -35,3 +37,25 @@ def seeded(seed, *shape, dtype=torch.float32, kind="rand", scale=1.0, low=0.0):
     else:
         raise ValueError(kind)
     return t.to(dtype)
+
+
+REF_LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref", "libmorphocore_ref.so")
+
+
+def reference_run(kind, timeout=600, **arrays):
+    """Runs the reference's own CPU extension (oracle/_ref, built from its sources) on `arrays` in a
+    child process (oracle/ref_run.py; it registers the product's torch.ops namespace) on up to 16 host
+    threads, and returns its outputs as a dict of arrays."""
+    import subprocess
+    import sys
+    import tempfile
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    with tempfile.TemporaryDirectory() as d:
+        src, dst = os.path.join(d, "in.npz"), os.path.join(d, "out.npz")
+        np.savez(src, kind=np.array(kind), threads=np.array(threads), **arrays)
+        script = os.path.join(os.path.dirname(REF_LIB), os.pardir, "ref_run.py")
+        r = subprocess.run([sys.executable, script, src, dst], capture_output=True, text=True, timeout=timeout)
+        assert r.returncode == 0, f"reference run failed: {r.stderr[-2000:]}"
+        with np.load(dst) as f:
+            return {k: f[k] for k in f.files}

@@ -113,7 +113,7 @@ def _smorph_full(merge, B, C, H, W, K, a, x_kind, w_scale, seed):
     assert abs(total - n * C * C) / (n * C * C) <= 1e-6, f"grad_input sum: {total}"
 
 
-@pytest.mark.parametrize("a", [1.0, -20.0])
+@pytest.mark.parametrize("a", [-20.0, -1.0, 0.0, 1.0, 20.0])
 def test_config3_full_size_smorph(a):
     """configs[2] at its full size: (8, 64, 256, 256), w~ (64, 64, 7, 7) ~N(0, 0.1), mean merge."""
     print(f"configs[2] full size, alpha {a}", flush=True)

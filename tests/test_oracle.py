@@ -536,3 +536,23 @@ def test_functional_smorph_passes_the_oracle_w_tilde(merge, alpha_shape, monkeyp
     alpha = torch.randn(alpha_shape, generator=g, dtype=torch.float64) * 2
     smod.smorph(torch.zeros(1, cw if merge != "identity" else 3, 4, 4, dtype=torch.float64), w, alpha, channel_merge_mode=merge)
     assert np.array_equal(seen["w"].numpy(), O.smorph_w_tilde(w.numpy(), alpha.numpy(), merge))
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref",
+                                                    "libmorphocore_ref.so")), reason="the reference's CPU extension is not built")
+@pytest.mark.parametrize("merge", ["mean", "max"])
+def test_reference_runner_agrees_with_the_oracle(merge):
+    """oracle/ref_run.py (the reference's own CPU extension in a child process, which the GPU tests at
+    the configs' channel counts check against) returns what the C oracle computes for the same smorph."""
+    from tests.helpers import reference_run
+
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 3, 11, 13)).astype(np.float32)
+    wt = (rng.standard_normal((4, 3, 5, 5)) * 0.1).astype(np.float32)
+    alpha = rng.uniform(-4, 4, (4, 3)).astype(np.float32)
+    g = rng.standard_normal((2, 4, 11, 13)).astype(np.float32)
+    m = O.MERGES[merge]
+    got = reference_run("smorph", x=x, wt=wt, alpha=alpha, grad=g, merge=np.array(m))
+    assert np.array_equal(got["out"], O.smorph_forward(m, x, wt, alpha))
+    for k, want in zip(("grad_input", "grad_weight", "grad_alpha"), O.smorph_backward(m, x, wt, alpha, g)):
+        assert normwise_error(got[k], want) <= 1e-6, k
