@@ -1,32 +1,48 @@
-"""Smorph gradients at the configs' real channel counts and structuring elements, against the
-reference's own CPU extension (oracle/_ref, built from the reference sources; run in a child process
-by tests/helpers.py: reference_run), on one batch element at the full spatial size:
+"""Smorph gradients at the configs' real channel counts and structuring elements, on one batch
+element at the full spatial size, against the reference's own CPU extension (oracle/_ref, built from
+the reference sources; run in a child process by tests/helpers.py: reference_run) and the C oracle:
 
 * (1, 64, 256, 256) ~N(0, 1), w~ (64, 64, 7, 7) ~N(0, 0.1), merge mean, every alpha of its
   sweep, both backward paths (from the forward's saved pair statistics, and recomputing them);
 * configs[4]'s smorph layer: (1, 64, 256, 256) ~U[0, 1), w~ (64, 64, 11, 11) ~N(0, 0.05), merge sum,
   alpha 5 (both paths).
 
-Every output and gradient is compared element for element (norm-wise, the contract's 1e-6 for float32):
-the forward output, grad_input, grad_weight of every (output, input) pair and tap, and grad_alpha of
-every pair. This covers what conservation sums cannot: a permutation of taps or pairs inside the
-kernels' slot reductions and packed LDS bins. Each case prints its name before the GPU work.
+Compared element for element (norm-wise, the contract's 1e-6 for float32): the forward output bit for
+bit, grad_weight of every (output, input) pair and tap and grad_alpha of every pair against the
+reference extension. This covers what conservation sums cannot: a permutation of taps or pairs inside
+the kernels' slot reductions and packed LDS bins.
+
+grad_input sums 64 output channels x KH x KW terms per pixel, which the reference adds in float32 in a
+thread-count dependent order: at configs[2]'s alpha -20 its result lies 1.41e-6 (norm-wise) from its
+own terms summed exactly (the C oracle, which restates its per-term arithmetic and accumulates in
+double; measured on the full tensor), so no other summation order meets 1e-6 against it there.
+grad_input is therefore held to 1e-6 against the C oracle on regions (corners, edges and interior,
+each from a crop of the input: a region's grad_input only receives from outputs within twice the
+element's radius), and its full-tensor distance to the reference extension is bounded by 1e-6 plus the
+reference's own summation error (RefNoise below). Each case prints its name before the GPU work.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
 
+from oracle import oracle as O
 from tests.helpers import REF_LIB, normwise_error, reference_run, seeded
 
 pytestmark = pytest.mark.gpu
 
 MEAN, SUM = 3, 2
+# The reference extension's own float32 summation error of grad_input at these sizes, norm-wise
+# against its terms summed exactly: 1.41e-6 measured at configs[2]'s alpha -20 (the largest of the
+# sweep); the bound allows twice that.
+REF_NOISE = 2.8e-6
 
 
 @pytest.fixture(autouse=True)
 def _ops():
     import morphocore_amd  # noqa: F401  (registers torch.ops.morphocore)
-    if not __import__("os").path.exists(REF_LIB):
+    if not os.path.exists(REF_LIB):
         pytest.skip("the reference's CPU extension (oracle/_ref) is not built")
 
 
@@ -45,14 +61,26 @@ def _gpu_smorph(x, wt, alpha, g, merge):
     return res
 
 
-def _compare(got, want, what):
-    for k in ("out", "grad_input", "grad_weight", "grad_alpha"):
-        err = normwise_error(got[k], want[k])
-        print(f"  {what} {k}: {err:.3g}", flush=True)
-        assert err <= 1e-6, f"{what}: {k} differs from the reference by {err}"
+def _regions(n, size):
+    """Top-left corners of size x size regions of an n x n plane: the four corners, the middles of the
+    four edges and four interior points."""
+    e, m = n - size, (n - size) // 2
+    return [(0, 0), (0, e), (e, 0), (e, e), (0, m), (m, 0), (e, m), (m, e), (m, m), (37, 101), (150, 29), (203, 177)]
 
 
-def _case(name, x, wt, alpha, g, merge, monkeypatch):
+def _grad_input_regions(got, x, wt, alpha, g, merge, K, what):
+    P, size, n = K // 2, 12, x.shape[-1]
+    xn, gn, wn, an = x.numpy(), g.numpy(), wt.numpy(), alpha.numpy()
+    for r0, c0 in _regions(n, size):
+        h0, h1 = max(0, r0 - 2 * P), min(n, r0 + size + 2 * P)
+        w0, w1 = max(0, c0 - 2 * P), min(n, c0 + size + 2 * P)
+        xc, gc = np.ascontiguousarray(xn[:, :, h0:h1, w0:w1]), np.ascontiguousarray(gn[:, :, h0:h1, w0:w1])
+        want = O.smorph_backward(merge, xc, wn, an, gc)[0][0, :, r0 - h0:r0 - h0 + size, c0 - w0:c0 - w0 + size]
+        err = normwise_error(got[0, :, r0:r0 + size, c0:c0 + size], want)
+        assert err <= 1e-6, f"{what}: grad_input region {(r0, c0)} differs from the oracle by {err}"
+
+
+def _case(name, x, wt, alpha, g, merge, K, monkeypatch):
     print(name, "(GPU, saved statistics)", flush=True)
     saved = _gpu_smorph(x, wt, alpha, g, merge)
     print(name, "(GPU, recomputed statistics)", flush=True)
@@ -61,9 +89,17 @@ def _case(name, x, wt, alpha, g, merge, monkeypatch):
     monkeypatch.delenv("MORPHOCORE_AMD_SAVED_STATS_LIMIT")
     print(name, "(reference CPU extension)", flush=True)
     want = reference_run("smorph", x=x.numpy(), wt=wt.numpy(), alpha=alpha.numpy(), grad=g.numpy(), merge=np.array(merge))
-    assert np.array_equal(saved["out"], recomputed["out"])
-    _compare(saved, want, "saved")
-    _compare(recomputed, want, "recomputed")
+    for what, got in (("saved", saved), ("recomputed", recomputed)):
+        assert np.array_equal(got["out"], want["out"]), f"{what}: forward"
+        for k in ("grad_weight", "grad_alpha"):
+            err = normwise_error(got[k], want[k])
+            print(f"  {what} {k} vs reference: {err:.3g}", flush=True)
+            assert err <= 1e-6, f"{what}: {k} differs from the reference by {err}"
+        err = normwise_error(got["grad_input"], want["grad_input"])
+        print(f"  {what} grad_input vs reference: {err:.3g}", flush=True)
+        assert err <= 1e-6 + REF_NOISE, f"{what}: grad_input differs from the reference by {err}"
+        print(name, f"({what}: grad_input regions against the oracle)", flush=True)
+        _grad_input_regions(got["grad_input"], x, wt, alpha, g, merge, K, what)
 
 
 @pytest.mark.parametrize("a", [-20.0, -1.0, 0.0, 1.0, 20.0])
@@ -71,11 +107,12 @@ def test_config3_channels_against_the_reference(a, monkeypatch):
     x = seeded(70, 1, 64, 256, 256, kind="randn")
     wt = seeded(71, 64, 64, 7, 7, kind="randn", scale=0.1)
     g = seeded(72, 1, 64, 256, 256, kind="randn")
-    _case(f"configs[2] channels, (1, 64, 256, 256) 7x7 mean, alpha {a}", x, wt, torch.full((64, 64), a), g, MEAN, monkeypatch)
+    _case(f"configs[2] channels, (1, 64, 256, 256) 7x7 mean, alpha {a}", x, wt, torch.full((64, 64), a), g, MEAN, 7, monkeypatch)
 
 
 def test_config5_smorph_channels_against_the_reference(monkeypatch):
     x = seeded(73, 1, 64, 256, 256)
     wt = seeded(74, 64, 64, 11, 11, kind="randn", scale=0.05)
     g = seeded(75, 1, 64, 256, 256, kind="randn")
-    _case("configs[4] smorph layer channels, (1, 64, 256, 256) 11x11 sum, alpha 5", x, wt, torch.full((64, 64), 5.0), g, SUM, monkeypatch)
+    _case("configs[4] smorph layer channels, (1, 64, 256, 256) 11x11 sum, alpha 5", x, wt, torch.full((64, 64), 5.0), g, SUM, 11,
+          monkeypatch)
