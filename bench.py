@@ -491,7 +491,7 @@ def kernel_roofline(config, cfg, which, k, kms, kn):
     roof["traffic"] = measured_traffic(key)
     roof.update({"kernel": k["what"], "phase": which, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": k["work"],
                  "work_unit": k["unit"]})
-    ceiling = instruction_ceiling(key, cfg, roof, k["executed"] if k["executed"] is not None else k["work"])
+    ceiling = instruction_ceiling(key, cfg, roof, k["work"])
     if ceiling is not None:
         roof["instruction_ceiling"] = ceiling
         roof["ceiling_frac"] = ceiling["ceiling_frac"]
