@@ -74,7 +74,7 @@ int make_geom(int merge, int64_t B, int64_t Cin, int64_t Cout, int64_t Cw, int64
 
 int check_lds(size_t bytes)
 {
-    if (bytes > mca::LDS_LIMIT) return fail("Structuring element too large for the kernels' shared memory");
+    if (bytes > mca::device_lds_limit()) return fail("Structuring element too large for the kernels' shared memory");
     return MCA_OK;
 }
 
@@ -147,7 +147,7 @@ size_t smorph_workspace_impl(int merge, int64_t B, int64_t Cin, int64_t Cout, in
 {
     mca::Geom g{};
     if (make_geom(merge, B, Cin, Cout, Cw, H, W, KH, KW, 0, g) != MCA_OK) return 0;
-    if (mca::smorph_lds<T>(merge, g, true) > mca::LDS_LIMIT) return 0;  // no backward for this element
+    if (mca::smorph_lds<T>(merge, g, true) > mca::device_lds_limit()) return 0;  // no backward for this element
     return mca::smorph_backward_workspace<T>(merge, g);
 }
 
@@ -190,7 +190,7 @@ size_t scm_backward_workspace_impl(int64_t B, int64_t Cin, int64_t Cout, int64_t
 {
     mca::Geom g{};
     if (make_scm_geom(B, Cin, Cout, Cw, H, W, KH, KW, g) != MCA_OK) return 0;
-    if (mca::smorph_scm_lds<T>(g, true) > mca::LDS_LIMIT) return 0;
+    if (mca::smorph_scm_lds<T>(g, true) > mca::device_lds_limit()) return 0;
     return mca::smorph_scm_backward_workspace<T>(g);
 }
 

@@ -24,8 +24,14 @@ constexpr int rows_per_wave()
     return sizeof(T) == 8 ? 4 : 8;
 }
 
-// Largest LDS allocation a launch may request (bytes).
+// LDS the tuned launch plans budget for one workgroup (bytes): what leaves room for two or more
+// workgroups per CU. A plan exceeds it only for elements that fit nothing smaller.
 constexpr size_t LDS_LIMIT = 64 * 1024;
+
+// LDS one workgroup may allocate on the current device (bytes): the device's per-workgroup maximum
+// (hipDeviceAttributeMaxSharedMemoryPerBlock, queried once per device). A launch needing more cannot
+// run; the entry points reject such elements with an error.
+size_t device_lds_limit();
 
 // Saved winners of the forward pass ("indices"):
 //   MAX / MIN merges: int32 (channel << 16) | tap per output pixel, [B, Cout, H, W];
@@ -49,7 +55,8 @@ template <typename ST>
 hipError_t morpho_forward(int op, int merge, bool replicate, compute_t<ST> fill, const ST* x, const ST* w, ST* out, void* indices,
                           const Geom& g, hipStream_t stream);
 
-// Bytes of LDS the forward kernel needs; > LDS_LIMIT means the structuring element is too large.
+// Bytes of LDS the forward kernel needs; more than device_lds_limit() means the structuring element is
+// too large.
 template <typename ST>
 size_t morpho_forward_lds(const Geom& g);
 

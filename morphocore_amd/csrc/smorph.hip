@@ -183,7 +183,9 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
     }
 }
 
-template <typename T, int MK, int RH>
+// GGIN: grad_input is summed in global memory (p.gacc, double atomics per routed tap) instead of an LDS
+// copy of the tile flushed per tile: for elements whose tile and its double copy exceed the LDS.
+template <typename T, int MK, int RH, bool GGIN = false>
 __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams<T> p)
 {
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
     const int nb = K + (MK == MK_SMOOTH ? 2 : 1);
     T* tile = reinterpret_cast<T*>(smem_raw);
     Acc* gtile = reinterpret_cast<Acc*>(smem_raw + align16((size_t)tile_elems * sizeof(T)));
-    Acc* bins = gtile + tile_elems;
+    Acc* bins = GGIN ? gtile : gtile + tile_elems;
     Acc* abins = bins + K * p.ncopy;
     Acc* bbins = abins + p.ncopy;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -226,8 +228,10 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
         const int iy0 = h0 + wave * RH + ph, ix = wc + pw;
         __syncthreads();
         stage_tile(tile, p.x + ((int64_t)b * g.Cin + i) * plane, g, t, y0, x0, false, T(0));
-        for (int j = threadIdx.x; j < tile_elems; j += BLOCK) gtile[j] = Acc(0);
+        if constexpr (!GGIN)
+            for (int j = threadIdx.x; j < tile_elems; j += BLOCK) gtile[j] = Acc(0);
         __syncthreads();
+        Acc* __restrict__ gacc_plane = GGIN ? p.gacc + ((int64_t)b * g.Cin + i) * plane : nullptr;
 
         const int o_begin = MK == MK_IDENT ? i : 0;
         const int o_end = MK == MK_IDENT ? i + 1 : g.Cout;
@@ -299,7 +303,10 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
                         // c = pg (1 + a centered) and the alpha term pg (v - ref) centered share pg centered.
                         const T q = pg * centered;
                         const T c = fma(a, q, pg);
-                        lds_add(&gtile[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)c);
+                        if constexpr (GGIN)
+                            global_add(&gacc_plane[(int64_t)(iy0 + r - kh) * g.W + (ix - kw)], (Acc)c);
+                        else
+                            lds_add(&gtile[(wave * RH + r + g.KH - 1 - kh) * t.pitch + lane + g.KW - 1 - kw], (Acc)c);
                         lds_add(&bins[k * p.ncopy + copy], (Acc)c);
                         asum[r] = fma(q, v - ref[r], asum[r]);
                     }
@@ -329,6 +336,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams
             __syncthreads();
         }
 
+        if constexpr (GGIN) continue;  // nothing staged: grad_input is already in global memory
         T* gplane = p.gin + ((int64_t)b * g.Cin + i) * plane;
         for (int ly = wave; ly < t.rows; ly += NWAVES)
         {
@@ -441,9 +449,19 @@ struct SmorphBwdPlan
     int tps;
     int ncopy;
     int npairs;
-    size_t part_w_bytes, part_a_bytes, part_b_bytes, counts_bytes;
+    bool ggin;  // generic kernel with grad_input summed in global memory (smorph_bwd_kernel<..., true>)
+    size_t part_w_bytes, part_a_bytes, part_b_bytes, counts_bytes, gacc_bytes;
     size_t lds;
 };
+
+// Rows per wave of the generic forward: the default while its tile fits the tuned LDS budget, else one
+// (a shorter tile, for large elements).
+template <typename T>
+static int smorph_fwd_rh(const Geom& g)
+{
+    const Tiling t = make_tiling(g, rows_per_wave<T>());
+    return (size_t)t.rows * t.pitch * sizeof(T) <= LDS_LIMIT ? rows_per_wave<T>() : 1;
+}
 
 // `saved`: the backward from saved statistics, whose static kernel takes two output rows per wave.
 // Its tiles are taller, but the rounding of tiles per strip can still give it more strips (slots)
@@ -455,8 +473,36 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     // The static kernels (smorph_static.hip) use one output row per wave (two from saved statistics)
     // and static LDS.
     const bool stat = smorph_static_supported<T>(g);
-    s.t = make_tiling(g, stat ? (saved ? 2 : 1) : rows_per_wave<T>());
+    int rh = stat ? (saved ? 2 : 1) : rows_per_wave<T>();
     s.ncopy = 16;
+    if (!stat)
+    {
+        // The generic kernel: tile, its double grad_input copy, and ncopy copies of the bins (K taps,
+        // alpha, beta for SMOOTH). The first of these that fits: the default rows per wave, then one
+        // row per wave (a shorter tile), within the tuned budget, then within the device's LDS, then
+        // grad_input summed in global memory (no copy of the tile); each with as many bin copies as
+        // fit (fewer copies: more same-address LDS adds).
+        const size_t nbins = (size_t)g.taps() + (merge == MERGE_SMOOTH ? 2 : 1);
+        const size_t dev = device_lds_limit();
+        const size_t budgets[2] = {LDS_LIMIT < dev ? LDS_LIMIT : dev, dev};
+        bool fit = false;
+        for (int attempt = 0; attempt < 5 && !fit; ++attempt)
+        {
+            const size_t budget = budgets[attempt < 2 ? 0 : 1];
+            const bool ggin = attempt == 4;
+            rh = (attempt == 0 || attempt == 2) ? rows_per_wave<T>() : 1;
+            const Tiling t = make_tiling(g, rh);
+            const size_t cells = (size_t)t.rows * t.pitch;
+            const size_t fixed = align16(cells * sizeof(T)) + (ggin ? 0 : cells * sizeof(Acc));
+            int ncopy = 16;
+            while (ncopy > 1 && fixed + nbins * ncopy * sizeof(Acc) > budget) ncopy /= 2;
+            s.ncopy = ncopy;
+            s.ggin = ggin;
+            s.lds = fixed + nbins * ncopy * sizeof(Acc);
+            fit = s.lds <= budget;
+        }
+    }
+    s.t = make_tiling(g, rh);
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
     const int64_t units = (int64_t)g.B * g.Cin;
     const int ntiles = s.t.ntiles();
@@ -474,18 +520,9 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     s.part_b_bytes = merge == MERGE_SMOOTH ? s.part_a_bytes : 0;
     // MAX / MIN: winner counts, then the merge target, per output pixel.
     s.counts_bytes = (merge == MERGE_MAX || merge == MERGE_MIN) ? 2 * (size_t)g.B * g.Cout * g.plane() * sizeof(T) : 0;
-    if (stat)
-    {
-        s.lds = 0;  // static LDS
-        return s;
-    }
-    // The generic kernel: tile, its double grad_input copy, and ncopy copies of the bins (K taps,
-    // alpha, beta for SMOOTH); fewer copies (more same-address LDS adds) when a large element would
-    // not fit otherwise.
-    const size_t fixed = align16((size_t)s.t.rows * s.t.pitch * sizeof(T)) + (size_t)s.t.rows * s.t.pitch * sizeof(Acc);
-    const size_t nbins = (size_t)g.taps() + (merge == MERGE_SMOOTH ? 2 : 1);
-    while (s.ncopy > 1 && fixed + nbins * s.ncopy * sizeof(Acc) > LDS_LIMIT) s.ncopy /= 2;
-    s.lds = fixed + nbins * s.ncopy * sizeof(Acc);
+    // grad_input summed in global memory: a double buffer, rounded into grad_input afterwards (float
+    // tensors; double ones sum into grad_input itself).
+    s.gacc_bytes = (s.ggin && sizeof(T) != sizeof(Acc)) ? (size_t)g.B * g.Cin * g.plane() * sizeof(Acc) : 0;
     return s;
 }
 
@@ -494,7 +531,7 @@ size_t smorph_lds(int merge, const Geom& g, bool backward)
 {
     if (backward) return plan_smorph_bwd<T>(merge, g).lds;
     if (smorph_static_supported<T>(g)) return 0;  // static LDS
-    const Tiling t = make_tiling(g, rows_per_wave<T>());
+    const Tiling t = make_tiling(g, smorph_fwd_rh<T>(g));
     return (size_t)t.rows * t.pitch * sizeof(T);
 }
 
@@ -508,7 +545,7 @@ static size_t smorph_plan_workspace(const SmorphBwdPlan& s, const Geom& g)
     // SMOOTH: grad_beta sums nslots * Cin partial rows of Cout values.
     const size_t red_b = s.part_b_bytes ? reduce_slots_scratch<T>(nslots * g.Cin, g.Cout) : 0;
     return align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes) + align_up(s.counts_bytes) +
-           align_up(red > red_b ? red : red_b);
+           align_up(red > red_b ? red : red_b) + align_up(s.gacc_bytes);
 }
 
 // Enough for either backward (recomputing or from saved statistics): the caller sizes the workspace
@@ -521,6 +558,50 @@ size_t smorph_backward_workspace(int merge, const Geom& g)
     return a > b ? a : b;
 }
 
+// The generic backward kernel of a plan: the default rows per wave or one, grad_input summed in an LDS
+// copy of the tile or in global memory.
+template <typename T, int MK>
+static hipError_t launch_smorph_bwd_generic(const SmorphBwdPlan& s, const SmorphBwdParams<T>& p, hipStream_t stream)
+{
+    constexpr int RH = rows_per_wave<T>();
+    const unsigned blocks = (unsigned)((int64_t)p.g.B * p.g.Cin * s.nstrips);
+    if (s.ggin)
+        smorph_bwd_kernel<T, MK, 1, true><<<blocks, BLOCK, s.lds, stream>>>(p);
+    else if (s.t.rh == 1)
+        smorph_bwd_kernel<T, MK, 1, false><<<blocks, BLOCK, s.lds, stream>>>(p);
+    else
+        smorph_bwd_kernel<T, MK, RH, false><<<blocks, BLOCK, s.lds, stream>>>(p);
+    return hipGetLastError();
+}
+
+// Where the global-memory grad_input sum of a plan goes: grad_input itself for double tensors, the
+// workspace buffer (zero-filled here, rounded into grad_input by finish_gacc) for float ones; null
+// when the plan sums it in LDS.
+template <typename T>
+static hipError_t prepare_gacc(const SmorphBwdPlan& s, const Geom& g, T* grad_in, Acc* buffer, Acc** gacc, hipStream_t stream)
+{
+    *gacc = nullptr;
+    if (!s.ggin) return hipSuccess;
+    if constexpr (sizeof(T) == sizeof(Acc))
+    {
+        *gacc = reinterpret_cast<Acc*>(grad_in);  // zero-filled by the caller
+        return hipSuccess;
+    }
+    else
+    {
+        *gacc = buffer;
+        return fill_async<Acc>(buffer, (int64_t)g.B * g.Cin * g.plane(), Acc(0), stream);
+    }
+}
+
+template <typename T>
+static hipError_t finish_gacc(const SmorphBwdPlan& s, const Geom& g, const Acc* buffer, T* grad_in, hipStream_t stream)
+{
+    if constexpr (sizeof(T) != sizeof(Acc))
+        if (s.ggin) return round_async<T>(buffer, grad_in, (int64_t)g.B * g.Cin * g.plane(), stream);
+    return hipSuccess;
+}
+
 template <typename T, int MK, bool STATS>
 static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t stream)
 {
@@ -529,7 +610,10 @@ static hipError_t launch_smorph_fwd(const SmorphFwdParams<T>& p, hipStream_t str
     constexpr int RH = rows_per_wave<T>();
     const int64_t blocks = (int64_t)p.g.B * p.t.nty * p.t.ntx * p.g.Cout;
     const size_t lds = (size_t)p.t.rows * p.t.pitch * sizeof(T);
-    smorph_fwd_kernel<T, MK, RH, STATS><<<(unsigned)blocks, BLOCK, lds, stream>>>(p);
+    if (p.t.rh == 1)
+        smorph_fwd_kernel<T, MK, 1, STATS><<<(unsigned)blocks, BLOCK, lds, stream>>>(p);
+    else
+        smorph_fwd_kernel<T, MK, RH, STATS><<<(unsigned)blocks, BLOCK, lds, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -552,7 +636,7 @@ hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* 
     p.nstat = smorph_stats_count<T>(merge, g);
     p.g = g;
     // The static kernels (smorph_static.hip) put one output row on each wave.
-    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
+    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : smorph_fwd_rh<T>(g));
     p.average = merge == MERGE_AVERAGE;
     switch (merge)
     {
@@ -588,7 +672,9 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     T* part_a = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes));
     T* counts = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
     T* target = counts + (int64_t)g.B * g.Cout * g.plane();
-    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes));
+    Acc* gbuf = reinterpret_cast<Acc*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes));
+    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.counts_bytes) +
+                                      align_up(s.gacc_bytes));
     const int nslots = g.B * s.nstrips;
     // The static kernels that keep their partials in LDS store every slot entry themselves.
     if (!(smorph_static_supported<T>(g) && smorph_bwd_lds_partials(g, merge == MERGE_IDENTITY)))
@@ -612,7 +698,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
         f.tout = target;
         f.target = out;
         f.g = g;
-        f.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
+        f.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : smorph_fwd_rh<T>(g));
         f.average = 0;
         err = merge == MERGE_MAX ? launch_smorph_fwd<T, MK_MAX, true>(f, stream) : launch_smorph_fwd<T, MK_MIN, true>(f, stream);
         if (err != hipSuccess) return err;
@@ -649,18 +735,20 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
             return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
         }
     }
-    constexpr int RH = rows_per_wave<T>();
-    const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
+    Acc* gacc = nullptr;
+    if ((err = prepare_gacc<T>(s, g, grad_in, gbuf, &gacc, stream)) != hipSuccess) return err;
+    p.gacc = gacc;
     switch (merge)
     {
         case MERGE_ADD:
-        case MERGE_AVERAGE: smorph_bwd_kernel<T, MK_SUM, RH><<<blocks, BLOCK, s.lds, stream>>>(p); break;
-        case MERGE_MAX: smorph_bwd_kernel<T, MK_MAX, RH><<<blocks, BLOCK, s.lds, stream>>>(p); break;
-        case MERGE_MIN: smorph_bwd_kernel<T, MK_MIN, RH><<<blocks, BLOCK, s.lds, stream>>>(p); break;
-        case MERGE_IDENTITY: smorph_bwd_kernel<T, MK_IDENT, RH><<<blocks, BLOCK, s.lds, stream>>>(p); break;
+        case MERGE_AVERAGE: err = launch_smorph_bwd_generic<T, MK_SUM>(s, p, stream); break;
+        case MERGE_MAX: err = launch_smorph_bwd_generic<T, MK_MAX>(s, p, stream); break;
+        case MERGE_MIN: err = launch_smorph_bwd_generic<T, MK_MIN>(s, p, stream); break;
+        case MERGE_IDENTITY: err = launch_smorph_bwd_generic<T, MK_IDENT>(s, p, stream); break;
         default: return hipErrorInvalidValue;
     }
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (err != hipSuccess) return err;
+    if ((err = finish_gacc<T>(s, g, gbuf, grad_in, stream)) != hipSuccess) return err;
     if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
     return reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream);
 }
@@ -704,7 +792,8 @@ template <typename T>
 size_t smorph_scm_lds(const Geom& g, bool backward)
 {
     if (backward) return plan_smorph_bwd<T>(MERGE_SMOOTH, g).lds;
-    const Tiling t = make_tiling(g, rows_per_wave<T>());
+    if (smorph_static_supported<T>(g)) return 0;  // static LDS
+    const Tiling t = make_tiling(g, smorph_fwd_rh<T>(g));
     return (size_t)t.rows * t.pitch * sizeof(T);
 }
 
@@ -735,7 +824,7 @@ hipError_t smorph_scm_forward(const T* x, const T* w, const T* alpha, const T* b
     }
     p.pout = pstats ? reinterpret_cast<T*>(pstats + 2 * p.nstat) : reinterpret_cast<T*>(workspace);
     // The float32 static kernels (one row per wave) write the pair outputs where they exist.
-    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : rows_per_wave<T>());
+    p.t = make_tiling(g, smorph_static_supported<T>(g) ? 1 : smorph_fwd_rh<T>(g));
     hipError_t err = launch_smorph_fwd<T, MK_SMOOTH, false>(p, stream);
     if (err != hipSuccess) return err;
     if (sizeof(T) == 4 && g.Cin <= 16)
@@ -770,7 +859,9 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     T* part_w = reinterpret_cast<T*>(ws);
     T* part_a = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes));
     T* part_b = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes));
-    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes));
+    Acc* gbuf = reinterpret_cast<Acc*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes));
+    T* scratch = reinterpret_cast<T*>(ws + align_up(s.part_w_bytes) + align_up(s.part_a_bytes) + align_up(s.part_b_bytes) +
+                                      align_up(s.gacc_bytes));
     const int nslots = g.B * s.nstrips;
     const bool stat = smorph_static_supported<T>(g);
     // The static kernel that keeps its partials in LDS stores every slot entry itself.
@@ -813,10 +904,11 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
         }
     if (!launched)
     {
-        constexpr int RH = rows_per_wave<T>();
-        const unsigned blocks = (unsigned)((int64_t)g.B * g.Cin * s.nstrips);
-        smorph_bwd_kernel<T, MK_SMOOTH, RH><<<blocks, BLOCK, s.lds, stream>>>(p);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        Acc* gacc = nullptr;
+        if ((err = prepare_gacc<T>(s, g, grad_in, gbuf, &gacc, stream)) != hipSuccess) return err;
+        p.gacc = gacc;
+        if ((err = launch_smorph_bwd_generic<T, MK_SMOOTH>(s, p, stream)) != hipSuccess) return err;
+        if ((err = finish_gacc<T>(s, g, gbuf, grad_in, stream)) != hipSuccess) return err;
     }
     if ((err = reduce_slots_async<T>(part_w, nslots, wnumel, grad_w, scratch, stream)) != hipSuccess) return err;
     if ((err = reduce_slots_async<T>(part_a, nslots, s.npairs, grad_alpha, scratch, stream)) != hipSuccess) return err;

@@ -198,6 +198,9 @@ struct SmorphBwdParams
     T* __restrict__ part_a;
     const float* __restrict__ pstats;  // the forward's saved pair statistics, or null (recomputed)
     int64_t nstat;
+    // Generic kernel for elements whose tile and grad_input copy exceed the LDS: grad_input summed in
+    // global memory, [B, Cin, H, W] double (grad_input itself for double tensors), else null.
+    Acc* __restrict__ gacc;
     // SMOOTH merge (smorph_scm): beta per output channel, the forward's soft-merge statistics (ref,
     // then 1 / sum, [B, Cout, H, W] each; `out` holds the merged output), and the grad_beta partials
     // [slot][Cin][Cout].

@@ -1,6 +1,8 @@
 // Small helper kernels shared by the launchers: fill (zeroing accumulators without hipMemsetAsync,
 // so that the launches stay valid under stream capture) and the fixed-order sum of per-workgroup
 // partial slots.
+#include <atomic>
+
 #include "launch.hpp"
 
 namespace mca
@@ -105,6 +107,23 @@ hipError_t reduce_slots_async(const T* part, int nslots, int64_t n, T* out, T* s
     reduce_groups_kernel<T><<<grid, BLOCK, 0, stream>>>(part, nslots, n, scratch);
     reduce_slots_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(scratch, groups, n, out);
     return hipGetLastError();
+}
+
+size_t device_lds_limit()
+{
+    constexpr int MAX_DEVICES = 64;
+    static std::atomic<int64_t> cached[MAX_DEVICES] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return LDS_LIMIT;
+    if (dev < MAX_DEVICES)
+    {
+        const int64_t c = cached[dev].load(std::memory_order_relaxed);
+        if (c > 0) return (size_t)c;
+    }
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) return LDS_LIMIT;
+    if (dev < MAX_DEVICES) cached[dev].store(v, std::memory_order_relaxed);
+    return (size_t)v;
 }
 
 template <typename T>

@@ -97,3 +97,44 @@ def test_smorph_static_forward_bit_exact(K, merge):
                 out = torch.ops.morphocore.smorph(xin.cuda(), w.cuda(), alpha.cuda(), O.MERGES[merge]).cpu().numpy()
             ref = O.smorph_forward(O.MERGES[merge], xin.numpy(), w.numpy(), alpha.numpy())
             assert np.array_equal(out, ref, equal_nan=True), (alphas, float(np.nanmax(np.abs(out - ref))))
+
+
+@pytest.mark.parametrize("merge", ["mean", "max", "identity"])
+@pytest.mark.parametrize("dtype,K,shape", [(torch.float32, 31, (2, 3, 4, 40, 70)), (torch.float64, 31, (2, 3, 4, 40, 70)),
+                                           (torch.float64, 41, (1, 2, 3, 30, 70)), (torch.float32, 101, (1, 2, 2, 24, 30))],
+                         ids=["f32-31", "f64-31", "f64-41", "f32-101"])
+def test_smorph_large_elements(dtype, K, shape, merge):
+    """Elements whose default tile, its grad_input copy and bins exceed the LDS budget train as in the
+    reference's CPU path, which takes any size (smorph_cpu_kernels.hxx:30-147,387-638): the backward
+    takes one row per wave, then the device's whole LDS, then grad_input summed in global memory
+    (31x31, 41x41 and 101x101 land on these in turn), with a non-zero workspace; forward and every
+    gradient against the oracle."""
+    from morphocore_amd import _native
+
+    B, Cin, Cout, H, W = shape
+    if merge == "identity":
+        Cout = Cin
+    print(f"smorph {K}x{K} {merge} {dtype} (device LDS per workgroup: "
+          f"{torch.cuda.get_device_properties(0).shared_memory_per_block} bytes)", flush=True)
+    x = seeded(150, B, Cin, H, W, dtype=dtype, kind="randn")
+    w = seeded(151, *_weight_shape(merge, Cin, Cout, K, K), dtype=dtype, kind="randn", scale=0.1)
+    g = seeded(152, B, Cout, H, W, dtype=dtype, kind="randn")
+    size = getattr(_native.lib(), f"mca_smorph_backward_workspace_size_{'f32' if dtype == torch.float32 else 'f64'}")
+    assert size(O.MERGES[merge], B, Cin, Cout, w.shape[1], H, W, K, K) > 0
+    for actual, expected in _smorph_case(merge, x, w, _alpha(merge, Cin, Cout, 3.0, dtype, 153), g):
+        assert normwise_error(actual, expected) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_smorph_scm_large_element(dtype):
+    """The SMOOTH merge (smorph_scm) with a 31x31 element: forward and every gradient against the oracle."""
+    from tests.test_gpu_scm import _check
+
+    B, C, H, W, K = 1, 3, 36, 70, 31
+    print(f"smorph_scm {K}x{K} {dtype}", flush=True)
+    x = seeded(154, B, C, H, W, dtype=dtype, kind="randn")
+    w = seeded(155, C, C, K, K, dtype=dtype, kind="randn", scale=0.1)
+    alpha = _alpha("sum", C, C, 2.0, dtype, 156)
+    beta = torch.tensor([1.5, -2.0, 0.0], dtype=dtype)
+    g = seeded(157, B, C, H, W, dtype=dtype, kind="randn")
+    _check(x, w, alpha, beta, g)

@@ -246,3 +246,18 @@ def test_sigma_rejects_bad_arguments():
 def test_rejects_planes_beyond_32_bit_offsets():
     assert _forward(2, (1, 1, 1, 1, 65536, 32768, 3, 3)) == 1
     assert "2^31 - 1 pixels" in _native.lib().mca_last_error().decode()
+
+
+@pytest.mark.parametrize("merge", [0, 2, 3, 5])
+def test_smorph_backward_takes_large_elements(merge):
+    """A 31x31 smorph element has a backward (a non-zero workspace) in float32 and float64, also for the
+    SMOOTH merge, even within the smallest per-workgroup LDS a device may report (64 KiB: the value
+    assumed without a device): the generic kernel takes one output row per wave there. The reference's
+    CPU path takes any size (smorph_cpu_kernels.hxx:30-147)."""
+    lib = _native.lib()
+    B, C, H, W, K = 2, 3, 40, 70, 31
+    cw = 1 if merge == 5 else C
+    assert lib.mca_smorph_backward_workspace_size_f32(merge, B, C, C, cw, H, W, K, K) > 0
+    assert lib.mca_smorph_backward_workspace_size_f64(merge, B, C, C, cw, H, W, K, K) > 0
+    assert lib.mca_smorph_scm_backward_workspace_size_f32(B, C, C, C, H, W, K, K) > 0
+    assert lib.mca_smorph_scm_backward_workspace_size_f64(B, C, C, C, H, W, K, K) > 0
