@@ -116,6 +116,26 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
                                T* grad_in, T* grad_w, T* grad_alpha, T* grad_beta, const Geom& g, void* workspace, size_t workspace_bytes,
                                hipStream_t stream, const float* pstats = nullptr);
 
+// Streaming kernels of the IDENTITY merge for 3x3 / 5x5 elements over bands of whole rows
+// (morpho_ident.hip). ident_bands: R rows per band (0: the shape has no such kernels: planes whose
+// width is not a multiple of 8, other elements, or bands too wide for the LDS), the bands per plane
+// and one workgroup's LDS (elem_bytes: the gradients' storage type for the backward).
+struct IdentBands
+{
+    int R, nbands;
+    size_t lds;
+};
+IdentBands ident_bands(const Geom& g, size_t elem_bytes, bool backward);
+// Forward (float / double): out and, when taps is not null, the first extremal tap of every pixel.
+// Pointers 16-byte aligned (taps: 8-byte).
+template <typename ST>
+hipError_t ident_band_forward(int op, bool replicate, ST fill, const ST* x, const ST* w, ST* out, uint8_t* taps, const Geom& g,
+                              hipStream_t stream);
+// Backward from the saved taps: grad_input, and grad_weight's sums per (batch element, band) in
+// part ([B * nbands][Cout][KH * KW], T: double for double storage, else float).
+template <typename T, typename ST>
+hipError_t ident_band_backward(int op, const uint8_t* taps, const ST* grad_out, ST* grad_in, T* part, const Geom& g, hipStream_t stream);
+
 // Opening / closing with IDENTITY merges fused into one pass (morpho_fused.hip). g: Cin == Cout == C,
 // Cw == 1; first_op: the first stage's op.
 bool morpho_pair_supported(const Geom& g);

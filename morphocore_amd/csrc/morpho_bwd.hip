@@ -698,12 +698,14 @@ struct TapsPlan
     int ig, nig, oc, ncopy;
     bool planes;  // morpho_bwd_planes_kernel
     bool gather;  // morpho_bwd_ident_gather_kernel (else morpho_bwd_taps_kernel)
+    bool band;    // gathered by ident_band_gather (morpho_ident.hip): slots per (batch element, band)
     size_t part_bytes;
     size_t lds;
 };
 
+// band_ok: the row-band gather may run (its pointers are aligned; see ident_band_backward).
 template <typename T>
-static TapsPlan plan_taps(int merge, const Geom& g)
+static TapsPlan plan_taps(int merge, const Geom& g, bool band_ok = true)
 {
     TapsPlan s{};
     s.t = make_tiling(g, rows_per_wave<T>());
@@ -717,6 +719,25 @@ static TapsPlan plan_taps(int merge, const Geom& g)
     s.part_bytes = (size_t)g.B * s.t.ntiles() * g.Cout * g.Cw * K * sizeof(T);
     if (ident && g.KH == g.KW && (g.KH == 3 || g.KH == 5))
     {
+        const IdentBands bands = band_ok ? ident_bands(g, sizeof(T), true) : IdentBands{0, 0, 0};
+        if (bands.R > 0)
+        {
+            // Bands of whole rows, one (batch element, channel, band) per workgroup; the tiling's
+            // "tiles" are the bands (one partial slot each per batch element).
+            s.t = make_tiling(g, 1);
+            s.t.th = bands.R;
+            s.t.ntx = 1;
+            s.t.nty = bands.nbands;
+            s.gather = true;
+            s.band = true;
+            s.ig = 1;
+            s.nig = 1;
+            s.oc = 1;
+            s.ncopy = 1;
+            s.part_bytes = (size_t)g.B * bands.nbands * g.Cout * g.Cw * K * sizeof(T);
+            s.lds = bands.lds;
+            return s;
+        }
         // 4 rows per wave for every dtype: 16-row tiles (float32 / 16-bit gathers 18-26% faster than
         // with 8 rows, measured at configs[3]'s shape).
         s.t = make_tiling(g, GATHER_RH);
@@ -787,7 +808,7 @@ size_t morpho_backward_lds(int merge, const Geom& g)
 
 // Partial slots of grad_weight (one per workgroup that writes them) and their count.
 template <typename T>
-static void partials(int merge, const Geom& g, size_t& part_bytes, int& nslots)
+static void partials(int merge, const Geom& g, size_t& part_bytes, int& nslots, bool band_ok = true)
 {
     if (packed_winners(merge))
     {
@@ -797,10 +818,29 @@ static void partials(int merge, const Geom& g, size_t& part_bytes, int& nslots)
     }
     else
     {
-        const TapsPlan s = plan_taps<T>(merge, g);
+        const TapsPlan s = plan_taps<T>(merge, g, band_ok);
         part_bytes = s.part_bytes;
         nslots = g.B * s.t.ntiles();
     }
+}
+
+// The larger partial slots of the two plans an IDENTITY gather may take (the row-band one, or the
+// tiled one when its pointers are not aligned): the workspace is sized before the pointers are known.
+template <typename T>
+static void partials_bound(int merge, const Geom& g, size_t& part_bytes, int& nslots)
+{
+    size_t b2;
+    int n2;
+    partials<T>(merge, g, part_bytes, nslots, true);
+    partials<T>(merge, g, b2, n2, false);
+    part_bytes = std::max(part_bytes, b2);
+    nslots = std::max(nslots, n2);
+}
+
+// Whether the row-band gather may take these buffers: 16-byte aligned gradients, 8-byte aligned taps.
+static bool band_aligned(const void* grad_out, const void* grad_in, const void* taps)
+{
+    return ((uintptr_t)grad_out | (uintptr_t)grad_in) % 16 == 0 && (uintptr_t)taps % 8 == 0;
 }
 
 // When the forward kept no per-pair taps (sum / mean / identity), the backward recomputes them for
@@ -831,7 +871,7 @@ size_t morpho_backward_workspace(int merge, bool has_indices, const Geom& g)
 {
     size_t part_bytes;
     int nslots;
-    partials<T>(merge, g, part_bytes, nslots);
+    partials_bound<T>(merge, g, part_bytes, nslots);
     size_t bytes = align_up(part_bytes) + align_up(reduce_slots_scratch<T>(nslots, (int64_t)g.Cout * g.Cw * g.taps()));
     if (!has_indices)
     {
@@ -852,8 +892,10 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     const bool packed = packed_winners(merge);
     const bool nonempty = (int64_t)g.B * g.Cout * g.plane() > 0;
+    // Recomputed taps live in the workspace (256-byte aligned).
+    const bool band_ok = band_aligned(grad_out, grad_in, indices);
     // The gather kernels write every grad_input pixel themselves; the others accumulate onto zeros.
-    const bool gather = nonempty && (packed ? plan_packed<T>(g).gather : plan_taps<T>(merge, g).gather);
+    const bool gather = nonempty && (packed ? plan_packed<T>(g).gather : plan_taps<T>(merge, g, band_ok).gather);
     const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
     // float32 max / min round their double grad_input accumulator into every pixel at the end.
     const bool rounded = packed && sizeof(T) != sizeof(Acc) && nonempty;
@@ -863,7 +905,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
 
     size_t part_bytes;
     int nslots;
-    partials<T>(merge, g, part_bytes, nslots);
+    partials<T>(merge, g, part_bytes, nslots, band_ok);
     T* part = reinterpret_cast<T*>(ws);
     ws += align_up(part_bytes);
     T* scratch = reinterpret_cast<T*>(ws);
@@ -913,7 +955,7 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         return reduce_slots_async<T>(part, nslots, wnumel, grad_w, scratch, stream);
     }
 
-    const TapsPlan s = plan_taps<T>(merge, g);
+    const TapsPlan s = plan_taps<T>(merge, g, band_ok);
     // Without saved taps, batch chunks: each chunk's taps recomputed into the workspace, then routed
     // into its own grad_input rows and partial slots (slots are per batch element and tile).
     const int chunk = indices ? g.B : recompute_batch<T>(merge, g);
@@ -954,7 +996,12 @@ static hipError_t backward_op(int merge, bool replicate, T fill, const T* x, con
         constexpr int RH = rows_per_wave<T>();
         const unsigned blocks = (unsigned)((int64_t)gc.B * s.t.ntiles() * s.nig);
         const bool wide = pair_tap_bytes(g) == 2;
-        if (s.gather)
+        if (s.band)
+        {
+            if ((err = ident_band_backward<T, T>(OP, static_cast<const uint8_t*>(taps), p.gout, p.gin, p.part, gc, stream)) != hipSuccess)
+                return err;
+        }
+        else if (s.gather)
         {
             switch (g.KH)
             {
@@ -1038,9 +1085,10 @@ static hipError_t half_direct(int merge, const void* indices, const ST* grad_out
 {
     hipError_t err;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
+    const bool band_ok = band_aligned(grad_out, grad_in, indices);
     size_t part_bytes;
     int nslots;
-    partials<float>(merge, g, part_bytes, nslots);
+    partials<float>(merge, g, part_bytes, nslots, band_ok);
     float* part = reinterpret_cast<float*>(ws);
     ws += align_up(part_bytes);
     float* scratch = reinterpret_cast<float*>(ws);
@@ -1072,7 +1120,15 @@ static hipError_t half_direct(int merge, const void* indices, const ST* grad_out
     }
     else
     {
-        const TapsPlan s = plan_taps<float>(merge, g);
+        const TapsPlan s = plan_taps<float>(merge, g, band_ok);
+        if (s.band)
+        {
+            if ((err = ident_band_backward<float, ST>(OP, static_cast<const uint8_t*>(indices), grad_out, grad_in, part, g, stream)) !=
+                hipSuccess)
+                return err;
+            if ((err = reduce_slots_async<float>(part, nslots, wnumel, gw, scratch, stream)) != hipSuccess) return err;
+            return convert_async<float, ST>(gw, grad_w, wnumel, stream);
+        }
         TapsParams<float, ST> p{};
         p.taps = indices;
         p.gout = grad_out;

@@ -18,6 +18,8 @@
 // generic kernel (morpho_fwd_generic) takes any size at runtime.
 #pragma once
 
+#include <type_traits>
+
 #include "launch.hpp"
 
 namespace mca
@@ -731,6 +733,14 @@ static hipError_t forward_op(int merge, FwdParams<ST> p, hipStream_t stream)
             if (save) return group4 ? launch_fwd<ST, OP, MK_MIN, 4, FWD_PACKED>(p, stream) : launch_fwd<ST, OP, MK_MIN, 1, FWD_PACKED>(p, stream);
             return group4 ? launch_fwd<ST, OP, MK_MIN, 4, FWD_VALUE>(p, stream) : launch_fwd<ST, OP, MK_MIN, 1, FWD_VALUE>(p, stream);
         case MERGE_IDENTITY:
+            // 3x3 / 5x5 planes whose width is a multiple of 8: the streaming row-band kernels (float32 /
+            // float64; the 16-bit tiles keep their border value in float32).
+            if constexpr (std::is_same_v<ST, float> || std::is_same_v<ST, double>)
+            {
+                const bool aligned = ((uintptr_t)p.x | (uintptr_t)p.out) % 16 == 0 && (uintptr_t)p.idx % 8 == 0;
+                if (aligned && ident_bands(p.g, sizeof(ST), false).R > 0)
+                    return ident_band_forward<ST>(OP, p.replicate != 0, p.fill, p.x, p.w, p.out, static_cast<uint8_t*>(p.idx), p.g, stream);
+            }
             if (save) return launch_fwd<ST, OP, MK_IDENT, 1, FWD_TAPS>(p, stream);
             return launch_fwd<ST, OP, MK_IDENT, 1, FWD_VALUE>(p, stream);
         default: return hipErrorInvalidValue;
