@@ -14,6 +14,8 @@
 //
 // They take planes whose width is a multiple of 8 (whole 16-byte vectors per row for every dtype) and
 // whose band fits the LDS (ident_bands); other shapes run the tiled kernels.
+#include <type_traits>
+
 #include "launch.hpp"
 
 namespace mca
@@ -26,6 +28,9 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int IDENT_HALO = 8;
 // Copies of the grad_weight bins in LDS (lane-striped, as the tiled kernels).
 constexpr int IDENT_NC = 32;
+// 16-byte vectors each thread has in flight while staging a band (a 16-row float64 band of a 112-wide
+// plane is 4 per thread).
+constexpr int IDENT_NB = 4;
 
 IdentBands ident_bands(const Geom& g, size_t elem_bytes, bool backward)
 {
@@ -112,14 +117,31 @@ __global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST>
         for (int e = 0; e < V; ++e) f[e] = p.fill;
         __builtin_memcpy(&fillv, f, 16);
     }
-    for (int j = threadIdx.x; j < rows * nv; j += BLOCK)
+    // IDENT_NB vectors per thread in flight at once: every load of a batch is issued (clamped into the
+    // plane, so unconditionally) before any is waited for.
+    const int total = rows * nv;
+    for (int j0 = threadIdx.x; j0 < total; j0 += IDENT_NB * BLOCK)
     {
-        const int lr = j / nv, vi = j - lr * nv;
-        const int y = wk.h0 - P + lr;
-        u32x4 v = fillv;
-        if ((unsigned)y < (unsigned)g.H || p.replicate)
-            v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + (int64_t)clampi(y, 0, g.H - 1) * g.W) + vi);
-        *reinterpret_cast<u32x4*>(tile + lr * pitch + H8 + vi * V) = v;
+        u32x4 v[IDENT_NB];
+#pragma unroll
+        for (int u = 0; u < IDENT_NB; ++u)
+        {
+            const int j = min(j0 + u * BLOCK, total - 1);
+            const int lr = j / nv, vi = j - lr * nv;
+            v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + (int64_t)clampi(wk.h0 - P + lr, 0, g.H - 1) * g.W) + vi);
+        }
+        // Keeps the compiler from sinking each load into the conditional store that uses it.
+#pragma unroll
+        for (int u = 0; u < IDENT_NB; ++u) asm volatile("" : "+v"(v[u]));
+#pragma unroll
+        for (int u = 0; u < IDENT_NB; ++u)
+        {
+            const int j = j0 + u * BLOCK;
+            if (j >= total) break;
+            const int lr = j / nv, vi = j - lr * nv;
+            const int y = wk.h0 - P + lr;
+            *reinterpret_cast<u32x4*>(tile + lr * pitch + H8 + vi * V) = ((unsigned)y < (unsigned)g.H || p.replicate) ? v[u] : fillv;
+        }
     }
     // The P columns left and right of every staged row.
     for (int j = threadIdx.x; j < rows * 2 * P; j += BLOCK)
@@ -263,36 +285,36 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
     for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
     // The band's output rows and the P rows around them: gradient and tap of every output pixel that
     // reads a pixel of the band; outside the image, no gradient and no tap.
-    for (int j = threadIdx.x; j < rows * nv; j += BLOCK)
+    // As the forward's staging: IDENT_NB vectors (and their taps) per thread in flight at once.
+    using TapBits = std::conditional_t<V == 2, uint16_t, std::conditional_t<V == 4, uint32_t, uint64_t>>;
+    const TapBits none = (TapBits)~(TapBits)0;
+    const int total = rows * nv;
+    for (int j0 = threadIdx.x; j0 < total; j0 += IDENT_NB * BLOCK)
     {
-        const int lr = j / nv, vi = j - lr * nv;
-        const int y = wk.h0 - P + lr;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        uint8_t t[V];
+        u32x4 v[IDENT_NB];
+        TapBits t[IDENT_NB];
 #pragma unroll
-        for (int e = 0; e < V; ++e) t[e] = NONE;
-        if ((unsigned)y < (unsigned)g.H)
+        for (int u = 0; u < IDENT_NB; ++u)
         {
-            v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gp + (int64_t)y * g.W) + vi);
-            const uint8_t* src = tp + (int64_t)y * g.W + vi * V;
-            if constexpr (V == 2)
-            {
-                const uint16_t b2 = *reinterpret_cast<const uint16_t*>(src);
-                __builtin_memcpy(t, &b2, 2);
-            }
-            else if constexpr (V == 4)
-            {
-                const uint32_t b4 = *reinterpret_cast<const uint32_t*>(src);
-                __builtin_memcpy(t, &b4, 4);
-            }
-            else
-            {
-                const uint64_t b8 = *reinterpret_cast<const uint64_t*>(src);
-                __builtin_memcpy(t, &b8, 8);
-            }
+            const int j = min(j0 + u * BLOCK, total - 1);
+            const int lr = j / nv, vi = j - lr * nv;
+            const int64_t row = (int64_t)clampi(wk.h0 - P + lr, 0, g.H - 1) * g.W;
+            v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gp + row) + vi);
+            t[u] = reinterpret_cast<const TapBits*>(tp + row)[vi];
         }
-        *reinterpret_cast<u32x4*>(gs + lr * pitch + H8 + vi * V) = v;
-        __builtin_memcpy(ts + lr * pitch + H8 + vi * V, t, V);
+#pragma unroll
+        for (int u = 0; u < IDENT_NB; ++u) asm volatile("" : "+v"(v[u]), "+v"(t[u]));
+#pragma unroll
+        for (int u = 0; u < IDENT_NB; ++u)
+        {
+            const int j = j0 + u * BLOCK;
+            if (j >= total) break;
+            const int lr = j / nv, vi = j - lr * nv;
+            const bool in = (unsigned)(wk.h0 - P + lr) < (unsigned)g.H;
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(gs + lr * pitch + H8 + vi * V) = in ? v[u] : zero;
+            *reinterpret_cast<TapBits*>(ts + lr * pitch + H8 + vi * V) = in ? t[u] : none;
+        }
     }
     for (int j = threadIdx.x; j < rows * 2 * P; j += BLOCK)
     {
@@ -310,7 +332,20 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
         const int r = j / nv, vi = j - r * nv;
         const int x0 = vi * V;
         // Input pixel (y, x) receives the gradient of output (y - P + kh, x - P + kw) when that
-        // output's tap is (kh, kw): LDS row r + kh, column H8 + x - P + kw.
+        // output's tap is (kh, kw): LDS row r + kh, column H8 + x - P + kw. The window of the V pixels
+        // is read first, unconditionally (a read inside the selection becomes a branch around each
+        // read, one LDS round trip after another).
+        uint8_t tw[KS][V + 2 * P];
+        T gw[KS][V + 2 * P];
+#pragma unroll
+        for (int kh = 0; kh < KS; ++kh)
+#pragma unroll
+            for (int cc = 0; cc < V + 2 * P; ++cc)
+            {
+                const int idx = (r + kh) * pitch + H8 + x0 - P + cc;
+                tw[kh][cc] = ts[idx];
+                gw[kh][cc] = (T)gs[idx];
+            }
         ST res[V];
 #pragma unroll
         for (int e = 0; e < V; ++e)
@@ -319,16 +354,11 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
 #pragma unroll
             for (int kh = 0; kh < KS; ++kh)
 #pragma unroll
-                for (int kw = 0; kw < KS; ++kw)
-                {
-                    const int idx = (r + kh) * pitch + H8 + x0 + e - P + kw;
-                    s += ts[idx] == kh * KS + kw ? (Acc)(T)gs[idx] : Acc(0);
-                }
+                for (int kw = 0; kw < KS; ++kw) s += tw[kh][e + kw] == kh * KS + kw ? (Acc)gw[kh][e + kw] : Acc(0);
             res[e] = (ST)(T)s;
-            // grad_weight: the output pixel at the same position (row r + P of the staged rows).
-            const int own = (r + P) * pitch + H8 + x0 + e;
-            const T gv = (T)gs[own];
-            const int k = ts[own];
+            // grad_weight: the output pixel at the same position (window row P, column e + P).
+            const T gv = gw[P][e + P];
+            const int k = tw[P][e + P];
             if (k < K) lds_add(&bins[k * NC + copy], (Acc)(OP == DILATION ? gv : -gv));
         }
         u32x4 ov;
