@@ -14,17 +14,32 @@ __global__ __launch_bounds__(BLOCK) void fill_kernel(T* __restrict__ p, int64_t 
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) p[j] = v;
 }
 
+// Sum of part[s * n + j] over the slots s0 <= s < s1, in slot order, accumulated in double. The loads
+// of REDUCE_GROUP slots are all issued before the first add (in bounds: clamped), so a thread waits
+// once per group instead of once per slot; slots past s1 add +0, which leaves the sum unchanged (it
+// starts at +0 and can never become -0).
+template <typename T>
+__device__ __forceinline__ Acc sum_slots(const T* __restrict__ part, int s0, int s1, int64_t n, int64_t j)
+{
+    Acc s = Acc(0);
+    for (int b = s0; b < s1; b += REDUCE_GROUP)
+    {
+        T v[REDUCE_GROUP];
+#pragma unroll
+        for (int u = 0; u < REDUCE_GROUP; ++u) v[u] = part[(int64_t)min(b + u, s1 - 1) * n + j];
+#pragma unroll
+        for (int u = 0; u < REDUCE_GROUP; ++u) s += b + u < s1 ? (Acc)v[u] : Acc(0);
+    }
+    return s;
+}
+
 // out[j] = sum over slots s = 0, 1, ... of part[s * n + j], always in slot order, accumulated in
 // double and rounded once.
 template <typename T>
 __global__ __launch_bounds__(BLOCK) void reduce_slots_kernel(const T* __restrict__ part, int nslots, int64_t n, T* __restrict__ out)
 {
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
-    {
-        Acc s = Acc(0);
-        for (int slot = 0; slot < nslots; ++slot) s += (Acc)part[(int64_t)slot * n + j];
-        out[j] = (T)s;
-    }
+        out[j] = (T)sum_slots(part, 0, nslots, n, j);
 }
 
 // First stage of a long reduction: group blockIdx.y sums slots [y * REDUCE_GROUP, (y + 1) *
@@ -35,11 +50,7 @@ __global__ __launch_bounds__(BLOCK) void reduce_groups_kernel(const T* __restric
     const int s0 = blockIdx.y * REDUCE_GROUP;
     const int s1 = min(s0 + REDUCE_GROUP, nslots);
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
-    {
-        Acc s = Acc(0);
-        for (int slot = s0; slot < s1; ++slot) s += (Acc)part[(int64_t)slot * n + j];
-        tmp[(int64_t)blockIdx.y * n + j] = (T)s;
-    }
+        tmp[(int64_t)blockIdx.y * n + j] = (T)sum_slots(part, s0, s1, n, j);
 }
 
 // dst[j] = (T)src[j]: a double accumulator rounded once into its float32 result.
