@@ -17,8 +17,9 @@ timed region is exactly K steps between device synchronisations.
 Prints one JSON line with the whole-job throughput in output elements per second, the roofline of
 the step's dominant kernel ("roofline") and of its other large kernel ("roofline_other_kernel"): the
 step's forward and backward launches, each enqueued through the C ABI after the timed region with the
-step's own inputs and timed with HIP events on torch's current stream (the stream it runs on); the one
-with the longer launch time (each is called once per phase of a step) is the dominant one. HBM traffic
+step's own inputs, in the step's order (forward, backward, forward, ...), and timed with HIP events
+between them on torch's current stream (the stream they run on); the one with the longer launch time
+(each is called once per phase of a step) is the dominant one. HBM traffic
 and VALU instruction counts come from the committed rocprofv3 counter summaries. Then the CPU baseline
 (the reference's own CPU extension, or the C oracle, on a bounded sample on the host cores, in a child
 process).
@@ -407,36 +408,64 @@ def step_work(cfg):
     return 2 * t + 26 * t + 2 * t, "flop"  # stack: dilation, smorph, erosion (index scatters not counted)
 
 
-def time_launches(torch, launch, target_s=1.0, max_n=50):
-    """Average duration of back-to-back launches between two HIP events on the current stream.
+# Untimed pairs of launches between the spin kernel and the first timed event (time_step_kernels).
+RAMP_PAIRS = 5
 
-    A spin kernel queued ahead of the first event keeps the GPU busy while the host queues the n
-    launches, so that the events bracket kernels that run back to back and not the host's launch
-    gaps (which exceed the kernel time of the smallest configurations)."""
+
+def time_step_kernels(torch, fwd, bwd, target_s=1.0, max_n=50):
+    """Average durations of the step's forward and backward launches, launched in the step's own
+    order (forward, backward, forward, ...) with a HIP event between consecutive launches on the
+    current stream. (A kernel launched back to back with itself can run at another speed: the
+    float64 identity forward of configs[3] measures 0.188 ms that way against 0.162 ms after each
+    backward, as in a step.)
+
+    When a pair of launches takes the GPU less than twice the host's time to enqueue it (the
+    smallest configurations), a spin kernel queued ahead of the first event keeps the GPU busy while
+    the host queues the n pairs, so that the events bracket kernels that run back to back and not the
+    host's launch gaps; RAMP_PAIRS untimed pairs follow the spin (it lets the clocks drop). Longer
+    launches keep the GPU ahead of the host by themselves and run without it: a queue of pairs built
+    up behind a spin runs the HBM-bound kernels of configs[3] 3-4% slower than the steps do."""
     s = torch.cuda.current_stream()
-    launch()
+    fwd()
+    bwd()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(s)
-    launch()
+    fwd()
+    bwd()
     e1.record(s)
     host_s = time.perf_counter() - t0
     torch.cuda.synchronize()
-    n = max(1, min(max_n, int(target_s * 1000.0 / max(e0.elapsed_time(e1), 1e-3))))
-    # Spin-kernel clock rate, then a spin covering twice the host time of n launches (at most 0.5 s).
-    e0.record(s)
-    torch.cuda._sleep(1 << 20)
-    e1.record(s)
+    pair_ms = e0.elapsed_time(e1)
+    n = max(1, min(max_n, int(target_s * 1000.0 / max(pair_ms, 1e-3))))
+    # About 20 ms of untimed pairs first: the clocks drop during the host's set-up after the steps (the
+    # first 50 pairs of configs[3] then average 11% slower).
+    for _ in range(int(20.0 / max(pair_ms, 1e-3))):
+        fwd()
+        bwd()
+    if pair_ms < 2.0 * host_s * 1e3:
+        # Spin-kernel clock rate, then a spin covering twice the host time of the pairs (at most 0.5 s).
+        e0.record(s)
+        torch.cuda._sleep(1 << 20)
+        e1.record(s)
+        torch.cuda.synchronize()
+        cycles_per_ms = (1 << 20) / max(e0.elapsed_time(e1), 1e-3)
+        torch.cuda._sleep(int(min(500.0, 2.0 * (n + RAMP_PAIRS) * host_s * 1e3 + 1.0) * cycles_per_ms))
+        for _ in range(RAMP_PAIRS):
+            fwd()
+            bwd()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * n + 1)]
+    ev[0].record(s)
+    for i in range(n):
+        fwd()
+        ev[2 * i + 1].record(s)
+        bwd()
+        ev[2 * i + 2].record(s)
     torch.cuda.synchronize()
-    cycles_per_ms = (1 << 20) / max(e0.elapsed_time(e1), 1e-3)
-    torch.cuda._sleep(int(min(500.0, 2.0 * n * host_s * 1e3 + 1.0) * cycles_per_ms))
-    e0.record(s)
-    for _ in range(n):
-        launch()
-    e1.record(s)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / n, n
+    f_ms = sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(n)) / n
+    b_ms = sum(ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) for i in range(n)) / n
+    return f_ms, b_ms, n
 
 
 def profile_record(key):
@@ -489,7 +518,7 @@ def kernel_roofline(config, cfg, which, k, kms, kn):
             roof["frac_executed"] = k["executed"] / (kms * 1e-3) / 1e12 / peak_flops
     key = config_key(config) + ("" if which == "forward" else " backward")
     roof["traffic"] = measured_traffic(key)
-    roof.update({"kernel": k["what"], "phase": which, "kernel_ms": kms, "launches_timed": kn, "work_per_launch": k["work"],
+    roof.update({"kernel": k["what"], "phase": which, "kernel_ms": kms, "launch_pairs_timed": kn, "work_per_launch": k["work"],
                  "work_unit": k["unit"]})
     ceiling = instruction_ceiling(key, cfg, roof, k["work"])
     if ceiling is not None:
@@ -499,14 +528,13 @@ def kernel_roofline(config, cfg, which, k, kms, kn):
 
 
 def kernel_rooflines(config, cfg, torch, native, x, ws, dtype, dev):
-    """The step's two largest launches timed one after the other with HIP events; returns (dominant,
+    """The step's two largest launches timed in the step's order with HIP events; returns (dominant,
     other): the dominant one is the one with the larger launch time, each called once per phase of a
     step, so the larger share of the step."""
     ks = step_kernels(cfg, torch, native, x, ws, dtype, dev)
-    roofs = {}
-    for which, k in ks.items():
-        kms, kn = time_launches(torch, k["launch"])
-        roofs[which] = kernel_roofline(config, cfg, which, k, kms, kn)
+    f_ms, b_ms, n = time_step_kernels(torch, ks["forward"]["launch"], ks["backward"]["launch"])
+    roofs = {"forward": kernel_roofline(config, cfg, "forward", ks["forward"], f_ms, n),
+             "backward": kernel_roofline(config, cfg, "backward", ks["backward"], b_ms, n)}
     del ks
     order = sorted(roofs, key=lambda w: roofs[w]["kernel_ms"], reverse=True)
     return roofs[order[0]], roofs[order[1]]
