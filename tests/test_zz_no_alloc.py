@@ -52,6 +52,15 @@ def test_noalloc_backward_matches_workspace_backward_twice(merge, with_indices):
     _case(op, merge, 1, 3, 4, 17, 30, 3, 200 + merge, with_indices)
 
 
+@pytest.mark.parametrize("K", [3, 5])
+def test_noalloc_identity_row_bands_twice(K):
+    """Identity planes whose width is a multiple of 8 (16-byte aligned buffers): the row-band gather
+    and its per-band partial slots in the scratch, then a smaller plane."""
+    print(f"noalloc identity row bands k{K}: 2x6x37x64, then 1x3x19x32", flush=True)
+    _case(O.DILATION, O.IDENTITY, 2, 6, 6, 37, 64, K, 400 + K, True)
+    _case(O.EROSION, O.IDENTITY, 1, 3, 3, 19, 32, K, 410 + K, True)
+
+
 def test_noalloc_backward_dyadic_exact():
     _case(O.DILATION, O.ADD, 2, 4, 4, 33, 70, 3, 300, True, kind="quant")
     _case(O.DILATION, O.MAX, 1, 2, 3, 20, 20, 3, 310, False, kind="quant")
