@@ -95,30 +95,24 @@ __device__ __forceinline__ void store_bytes(uint8_t* p, const int (&a)[N])
         *reinterpret_cast<uint32_t*>(p) = (uint32_t)(a[0] | (a[1] << 8) | (a[2] << 16) | (a[3] << 24));
 }
 
-template <typename ST, int OP, int KS, bool TAPS>
-__global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST> p)
+// Stages `rows` image rows from row y0 of one plane into an LDS tile of row pitch `pitch` (image column
+// x at H8 + x): rows outside the image are the clamped row (replicate) or the fill value; then the P
+// columns left and right of every staged row (replicate: the row's edge pixel, else the fill value).
+// IDENT_NB vectors per thread are in flight at once: every load of a batch is issued (clamped into the
+// plane, so unconditionally) before any is waited for.
+template <typename ST, int P>
+__device__ __forceinline__ void band_stage(ST* tile, const ST* __restrict__ xp, const Geom& g, int pitch, int rows, int y0, bool replicate,
+                                           ST fill)
 {
-    using Tr = OpTraits<OP, ST>;
-    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST), H8 = IDENT_HALO;
-    extern __shared__ __align__(16) unsigned char smem[];
-    ST* tile = reinterpret_cast<ST*>(smem);
-    const Geom& g = p.g;
-    const IdentWork wk = ident_work(g, p.R, p.nbands);
-    const int pitch = g.W + 2 * H8, nv = g.W / V, rows = wk.hn + 2 * P;
-    const int64_t plane = g.plane();
-    const ST* __restrict__ xp = p.x + ((int64_t)wk.b * g.Cin + wk.c) * plane;
-
-    // The band's rows and its halo rows: rows outside the image are the clamped row (replicate) or
-    // the fill value.
+    constexpr int V = 16 / sizeof(ST), H8 = IDENT_HALO;
+    const int nv = g.W / V;
     u32x4 fillv;
     {
         ST f[V];
 #pragma unroll
-        for (int e = 0; e < V; ++e) f[e] = p.fill;
+        for (int e = 0; e < V; ++e) f[e] = fill;
         __builtin_memcpy(&fillv, f, 16);
     }
-    // IDENT_NB vectors per thread in flight at once: every load of a batch is issued (clamped into the
-    // plane, so unconditionally) before any is waited for.
     const int total = rows * nv;
     for (int j0 = threadIdx.x; j0 < total; j0 += IDENT_NB * BLOCK)
     {
@@ -128,7 +122,7 @@ __global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST>
         {
             const int j = min(j0 + u * BLOCK, total - 1);
             const int lr = j / nv, vi = j - lr * nv;
-            v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + (int64_t)clampi(wk.h0 - P + lr, 0, g.H - 1) * g.W) + vi);
+            v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xp + (int64_t)clampi(y0 + lr, 0, g.H - 1) * g.W) + vi);
         }
         // Keeps the compiler from sinking each load into the conditional store that uses it.
 #pragma unroll
@@ -139,20 +133,85 @@ __global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST>
             const int j = j0 + u * BLOCK;
             if (j >= total) break;
             const int lr = j / nv, vi = j - lr * nv;
-            const int y = wk.h0 - P + lr;
-            *reinterpret_cast<u32x4*>(tile + lr * pitch + H8 + vi * V) = ((unsigned)y < (unsigned)g.H || p.replicate) ? v[u] : fillv;
+            const int y = y0 + lr;
+            *reinterpret_cast<u32x4*>(tile + lr * pitch + H8 + vi * V) = ((unsigned)y < (unsigned)g.H || replicate) ? v[u] : fillv;
         }
     }
-    // The P columns left and right of every staged row.
     for (int j = threadIdx.x; j < rows * 2 * P; j += BLOCK)
     {
         const int lr = j / (2 * P), q = j - lr * (2 * P);
         const bool right = q >= P;
         const int col = right ? g.W + (q - P) : -1 - q;
-        ST v = p.fill;
-        if (p.replicate) v = xp[(int64_t)clampi(wk.h0 - P + lr, 0, g.H - 1) * g.W + (right ? g.W - 1 : 0)];
+        ST v = fill;
+        if (replicate) v = xp[(int64_t)clampi(y0 + lr, 0, g.H - 1) * g.W + (right ? g.W - 1 : 0)];
         tile[lr * pitch + H8 + col] = v;
     }
+}
+
+// V consecutive outputs (image columns x0 ..) of one row from an LDS tile laid out as band_stage's,
+// whose row r + 2P - kh holds the input row that the outputs' tap row kh reads: the extremum
+// (NaN-ignoring, from the start value) and, for TAPS, the first tap (kh, then kw) equal to it, which is
+// the tap the reference's strict scan keeps; a pair that never improves on the start value keeps tap 0.
+template <typename ST, int OP, int KS, bool TAPS>
+__device__ __forceinline__ void band_scan(const ST* tile, int pitch, int r, int x0, const ST (&wv)[KS * KS], ST (&res)[16 / sizeof(ST)],
+                                          int (&arg)[16 / sizeof(ST)])
+{
+    using Tr = OpTraits<OP, ST>;
+    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST), H8 = IDENT_HALO;
+    // Output (h, w) tap (kh, kw) reads input (h + P - kh, w + P - kw): LDS row r + 2P - kh, column
+    // H8 + w + P - kw.
+    ST win[KS][V + 2 * P];
+#pragma unroll
+    for (int kh = 0; kh < KS; ++kh)
+#pragma unroll
+        for (int cc = 0; cc < V + 2 * P; ++cc) win[kh][cc] = tile[(r + 2 * P - kh) * pitch + H8 + x0 - P + cc];
+    auto tap = [&](int e, int k) { return Tr::combine(win[k / KS][e + 2 * P - k % KS], wv[k]); };
+    bool zero = false;
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+    {
+        ST best = Tr::init();
+#pragma unroll
+        for (int k = 0; k < K; ++k) best = Tr::pick(best, tap(e, k));
+        res[e] = best;
+        zero |= best == ST(0);
+        if constexpr (TAPS)
+        {
+            int a = 0;
+#pragma unroll
+            for (int k = K - 1; k >= 0; --k) a = tap(e, k) == best ? k : a;
+            arg[e] = best == Tr::init() ? 0 : a;
+        }
+    }
+    // A zero extremum takes the sign of its first tap (the NaN-ignoring extremum does not order -0 and
+    // +0; the strict scan keeps the first): rare, so behind a branch uniform over the active lanes.
+    if (__builtin_amdgcn_ballot_w64(zero))
+    {
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+        {
+            ST first = res[e];
+#pragma unroll
+            for (int k = K - 1; k >= 0; --k) first = tap(e, k) == res[e] ? tap(e, k) : first;
+            res[e] = res[e] == ST(0) ? first : res[e];
+        }
+    }
+}
+
+template <typename ST, int OP, int KS, bool TAPS>
+__global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST> p)
+{
+    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST);
+    extern __shared__ __align__(16) unsigned char smem[];
+    ST* tile = reinterpret_cast<ST*>(smem);
+    const Geom& g = p.g;
+    const IdentWork wk = ident_work(g, p.R, p.nbands);
+    const int pitch = g.W + 2 * IDENT_HALO, nv = g.W / V;
+    const int64_t plane = g.plane();
+    const ST* __restrict__ xp = p.x + ((int64_t)wk.b * g.Cin + wk.c) * plane;
+
+    // The band's rows and its P halo rows above and below.
+    band_stage<ST, P>(tile, xp, g, pitch, wk.hn + 2 * P, wk.h0 - P, p.replicate != 0, p.fill);
     ST wv[K];
     const ST* __restrict__ wp = p.w + (int64_t)wk.b * g.wbs + (int64_t)wk.c * K;
 #pragma unroll
@@ -164,49 +223,9 @@ __global__ __launch_bounds__(BLOCK) void ident_band_fwd(const IdentFwdParams<ST>
     {
         const int r = j / nv, vi = j - r * nv;
         const int x0 = vi * V;
-        // Output (h, w) tap (kh, kw) reads input (h + P - kh, w + P - kw): LDS row r + 2P - kh, column
-        // H8 + w + P - kw.
-        ST win[KS][V + 2 * P];
-#pragma unroll
-        for (int kh = 0; kh < KS; ++kh)
-#pragma unroll
-            for (int cc = 0; cc < V + 2 * P; ++cc) win[kh][cc] = tile[(r + 2 * P - kh) * pitch + H8 + x0 - P + cc];
-        auto tap = [&](int e, int k) { return Tr::combine(win[k / KS][e + 2 * P - k % KS], wv[k]); };
         ST res[V];
         int arg[V];
-        bool zero = false;
-#pragma unroll
-        for (int e = 0; e < V; ++e)
-        {
-            // The extremum (NaN-ignoring, from the start value), then the first tap (kh, then kw)
-            // equal to it: the tap the reference's strict scan keeps. A pair that never improves on
-            // the start value keeps tap 0.
-            ST best = Tr::init();
-#pragma unroll
-            for (int k = 0; k < K; ++k) best = Tr::pick(best, tap(e, k));
-            res[e] = best;
-            zero |= best == ST(0);
-            if constexpr (TAPS)
-            {
-                int a = 0;
-#pragma unroll
-                for (int k = K - 1; k >= 0; --k) a = tap(e, k) == best ? k : a;
-                arg[e] = best == Tr::init() ? 0 : a;
-            }
-        }
-        // A zero extremum takes the sign of its first tap (the NaN-ignoring extremum does not order
-        // -0 and +0; the strict scan keeps the first): rare, so behind a wave-uniform branch.
-        if (__builtin_amdgcn_ballot_w64(zero))
-        {
-#pragma unroll
-            for (int e = 0; e < V; ++e)
-            {
-                ST first = res[e];
-#pragma unroll
-                for (int k = K - 1; k >= 0; --k) first = tap(e, k) == res[e] ? tap(e, k) : first;
-                res[e] = res[e] == ST(0) ? first : res[e];
-            }
-        }
+        band_scan<ST, OP, KS, TAPS>(tile, pitch, r, x0, wv, res, arg);
         const int64_t o = (int64_t)(wk.h0 + r) * g.W + x0;
         u32x4 ov;
         __builtin_memcpy(&ov, res, 16);
@@ -263,32 +282,21 @@ struct IdentGatherParams
     int R, nbands;
 };
 
-// T: the type of the sums and partial slots (float for 16-bit storage), ST: the storage type of the
-// gradients.
-template <typename T, int OP, int KS, typename ST>
-__global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherParams<T, ST> p)
-{
-    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST), H8 = IDENT_HALO, NC = IDENT_NC;
-    constexpr uint8_t NONE = 0xff;  // matches no tap: outside the image
-    extern __shared__ __align__(16) unsigned char smem[];
-    const Geom& g = p.g;
-    const IdentWork wk = ident_work(g, p.R, p.nbands);
-    const int pitch = g.W + 2 * H8, nv = g.W / V, rows = wk.hn + 2 * P, rows_max = p.R + 2 * P;
-    ST* gs = reinterpret_cast<ST*>(smem);
-    uint8_t* ts = smem + align16((size_t)rows_max * pitch * sizeof(ST));
-    Acc* bins = reinterpret_cast<Acc*>(ts + align16((size_t)rows_max * pitch));
-    const int64_t plane = g.plane();
-    const int64_t pl = ((int64_t)wk.b * g.Cout + wk.c) * plane;
-    const ST* __restrict__ gp = p.gout + pl;
-    const uint8_t* __restrict__ tp = p.taps + pl;
+constexpr uint8_t IDENT_NONE = 0xff;  // a tap byte that matches no tap: outside the image
 
-    for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
-    // The band's output rows and the P rows around them: gradient and tap of every output pixel that
-    // reads a pixel of the band; outside the image, no gradient and no tap.
-    // As the forward's staging: IDENT_NB vectors (and their taps) per thread in flight at once.
+// Stages `rows` rows from row y0 of an output-gradient plane and of its tap plane into LDS tiles of
+// pitch `pitch` (image column x at H8 + x), as band_stage: rows outside the image and the P columns
+// left and right of every row hold no gradient (0) and no tap (IDENT_NONE).
+template <typename ST, int P>
+__device__ __forceinline__ void gather_stage(ST* gs, uint8_t* ts, const ST* __restrict__ gp, const uint8_t* __restrict__ tp, const Geom& g,
+                                             int pitch, int rows, int y0)
+{
+    constexpr int V = 16 / sizeof(ST), H8 = IDENT_HALO;
     using TapBits = std::conditional_t<V == 2, uint16_t, std::conditional_t<V == 4, uint32_t, uint64_t>>;
     const TapBits none = (TapBits)~(TapBits)0;
+    const int nv = g.W / V;
     const int total = rows * nv;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
     for (int j0 = threadIdx.x; j0 < total; j0 += IDENT_NB * BLOCK)
     {
         u32x4 v[IDENT_NB];
@@ -298,7 +306,7 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
         {
             const int j = min(j0 + u * BLOCK, total - 1);
             const int lr = j / nv, vi = j - lr * nv;
-            const int64_t row = (int64_t)clampi(wk.h0 - P + lr, 0, g.H - 1) * g.W;
+            const int64_t row = (int64_t)clampi(y0 + lr, 0, g.H - 1) * g.W;
             v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gp + row) + vi);
             t[u] = reinterpret_cast<const TapBits*>(tp + row)[vi];
         }
@@ -310,8 +318,7 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
             const int j = j0 + u * BLOCK;
             if (j >= total) break;
             const int lr = j / nv, vi = j - lr * nv;
-            const bool in = (unsigned)(wk.h0 - P + lr) < (unsigned)g.H;
-            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const bool in = (unsigned)(y0 + lr) < (unsigned)g.H;
             *reinterpret_cast<u32x4*>(gs + lr * pitch + H8 + vi * V) = in ? v[u] : zero;
             *reinterpret_cast<TapBits*>(ts + lr * pitch + H8 + vi * V) = in ? t[u] : none;
         }
@@ -321,8 +328,86 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
         const int lr = j / (2 * P), q = j - lr * (2 * P);
         const int col = q >= P ? g.W + (q - P) : -1 - q;
         gs[lr * pitch + H8 + col] = ST(0);
-        ts[lr * pitch + H8 + col] = NONE;
+        ts[lr * pitch + H8 + col] = IDENT_NONE;
     }
+}
+
+// grad_input of V consecutive pixels (image columns x0 ..) of one row, gathered in tap order from the
+// output gradients gs and taps ts staged as gather_stage's: input pixel (y, x) receives the gradient of
+// output (y - P + kh, x - P + kw) when that output's tap is (kh, kw), at LDS row r + kh, column
+// H8 + x - P + kw. With OWN, also the grad_weight terms of the outputs at the pixels' own positions
+// (row r + P) into the copy `copy` of the K bins. The window of the V pixels is read first,
+// unconditionally (a read inside the selection becomes a branch around each read, one LDS round trip
+// after another).
+template <typename T, int OP, int KS, typename ST>
+__device__ __forceinline__ void gather_vec(const ST* gs, const uint8_t* ts, int pitch, int r, int x0, bool own, Acc* bins, int copy,
+                                           ST (&res)[16 / sizeof(ST)])
+{
+    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST), H8 = IDENT_HALO, NC = IDENT_NC;
+    uint8_t tw[KS][V + 2 * P];
+    T gw[KS][V + 2 * P];
+#pragma unroll
+    for (int kh = 0; kh < KS; ++kh)
+#pragma unroll
+        for (int cc = 0; cc < V + 2 * P; ++cc)
+        {
+            const int idx = (r + kh) * pitch + H8 + x0 - P + cc;
+            tw[kh][cc] = ts[idx];
+            gw[kh][cc] = (T)gs[idx];
+        }
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+    {
+        Acc s = Acc(0);
+#pragma unroll
+        for (int kh = 0; kh < KS; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < KS; ++kw) s += tw[kh][e + kw] == kh * KS + kw ? (Acc)gw[kh][e + kw] : Acc(0);
+        res[e] = (ST)(T)s;
+        // grad_weight: the output pixel at the same position (window row P, column e + P).
+        const T gv = gw[P][e + P];
+        const int k = tw[P][e + P];
+        if (own && k < K) lds_add(&bins[k * NC + copy], (Acc)(OP == DILATION ? gv : -gv));
+    }
+}
+
+// The band's grad_weight bins into its partial slot: 8 threads per tap each add 4 copies, a butterfly
+// over the 8 finishes. The caller synchronises the workgroup first.
+template <typename T, int K>
+__device__ __forceinline__ void flush_bins(const Acc* bins, T* slot)
+{
+    static_assert(K * 8 <= BLOCK, "one pass over the bins");
+    static_assert(IDENT_NC == 32, "four copies per thread");
+    if (threadIdx.x < K * 8)
+    {
+        const Acc* q = bins + threadIdx.x * 4;
+        Acc v = (q[0] + q[1]) + (q[2] + q[3]);
+#pragma unroll
+        for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
+        if ((threadIdx.x & 7) == 0) slot[threadIdx.x >> 3] = (T)v;
+    }
+}
+
+// T: the type of the sums and partial slots (float for 16-bit storage), ST: the storage type of the
+// gradients.
+template <typename T, int OP, int KS, typename ST>
+__global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherParams<T, ST> p)
+{
+    constexpr int P = KS / 2, K = KS * KS, V = 16 / sizeof(ST), NC = IDENT_NC;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const Geom& g = p.g;
+    const IdentWork wk = ident_work(g, p.R, p.nbands);
+    const int pitch = g.W + 2 * IDENT_HALO, nv = g.W / V, rows_max = p.R + 2 * P;
+    ST* gs = reinterpret_cast<ST*>(smem);
+    uint8_t* ts = smem + align16((size_t)rows_max * pitch * sizeof(ST));
+    Acc* bins = reinterpret_cast<Acc*>(ts + align16((size_t)rows_max * pitch));
+    const int64_t plane = g.plane();
+    const int64_t pl = ((int64_t)wk.b * g.Cout + wk.c) * plane;
+
+    for (int j = threadIdx.x; j < K * NC; j += BLOCK) bins[j] = Acc(0);
+    // The band's output rows and the P rows around them: gradient and tap of every output pixel that
+    // reads a pixel of the band.
+    gather_stage<ST, P>(gs, ts, p.gout + pl, p.taps + pl, g, pitch, wk.hn + 2 * P, wk.h0 - P);
     __syncthreads();
 
     ST* __restrict__ ip = p.gin + ((int64_t)wk.b * g.Cin + wk.c) * plane;
@@ -331,55 +416,14 @@ __global__ __launch_bounds__(BLOCK) void ident_band_gather(const IdentGatherPara
     {
         const int r = j / nv, vi = j - r * nv;
         const int x0 = vi * V;
-        // Input pixel (y, x) receives the gradient of output (y - P + kh, x - P + kw) when that
-        // output's tap is (kh, kw): LDS row r + kh, column H8 + x - P + kw. The window of the V pixels
-        // is read first, unconditionally (a read inside the selection becomes a branch around each
-        // read, one LDS round trip after another).
-        uint8_t tw[KS][V + 2 * P];
-        T gw[KS][V + 2 * P];
-#pragma unroll
-        for (int kh = 0; kh < KS; ++kh)
-#pragma unroll
-            for (int cc = 0; cc < V + 2 * P; ++cc)
-            {
-                const int idx = (r + kh) * pitch + H8 + x0 - P + cc;
-                tw[kh][cc] = ts[idx];
-                gw[kh][cc] = (T)gs[idx];
-            }
         ST res[V];
-#pragma unroll
-        for (int e = 0; e < V; ++e)
-        {
-            Acc s = Acc(0);
-#pragma unroll
-            for (int kh = 0; kh < KS; ++kh)
-#pragma unroll
-                for (int kw = 0; kw < KS; ++kw) s += tw[kh][e + kw] == kh * KS + kw ? (Acc)gw[kh][e + kw] : Acc(0);
-            res[e] = (ST)(T)s;
-            // grad_weight: the output pixel at the same position (window row P, column e + P).
-            const T gv = gw[P][e + P];
-            const int k = tw[P][e + P];
-            if (k < K) lds_add(&bins[k * NC + copy], (Acc)(OP == DILATION ? gv : -gv));
-        }
+        gather_vec<T, OP, KS, ST>(gs, ts, pitch, r, x0, true, bins, copy, res);
         u32x4 ov;
         __builtin_memcpy(&ov, res, 16);
         __builtin_nontemporal_store(ov, reinterpret_cast<u32x4*>(ip + (int64_t)(wk.h0 + r) * g.W + x0));
     }
     __syncthreads();
-    // The band's bins: 8 threads per tap each add 4 copies, a butterfly over the 8 finishes.
-    static_assert(K * 8 <= BLOCK, "one pass over the bins");
-    if (threadIdx.x < K * 8)
-    {
-        const Acc* q = bins + threadIdx.x * 4;
-        Acc v = (q[0] + q[1]) + (q[2] + q[3]);
-#pragma unroll
-        for (int d = 4; d >= 1; d /= 2) v += __shfl_xor(v, d, 8);
-        if ((threadIdx.x & 7) == 0)
-        {
-            const int band = wk.h0 / p.R;
-            p.part[((int64_t)wk.b * p.nbands + band) * g.Cout * K + (int64_t)wk.c * K + (threadIdx.x >> 3)] = (T)v;
-        }
-    }
+    flush_bins<T, K>(bins, p.part + ((int64_t)wk.b * p.nbands + wk.h0 / p.R) * g.Cout * K + (int64_t)wk.c * K);
 }
 
 template <typename T, typename ST>
