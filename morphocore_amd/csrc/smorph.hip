@@ -85,6 +85,7 @@ __device__ __forceinline__ void smorph_pair_stats(const T* tbase, int pitch, con
 template <typename T, int MK, int RH, bool STATS>
 __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams<T> p)
 {
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fma)
     extern __shared__ __align__(16) unsigned char smem_raw[];
     T* tile = reinterpret_cast<T*>(smem_raw);
     const Geom g = p.g;
@@ -188,6 +189,7 @@ __global__ __launch_bounds__(BLOCK) void smorph_fwd_kernel(const SmorphFwdParams
 template <typename T, int MK, int RH, bool GGIN = false>
 __global__ __launch_bounds__(BLOCK) void smorph_bwd_kernel(const SmorphBwdParams<T> p)
 {
+#pragma clang fp contract(off)  // fused only where the reference fuses (written as fma)
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const Geom g = p.g;
     const Tiling t = p.t;

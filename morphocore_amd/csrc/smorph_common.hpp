@@ -74,10 +74,14 @@ __device__ __forceinline__ T smorph_merge_target(T forward_out, T channel0_out)
 }
 
 // Tolerance within which a channel counts as a MAX / MIN winner (reference: smorph.cu:7-9,
-// smorph_cpu_kernels.hxx:622-627).
+// smorph_cpu_kernels.hxx:622-627). `out` is the pair output rounded to T, as the reference stores it:
+// the subtraction is never fused with a caller's W * (1 / S) (an unrounded product moves d by up to
+// half a unit of the output's last place, which decides a pair lying that close to the tolerance
+// differently from the reference, and from the routing's own rounded test).
 template <typename T>
 __device__ __forceinline__ bool is_winner(T out, T target)
 {
+#pragma clang fp contract(off)
     const T d = out - target;
     const T tol = T(1e-6);
     return d < tol && d > -tol;

@@ -7,9 +7,10 @@ the HIP kernels against it at sizes the C oracle is too slow for start this scri
 (tests/helpers.py: reference_run) and read its results back.
 
 Usage: python oracle/ref_run.py IN.npz OUT.npz
-  IN holds "kind" ("smorph"), "threads" and the operator's arguments; for smorph: x, wt (the element
-  the operator receives, w~), alpha, grad (the output gradient), merge (the reference's int).
-  OUT receives out, grad_input, grad_weight (of wt) and grad_alpha.
+  IN holds "kind" ("smorph" or "smorph_scm"), "threads" and the operator's arguments: x, wt (the
+  element the operator receives, w~), alpha, grad (the output gradient), and merge (the reference's
+  int) for smorph or beta for smorph_scm.
+  OUT receives out, grad_input, grad_weight (of wt), grad_alpha and, for smorph_scm, grad_beta.
 """
 import os
 import sys
@@ -27,14 +28,21 @@ def main(src, dst):
     torch.ops.load_library(REF_LIB)
     ops = torch.ops.morphocore
     kind = str(inp["kind"])
-    if kind != "smorph":
+    if kind not in ("smorph", "smorph_scm"):
         raise ValueError(f"unknown kind {kind}")
     x = torch.from_numpy(inp["x"]).requires_grad_(True)
     wt = torch.from_numpy(inp["wt"]).requires_grad_(True)
     alpha = torch.from_numpy(inp["alpha"]).requires_grad_(True)
-    out = ops.smorph(x, wt, alpha, int(inp["merge"]))
+    extra = {}
+    if kind == "smorph":
+        out = ops.smorph(x, wt, alpha, int(inp["merge"]))
+    else:
+        beta = torch.from_numpy(inp["beta"]).requires_grad_(True)
+        out = ops.smorph_scm(x, wt, alpha, beta)
     out.backward(torch.from_numpy(inp["grad"]))
-    np.savez(dst, out=out.detach().numpy(), grad_input=x.grad.numpy(), grad_weight=wt.grad.numpy(), grad_alpha=alpha.grad.numpy())
+    if kind == "smorph_scm":
+        extra["grad_beta"] = beta.grad.numpy()
+    np.savez(dst, out=out.detach().numpy(), grad_input=x.grad.numpy(), grad_weight=wt.grad.numpy(), grad_alpha=alpha.grad.numpy(), **extra)
 
 
 if __name__ == "__main__":

@@ -5,16 +5,20 @@ tile or than the element, one channel), element size (square and rectangular, ev
 padding, dtype (dilation / erosion also float16 and bfloat16) and saving choice, then runs the operator through torch.ops.morphocore (the product
 path) and compares with the oracle: dilation / erosion forwards bit for bit, smorph forwards and every
 gradient within 1e-6 (float32) / 1e-12 (float64) norm-wise (a shared alpha's gradient, a sum over the
-pairs that can cancel, relative to the sum of its terms' magnitudes). The sweep exercises the launch plans
+pairs that can cancel, relative to the sum of its terms' magnitudes; an alpha gradient whose terms cancel
+so far that the reference extension's own float32 result misses 1e-6, within 1e-6 plus twice that
+miss of the float64 oracle). The sweep exercises the launch plans
 (tilings, workspace layouts, saved-statistics slots, small-grid shapes) on shapes no hand-written
 case picks.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import TOL, normwise_error
+from tests.helpers import REF_LIB, TOL, normwise_error, reference_run
 
 pytestmark = pytest.mark.gpu
 
@@ -128,27 +132,51 @@ def _smorph_run(c, monkeypatch, scm):
         out = torch.ops.morphocore.smorph_scm(xd, wd, ad, bd)
         out.backward(gout.to(dev))
         ref = O.smorph_scm_forward(x.numpy(), w.numpy(), alpha.numpy(), beta.numpy())
-        want = O.smorph_scm_backward(x.numpy(), w.numpy(), alpha.numpy(), beta.numpy(), gout.numpy())
+        backward = lambda *a: O.smorph_scm_backward(*a)  # noqa: E731
+        args = (x, w, alpha, beta, gout)
         got = (xd.grad, wd.grad, ad.grad, bd.grad)
     else:
         merge = O.MERGES[c["merge"]]
         out = torch.ops.morphocore.smorph(xd, wd, ad, merge)
         out.backward(gout.to(dev))
         ref = O.smorph_forward(merge, x.numpy(), w.numpy(), alpha.numpy())
-        want = O.smorph_backward(merge, x.numpy(), w.numpy(), alpha.numpy(), gout.numpy())
+        backward = lambda *a: O.smorph_backward(merge, *a)  # noqa: E731
+        args = (x, w, alpha, gout)
         got = (xd.grad, wd.grad, ad.grad)
+    want = backward(*(t.numpy() for t in args))
     _check(out, ref, c["dtype"], "forward")
     for name, a, b in zip(("grad_input", "grad_weight", "grad_alpha", "grad_beta"), got, want):
-        if name == "grad_alpha" and c["shared"]:
+        if name != "grad_alpha":
+            _check(a, b, c["dtype"], name)
+            continue
+        if c["shared"]:
             # A shared alpha receives the sum of every pair's gradient (smorph.cpp:96-98), which can
-            # cancel far below its terms (float32's own sum then moves by more than 1e-6 of the
-            # result: the oracle's differs from its float64 counterpart by up to ~5e-5 on these
-            # inputs); its error is measured against the sum of the terms' magnitudes instead.
+            # cancel far below its terms; its error is measured against the sum of the terms' magnitudes.
             per_pair = _per_pair_alpha_grads(c, x, w, alpha, gout, beta if scm else None)
             err = abs(float(a) - float(b)) / max(float(np.abs(per_pair).sum(dtype=np.float64)), 1e-30)
-            assert err <= TOL[c["dtype"]], f"{name} (shared): {err}"
+        else:
+            err = normwise_error(a.detach().cpu().numpy(), b)
+        if err <= TOL[c["dtype"]]:
             continue
-        _check(a, b, c["dtype"], name)
+        # Each pair's alpha gradient sums a term over every pixel (and a shared one over every pair too);
+        # the terms can cancel far below their size, and then no float32 evaluation meets 1e-6 of the
+        # result: on the 13 cases of an 8,100-case sweep that reached this branch, the reference
+        # extension's own result lay 1.6e-7 to 9.5e-5 from the float64 oracle, the kernels' 3.6e-7 to
+        # 1.1e-4 (closer than the reference's in 6 of them). There the kernels are held to 1e-6 plus
+        # twice the reference extension's distance, both against the float64 oracle.
+        assert c["dtype"] == torch.float32, f"{name}: {err}"
+        exact = backward(*(t.double().numpy() for t in args))[2]
+        if not os.path.exists(REF_LIB):
+            pytest.skip(f"{name}: {err} from the oracle, and the reference extension (oracle/_ref) is not built to measure its own")
+        ref_args = dict(x=x.numpy(), wt=w.numpy(), alpha=alpha.numpy(), grad=gout.numpy())
+        if scm:
+            refx = reference_run("smorph_scm", beta=beta.numpy(), **ref_args)
+        else:
+            refx = reference_run("smorph", merge=np.array(O.MERGES[c["merge"]]), **ref_args)
+        noise = normwise_error(refx["grad_alpha"].astype(np.float64), exact)
+        err = normwise_error(a.detach().cpu().numpy().astype(np.float64), exact)
+        print(f"grad_alpha against the float64 oracle: kernels {err:.3g}, the reference extension {noise:.3g}", flush=True)
+        assert err <= TOL[c["dtype"]] + 2 * noise, f"{name}: {err} against the float64 oracle (the reference extension: {noise})"
 
 
 def _per_pair_alpha_grads(c, x, w, alpha, gout, beta):
@@ -169,3 +197,13 @@ def test_smorph_sweep(c, monkeypatch):
 @pytest.mark.parametrize("c", list(_smorph_cases(80, 7303, ["sum"])), ids=_ids)
 def test_smorph_scm_sweep(c, monkeypatch):
     _smorph_run(c, monkeypatch, scm=True)
+
+@pytest.mark.parametrize("save", [False, True])
+def test_smorph_max_pair_just_outside_the_winner_tolerance(save, monkeypatch):
+    """A MAX merge where a second channel's pair output lies 1.0133e-6 below the winner's (batch 1,
+    output channel 1, pixel (16, 142)): outside the 1e-6 tolerance once the pair output is rounded, as
+    the reference rounds it, but inside it if the winner count fused W * (1 / S) into the subtraction,
+    which then split that pixel's gradient between two channels (grad_input off by 8e-3 there)."""
+    c = dict(B=3, Cin=7, Cout=6, H=85, W=143, KH=4, KW=2, dtype=torch.float32, seed=803402658, merge="max", shared=True,
+             alpha_scale=5.0, save=save)
+    _smorph_run(c, monkeypatch, scm=False)
