@@ -109,6 +109,15 @@ float oracle_expf(float x) { return oracle_exp_f32(x); }
 double oracle_exp(double x) { return oracle_exp_f64(x); }
 
 /* The exponential over an array (y[j] = exp(x[j])), for bitwise comparisons of many arguments. */
+/* Test helper, no counterpart in the reference: while set, the smorph backwards accumulate the magnitude
+ * of every grad_weight, grad_alpha and grad_beta term instead of the term (each routed tap's |c|, each
+ * pixel's |pg (v - ref)(v - out)| and |q (c - ref)(c - out) g|, in ACC), giving the sum of the terms'
+ * magnitudes: the scale against which the float32 error of those sums, whose terms can cancel far below
+ * their size, is measured. */
+static int oracle_abs_terms = 0;
+void oracle_set_abs_terms(int on) { oracle_abs_terms = on; }
+#define TERM(v) (oracle_abs_terms ? fabsl((long double)(v)) : (long double)(v))
+
 void oracle_expf_array(const float* x, float* y, int64_t n)
 {
 #pragma omp parallel for schedule(static)

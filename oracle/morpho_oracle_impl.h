@@ -433,8 +433,8 @@ int FN(oracle_smorph_backward)(int merge, const T* x, const T* wt, const T* alph
                                     const T centered = v - out;
                                     const T c = FMA_T(a * pg, centered, pg); /* pg + alpha * pg * centered, fused */
                                     gx_acc[(b * Cin + i) * plane + ih * W + iw] += (ACC)c;
-                                    gw[(o * Cw + wi) * taps + k] += (ACC)c;
-                                    alpha_sum += (ACC)(pg * (v - ref) * centered);
+                                    gw[(o * Cw + wi) * taps + k] += (ACC)TERM(c);
+                                    alpha_sum += (ACC)TERM(pg * (v - ref) * centered);
                                 }
                             }
                             ga[ai] += alpha_sum;
@@ -599,7 +599,7 @@ int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, cons
                         {
                             const T c = outs[i];
                             const T p = EXP_T((c - sref) * bt) * sinv;
-                            gb[o] += (ACC)(p * (c - sref) * (c - fin) * grad);
+                            gb[o] += (ACC)TERM(p * (c - sref) * (c - fin) * grad);
                         }
                         for (int64_t i = 0; i < Cin; i++)
                         {
@@ -626,8 +626,8 @@ int FN(oracle_smorph_scm_backward)(const T* x, const T* wt, const T* alpha, cons
                                     const T centered = v - out;
                                     const T cc = FMA_T(a * pg, centered, pg);
                                     gx_acc[(b * Cin + i) * plane + ih * W + iw] += (ACC)cc;
-                                    gw[(o * Cw + i) * taps + k] += (ACC)cc;
-                                    alpha_sum += (ACC)(pg * (v - ref) * centered);
+                                    gw[(o * Cw + i) * taps + k] += (ACC)TERM(cc);
+                                    alpha_sum += (ACC)TERM(pg * (v - ref) * centered);
                                 }
                             }
                             ga[ai] += alpha_sum;

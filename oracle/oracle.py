@@ -65,6 +65,8 @@ def lib() -> ctypes.CDLL:
             f = getattr(_lib, f"oracle_smorph_scm_backward_{sfx}")
             f.argtypes = [p, p, p, p, p, p, p, p, p] + geom
             f.restype = i32
+        _lib.oracle_set_abs_terms.argtypes = [i32]
+        _lib.oracle_set_abs_terms.restype = None
         _lib.oracle_expf.argtypes = [ctypes.c_float]
         _lib.oracle_expf.restype = ctypes.c_float
         _lib.oracle_exp.argtypes = [ctypes.c_double]
@@ -240,6 +242,30 @@ def smorph_scm_backward(x, w_tilde, alpha, beta, grad_out):
     else:
         ga = ga.reshape(alpha.shape)
     return gx, gw, ga, gb.reshape(beta.shape)
+
+
+def smorph_term_magnitudes(merge, x, w_tilde, alpha, grad_out):
+    """Test helper, no counterpart in the reference: for the weight and alpha gradients of smorph_backward
+    (shaped like them), the sums of the magnitudes of their terms (every routed tap's c, every pixel's and
+    tap's pg (v - ref)(v - out)): ``(weight magnitudes, alpha magnitudes)``, the scale against which the
+    float32 error of those sums, whose terms can cancel far below their size, is measured."""
+    lib().oracle_set_abs_terms(1)
+    try:
+        r = smorph_backward(merge, x, w_tilde, alpha, grad_out)
+        return r[1], r[2]
+    finally:
+        lib().oracle_set_abs_terms(0)
+
+
+def smorph_scm_term_magnitudes(x, w_tilde, alpha, beta, grad_out):
+    """As smorph_term_magnitudes for smorph_scm_backward: ``(weight, alpha, beta magnitudes)``, the beta
+    terms being each pixel's and pair's q (c - ref)(c - out) g."""
+    lib().oracle_set_abs_terms(1)
+    try:
+        r = smorph_scm_backward(x, w_tilde, alpha, beta, grad_out)
+        return r[1], r[2], r[3]
+    finally:
+        lib().oracle_set_abs_terms(0)
 
 
 # ----------------------------------------------------------------------------------------------

@@ -556,3 +556,40 @@ def test_reference_runner_agrees_with_the_oracle(merge):
     assert np.array_equal(got["out"], O.smorph_forward(m, x, wt, alpha))
     for k, want in zip(("grad_input", "grad_weight", "grad_alpha"), O.smorph_backward(m, x, wt, alpha, g)):
         assert normwise_error(got[k], want) <= 1e-6, k
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_smorph_term_magnitudes(dtype):
+    """The oracle's sums of the weight, alpha and beta terms' magnitudes (the scale of the GPU tests'
+    measure for sums that cancel): equal to the gradient where every term has one sign (a 1x2 element with alpha > 0
+    and a positive output gradient: each pixel's terms pg (v - ref)(v - out) are 0 and positive), at least
+    the gradient's magnitude otherwise, unchanged by the gradient's sign, linear in its scale, summed over
+    the pairs for a shared alpha, and with the normal backward unchanged afterwards."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((2, 3, 6, 9)).astype(dtype)
+    w = (rng.standard_normal((2, 3, 1, 2)) * 0.3).astype(dtype)
+    alpha = rng.uniform(0.5, 3.0, (2, 3)).astype(dtype)
+    gpos = np.abs(rng.standard_normal((2, 2, 6, 9))).astype(dtype)
+    tol = 1e-6 if dtype == np.float32 else 1e-12
+    assert normwise_error(O.smorph_term_magnitudes(O.ADD, x, w, alpha, gpos)[1], O.smorph_backward(O.ADD, x, w, alpha, gpos)[2]) <= tol
+    g = rng.standard_normal((2, 2, 6, 9)).astype(dtype)
+    before = O.smorph_backward(O.AVERAGE, x, w, alpha, g)
+    for merge in (O.ADD, O.AVERAGE, O.MAX, O.MIN):
+        grads = O.smorph_backward(merge, x, w, alpha, g)[1:]
+        mags = O.smorph_term_magnitudes(merge, x, w, alpha, g)
+        for grad, mag, mag_neg, mag2 in zip(grads, mags, O.smorph_term_magnitudes(merge, x, w, alpha, -g),
+                                            O.smorph_term_magnitudes(merge, x, w, alpha, 2 * g)):
+            assert np.all(mag >= np.abs(grad) * (1 - tol)), merge
+            assert np.array_equal(mag_neg, mag), merge
+            assert normwise_error(mag2, 2 * mag) <= tol, merge
+    shared = np.asarray(alpha[0, 0])
+    per_pair = O.smorph_term_magnitudes(O.ADD, x, w, np.full((2, 3), shared, dtype), g)[1]
+    assert abs(float(O.smorph_term_magnitudes(O.ADD, x, w, shared, g)[1]) - float(per_pair.sum(dtype=np.float64))) <= tol * float(per_pair.sum())
+    after = O.smorph_backward(O.AVERAGE, x, w, alpha, g)
+    assert all(np.array_equal(p, q) for p, q in zip(before, after))
+    beta = rng.standard_normal(2).astype(dtype)
+    ga, gb = O.smorph_scm_backward(x, w, alpha, beta, g)[2:]
+    mw, ma, mb = O.smorph_scm_term_magnitudes(x, w, alpha, beta, g)
+    gw = O.smorph_scm_backward(x, w, alpha, beta, g)[1]
+    assert np.all(mw >= np.abs(gw) * (1 - tol)) and np.all(ma >= np.abs(ga) * (1 - tol)) and np.all(mb >= np.abs(gb) * (1 - tol))
+    assert np.array_equal(O.smorph_scm_term_magnitudes(x, w, alpha, beta, -g)[2], mb)
