@@ -8,7 +8,9 @@ gradient within 1e-6 (float32) / 1e-12 (float64) norm-wise (a shared alpha's gra
 pairs that can cancel, relative to the sum of its terms' magnitudes, as is any weight, alpha or beta
 gradient whose terms cancel so far that it misses the norm-wise measure). The sweep exercises the launch plans
 (tilings, workspace layouts, saved-statistics slots, small-grid shapes) on shapes no hand-written
-case picks.
+case picks. Two more families: elements beyond the compiled static sizes, up to 51x51 (the generic
+kernels, two-byte pair taps past 256 taps, the large-element smorph backwards), and IDENTITY 3x3 / 5x5
+planes whose width is a multiple of 8 (the row-band kernels, partial last bands).
 """
 import numpy as np
 import pytest
@@ -78,8 +80,71 @@ def _check(got, want, dtype, what):
     assert err <= TOL[dtype], f"{what}: {err}"
 
 
+# Elements beyond the compiled static sizes, up to 51x51 (the generic kernels; more than 256 taps
+# saves two-byte pair taps), on small planes and channel counts.
+LARGE = [(13, 13), (15, 15), (9, 17), (17, 9), (21, 21), (25, 25), (31, 31), (35, 35), (41, 41), (51, 51), (12, 12), (1, 31)]
+
+
+def _large_geometry(rng, dtypes):
+    KH, KW = LARGE[int(rng.integers(0, len(LARGE)))]
+    big = KH * KW > 700
+    hmax, wmax, cmax = (40, 48, 3) if big else (70, 90, 5)
+    return dict(B=int(rng.integers(1, 3)), Cin=int(rng.integers(1, cmax + 1)), Cout=int(rng.integers(1, cmax + 1)),
+                H=int(rng.integers(1, hmax)), W=int(rng.integers(1, wmax)), KH=KH, KW=KW,
+                dtype=dtypes[int(rng.integers(0, len(dtypes)))], seed=int(rng.integers(0, 1 << 30)))
+
+
+def _morpho_large_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        c = _large_geometry(rng, (torch.float32, torch.float64, torch.float16, torch.bfloat16))
+        c.update(op=int(rng.integers(0, 2)), merge=MERGES[int(rng.integers(0, 5))], padding=PADDINGS[int(rng.integers(0, 4))],
+                 pv=float(rng.normal()), save=bool(rng.integers(0, 2)))
+        if c["merge"] == "identity":
+            c["Cout"] = c["Cin"]
+        yield c
+
+
+def _smorph_large_cases(n, seed, merges):
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        c = _large_geometry(rng, (torch.float32, torch.float64))
+        c.update(merge=merges[int(rng.integers(0, len(merges)))], shared=bool(rng.integers(0, 2)),
+                 alpha_scale=float(rng.choice([0.0, 1.0, 5.0, 20.0])), save=bool(rng.integers(0, 2)))
+        if c["merge"] == "identity":
+            c["Cout"] = c["Cin"]
+        yield c
+
+
+def _band_cases(n, seed):
+    """IDENTITY 3x3 / 5x5 on planes whose width is a multiple of 8: the row-band kernels' shapes (any
+    height, so partial last bands; every padding and dtype)."""
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        K = 3 if rng.integers(0, 2) == 0 else 5
+        C = int(rng.integers(1, 11))
+        yield dict(B=int(rng.integers(1, 4)), Cin=C, Cout=C, H=int(rng.integers(1, 130)), W=8 * int(rng.integers(1, 33)), KH=K, KW=K,
+                   dtype=(torch.float32, torch.float64, torch.float16, torch.bfloat16)[int(rng.integers(0, 4))],
+                   seed=int(rng.integers(0, 1 << 30)), op=int(rng.integers(0, 2)), merge="identity",
+                   padding=PADDINGS[int(rng.integers(0, 4))], pv=float(rng.normal()), save=bool(rng.integers(0, 2)))
+
+
 @pytest.mark.parametrize("c", list(_morpho_cases(200, 7101)), ids=_ids)
 def test_morpho_sweep(c):
+    _morpho_run(c)
+
+
+@pytest.mark.parametrize("c", list(_morpho_large_cases(60, 7404)), ids=_ids)
+def test_morpho_large_element_sweep(c):
+    _morpho_run(c)
+
+
+@pytest.mark.parametrize("c", list(_band_cases(60, 7505)), ids=_ids)
+def test_morpho_band_sweep(c):
+    _morpho_run(c)
+
+
+def _morpho_run(c):
     import morphocore_amd  # noqa: F401  (registers torch.ops.morphocore)
 
     dev = torch.device("cuda")
@@ -176,6 +241,17 @@ def test_smorph_sweep(c, monkeypatch):
 @pytest.mark.parametrize("c", list(_smorph_cases(80, 7303, ["sum"])), ids=_ids)
 def test_smorph_scm_sweep(c, monkeypatch):
     _smorph_run(c, monkeypatch, scm=True)
+
+
+@pytest.mark.parametrize("c", list(_smorph_large_cases(40, 7606, MERGES)), ids=_ids)
+def test_smorph_large_element_sweep(c, monkeypatch):
+    _smorph_run(c, monkeypatch, scm=False)
+
+
+@pytest.mark.parametrize("c", list(_smorph_large_cases(12, 7707, ["sum"])), ids=_ids)
+def test_smorph_scm_large_element_sweep(c, monkeypatch):
+    _smorph_run(c, monkeypatch, scm=True)
+
 
 @pytest.mark.parametrize("save", [False, True])
 def test_smorph_max_pair_just_outside_the_winner_tolerance(save, monkeypatch):
