@@ -11,7 +11,9 @@
 //   PACKED (MAX / MIN) VALUE plus the packed (channel << 16 | tap) winner of every output pixel.
 // The winning tap of a MAX / MIN merge is found by one rescan of the winning channel (the first tap
 // equal to the winning value, which is the tap the strict scan keeps), which also restores the sign
-// of a zero result (the NaN-ignoring max does not order -0 and +0).
+// of a zero result (the NaN-ignoring max does not order -0 and +0). The static kernels of 5x5 and
+// larger elements rescan channel by channel from LDS, after sorting the workgroup's pixels by winning
+// channel; the others rescan each pixel from global memory.
 //
 // The static kernel (morpho_fwd_static) is compiled for the structuring-element sizes of the common
 // layers, holds each thread's input window in registers and double-buffers the LDS tile; the
@@ -314,6 +316,12 @@ struct StaticTile
     static constexpr int WR = RH + KH - 1;                  // window rows of one thread
 };
 
+// The PACKED winner rescan runs by channel from LDS for elements of at least this many taps and up to
+// this many input channels (a bucket start per channel in LDS); smaller elements rescan each pixel from
+// global memory, which costs fewer staging passes than it saves.
+constexpr int BUCKET_MIN_TAPS = 25;
+constexpr int BUCKET_MAX_CIN = 256;
+
 // Structuring-element values of the workgroup's OB output channels for one input channel, staged
 // with the input tile and read by every lane at the same LDS address (a broadcast).
 template <int OB, int K>
@@ -323,8 +331,16 @@ struct StaticWeights
     static constexpr int NW = (ELEMS + BLOCK - 1) / BLOCK;
 };
 
+// The channel-sorted winner rescan (bucket_rescan) is held to the channel loop's four waves per SIMD.
+template <int MODE, int MK, int OB, int RH, int K>
+constexpr bool bucket_rescan()
+{
+    return MODE == FWD_PACKED && MK != MK_IDENT && OB * RH > 1 && K >= BUCKET_MIN_TAPS;
+}
+
 template <typename ST, int OP, int MK, int KH, int KW, int OB, int RH, int MODE>
-__global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<ST> p)
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(bucket_rescan<MODE, MK, OB, RH, KH * KW>() ? 4 : 1, 8))) void
+morpho_fwd_static(const FwdParams<ST> p)
 {
     using T = compute_t<ST>;
     using Tr = OpTraits<OP, T>;
@@ -332,8 +348,13 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<ST> p
     using SW = StaticWeights<OB, KH * KW>;
     constexpr int K = S::K, COLS = S::COLS, NS = S::NS, WR = S::WR, NW = SW::NW;
     constexpr bool ident = MK == MK_IDENT;
+    constexpr bool BUCKET = bucket_rescan<MODE, MK, OB, RH, K>();
     __shared__ T tiles[2][S::ELEMS];
     __shared__ T wts[2][SW::ELEMS];
+    // Winner rescan by channel (BUCKET): bucket starts per input channel, then the workgroup's
+    // pixel-channel items sorted by winning channel (an item id, replaced by its result).
+    __shared__ int rstart[BUCKET ? BUCKET_MAX_CIN + 1 : 1];
+    __shared__ uint16_t rbucket[BUCKET ? BLOCK * OB * RH : 1];
 
     const Geom& g = p.g;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -587,6 +608,158 @@ __global__ __launch_bounds__(BLOCK) void morpho_fwd_static(const FwdParams<ST> p
         __syncthreads();
     }
 
+    if constexpr (BUCKET)
+    {
+        if (g.Cin >= 1 && g.Cin <= BUCKET_MAX_CIN)
+        {
+            // The winning tap of every output pixel, found channel by channel from LDS instead of one
+            // lane at a time from global memory (whose scattered loads, one plane per lane, bound the
+            // per-pixel rescan): the items (output channel, pixel) are sorted by winning channel, each
+            // winning channel's tile and elements are staged again, and each item's pair is scanned
+            // strictly in tap order (kh, then kw). Its first extremal tap is the first tap equal to the
+            // merged value, which is that pair's extremum; a zero result takes that tap's sign.
+            constexpr int ITEMS = OB * RH;
+            const int hw0 = h0 + wave * RH;
+            for (int c = threadIdx.x; c < g.Cin; c += BLOCK) rstart[c] = 0;
+            __syncthreads();
+            // Each item's rank in its channel's bucket, then its bucket position, kept in the upper half of
+            // its winner register (NOPOS: nothing to find, tap 0).
+            constexpr int NOPOS = 0xffff;
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                for (int r = 0; r < RH; ++r)
+                {
+                    const bool need = o0 + ob < g.Cout && hw0 + r < g.H && wc < g.W && acc[ob][r] != Tr::init();
+                    const int rank = need ? atomicAdd(&rstart[win[ob][r]], 1) : NOPOS;
+                    win[ob][r] |= (int)((unsigned)rank << 16);
+                }
+            __syncthreads();
+            // Bucket starts: an exclusive prefix over the channels' counts, in the first wave.
+            if (wave == 0)
+            {
+                constexpr int PER = BUCKET_MAX_CIN / WAVE;
+                int cnt[PER], s = 0;
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                {
+                    const int c = lane * PER + j;
+                    cnt[j] = c < g.Cin ? rstart[c] : 0;
+                    s += cnt[j];
+                }
+                int incl = s;
+#pragma unroll
+                for (int d = 1; d < WAVE; d <<= 1)
+                {
+                    const int t = __shfl_up(incl, d);
+                    if (lane >= d) incl += t;
+                }
+                int base = incl - s;
+#pragma unroll
+                for (int j = 0; j < PER; ++j)
+                {
+                    const int c = lane * PER + j;
+                    if (c < g.Cin) rstart[c] = base;
+                    base += cnt[j];
+                }
+                if (lane == WAVE - 1) rstart[g.Cin] = incl;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                for (int r = 0; r < RH; ++r)
+                    if (((unsigned)win[ob][r] >> 16) != NOPOS)
+                    {
+                        const int c = win[ob][r] & 0xffff;
+                        const int at = (int)((unsigned)win[ob][r] >> 16) + rstart[c];
+                        win[ob][r] = c | (int)((unsigned)at << 16);
+                        rbucket[at] = (uint16_t)(threadIdx.x * ITEMS + ob * RH + r);
+                    }
+            __syncthreads();
+            // The winning channels in order, each tile staged behind the previous channel's scans (as
+            // the channel loop above).
+            auto next_won = [&](int c) {
+                while (c < g.Cin && rstart[c + 1] == rstart[c]) ++c;
+                return c;
+            };
+            int c = next_won(0);
+            if (c < g.Cin)
+            {
+                load(c);
+                store(0);
+                __syncthreads();
+                int buf = 0;
+                while (c < g.Cin)
+                {
+                    const int cn = next_won(c + 1);
+                    if (cn < g.Cin) load(cn);
+                    const int e1 = rstart[c + 1];
+                    for (int e = rstart[c] + threadIdx.x; e < e1; e += BLOCK)
+                    {
+                        const int id = rbucket[e];
+                        const int t = id / ITEMS, s = id - t * ITEMS;
+                        const int ob = s / RH, r = s - ob * RH;
+                        const T* xp = &tiles[buf][((t / WAVE) * RH + r + KH - 1) * COLS + (t % WAVE) + KW - 1];
+                        const T* wp = &wts[buf][ob * K];
+                        // The first row holding the pair's extremum: each row folds to its extremum
+                        // (max3 / min3), and only a strictly better row replaces the provisional one
+                        // (a row of NaN never does; one row at a time, which keeps the channel loop's
+                        // register budget). Then the first tap of that row equal to the extremum,
+                        // whose value carries the sign of a zero.
+                        T best = Tr::init();
+                        int krow = 0;
+#pragma unroll 1
+                        for (int kh = 0; kh < KH; ++kh)
+                        {
+                            T mm = Tr::combine(xp[-kh * COLS], wp[kh * KW]);
+#pragma unroll
+                            for (int kw = 1; kw < KW; ++kw) mm = Tr::pick(mm, Tr::combine(xp[-kh * COLS - kw], wp[kh * KW + kw]));
+                            const bool up = Tr::better(mm, best);
+                            best = up ? mm : best;
+                            krow = up ? kh : krow;
+                        }
+                        int kcol = 0;
+                        T fval = best;
+#pragma unroll
+                        for (int kw = KW - 1; kw >= 0; --kw)
+                        {
+                            const T v = Tr::combine(xp[-krow * COLS - kw], wp[krow * KW + kw]);
+                            const bool eq = v == best;
+                            kcol = eq ? kw : kcol;
+                            fval = eq ? v : fval;
+                        }
+                        rbucket[e] = (uint16_t)((krow * KW + kcol) | (fval == T(0) && signbit(fval) ? 0x8000 : 0));
+                    }
+                    if (cn < g.Cin) store(buf ^ 1);
+                    __syncthreads();
+                    buf ^= 1;
+                    c = cn;
+                }
+            }
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+                for (int r = 0; r < RH; ++r)
+                {
+                    const int o = o0 + ob, h = hw0 + r;
+                    if (o >= g.Cout || h >= g.H || wc >= g.W) continue;
+                    T v = acc[ob][r];
+                    int karg = 0;
+                    const int at = (int)((unsigned)win[ob][r] >> 16);
+                    if (at != NOPOS)
+                    {
+                        const int res = rbucket[at];
+                        karg = res & 0x7fff;
+                        if (v == T(0)) v = (res & 0x8000) ? -T(0) : T(0);
+                    }
+                    const int64_t oi = ((int64_t)b * g.Cout + o) * plane + (int64_t)h * g.W + wc;
+                    p.out[oi] = (ST)v;
+                    static_cast<int32_t*>(p.idx)[oi] = (int32_t)(((win[ob][r] & 0xffff) << 16) | karg);
+                }
+            return;
+        }
+    }
     if constexpr (!ident)
     {
 #pragma unroll
