@@ -10,7 +10,9 @@ gradient whose terms cancel so far that it misses the norm-wise measure). The sw
 (tilings, workspace layouts, saved-statistics slots, small-grid shapes) on shapes no hand-written
 case picks. Two more families: elements beyond the compiled static sizes, up to 51x51 (the generic
 kernels, two-byte pair taps past 256 taps, the large-element smorph backwards), and IDENTITY 3x3 / 5x5
-planes whose width is a multiple of 8 (the row-band kernels, partial last bands).
+planes whose width is a multiple of 8 (the row-band kernels, partial last bands); and dilation / erosion on
+planes large enough for the forward's full launch shape (at least 1024 workgroups), which the other
+families' planes never reach.
 """
 import numpy as np
 import pytest
@@ -129,6 +131,27 @@ def _band_cases(n, seed):
                    padding=PADDINGS[int(rng.integers(0, 4))], pv=float(rng.normal()), save=bool(rng.integers(0, 2)))
 
 
+def _full_launch_cases(n, seed):
+    """Dilation / erosion on planes large enough that the forward takes its full launch shape (at least
+    1024 workgroups of 16 x 64 output tiles: 4 rows per wave, several output channels per workgroup),
+    which the smaller cases above never reach."""
+    rng = np.random.default_rng(seed)
+    while n > 0:
+        K = [3, 5, 7, 11][int(rng.integers(0, 4))]
+        merge = MERGES[int(rng.integers(0, 5))]
+        Cin = int(rng.integers(1, 4 if K == 11 else 6))
+        Cout = Cin if merge == "identity" else int(rng.integers(1, 9))
+        B, H, W = int(rng.integers(2, 5)), int(rng.integers(200, 330)), int(rng.integers(500, 760))
+        groups = Cout if merge == "identity" or Cout < 4 else (Cout + 3) // 4
+        if B * -(-H // 16) * -(-W // 64) * groups < 1024:
+            continue
+        n -= 1
+        yield dict(B=B, Cin=Cin, Cout=Cout, H=H, W=W, KH=K, KW=K, seed=int(rng.integers(0, 1 << 30)),
+                   dtype=(torch.float32, torch.float64, torch.float16, torch.bfloat16)[int(rng.integers(0, 4))],
+                   op=int(rng.integers(0, 2)), merge=merge, padding=PADDINGS[int(rng.integers(0, 4))], pv=float(rng.normal()),
+                   save=bool(rng.integers(0, 2)))
+
+
 @pytest.mark.parametrize("c", list(_morpho_cases(200, 7101)), ids=_ids)
 def test_morpho_sweep(c):
     _morpho_run(c)
@@ -141,6 +164,11 @@ def test_morpho_large_element_sweep(c):
 
 @pytest.mark.parametrize("c", list(_band_cases(60, 7505)), ids=_ids)
 def test_morpho_band_sweep(c):
+    _morpho_run(c)
+
+
+@pytest.mark.parametrize("c", list(_full_launch_cases(24, 7808)), ids=_ids)
+def test_morpho_full_launch_sweep(c):
     _morpho_run(c)
 
 
