@@ -599,6 +599,36 @@ def run_steps(cfg, torch, mca, dev, steps, warmup):
     return dict(ms_per_step=ms_per_step, fwd_ms=fwd_ms, bwd_ms=bwd_ms, n_out=n_out, x=x, ws=ws, dtype=dtype)
 
 
+def run_graph_steps(cfg, torch, mca, dev, steps, warmup):
+    """The same step captured once in a HIP graph (torch.cuda.graph: forward and backward, the
+    operators' launches on the capture stream) and replayed: `warmup` untimed replays, then `steps`
+    timed ones between device synchronisations. For the launch-bound configuration, where the eager
+    step's time is the host's (PyTorch's autograd and the launches), not the kernels'."""
+    x, ws, dtype = make_inputs(cfg, torch, dev)
+    step, n_out, _ = build_step(cfg, torch, mca, x, ws, dtype, dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    del graph
+    return {"workload": "the same step captured once in a HIP graph (torch.cuda.graph) and replayed", "steps": steps, "warmup": warmup,
+            "ms_per_step": ms, "value": n_out / (ms * 1e-3), "unit": "output-elements/s"}
+
+
 def step_roofline(cfg, ms_per_step, peak):
     """The whole step's algorithmic work (step_work) over the step time, against the same peak."""
     sw = step_work(cfg)
@@ -625,6 +655,9 @@ def measure(config, torch, mca, native, dev, steps, warmup):
     res["roofline_other_kernel"] = other
     res["step_roofline"] = step_roofline(cfg, ms, dom["peak"] if dom["bound"] == "valu" else
                                          (PEAK_FP64_TFLOPS if cfg["dtype"] == "f64" else PEAK_FP32_TFLOPS))
+    if step_work(cfg) is None:
+        # Launch bound: the step replayed from a HIP graph, beside the eager one.
+        res["graph_step"] = run_graph_steps(cfg, torch, mca, dev, steps, warmup)
     del x, ws
     torch.cuda.empty_cache()
     return res
@@ -693,6 +726,8 @@ def main():
         "step_roofline": m["step_roofline"],
         "cpu_baseline": None,
     }
+    if "graph_step" in m:
+        line["graph_step"] = m["graph_step"]
     if args.config == 5 and not args.no_extra:
         # The other BASELINE.json configs, each at its own default steps: configs[2] (the smorph alpha
         # sweep) and configs[3] (the HBM-bound identity layer) are the two readings of the north star's
