@@ -280,7 +280,7 @@ int pair_backward_impl(int first_op, const uint8_t* taps1, const uint8_t* taps2,
     mca::Geom g{};
     int rc = make_pair_geom(first_op, B, C, H, W, KH, KW, 0, g);
     if (rc != MCA_OK) return rc;
-    if (!taps1 || !taps2) return fail("The fused opening / closing backward needs both stages' saved taps");
+    if ((!taps1 || !taps2) && B * C * H * W > 0) return fail("The fused opening / closing backward needs both stages' saved taps");
     const size_t need = mca::morpho_pair_backward_workspace<T>(g);
     if ((rc = check_workspace(workspace_bytes, need, workspace)) != MCA_OK) return rc;
     return hip_status(mca::morpho_pair_backward<T>(first_op, taps1, taps2, grad_output, grad_input, grad_w1, grad_w2, g, workspace,
@@ -336,7 +336,7 @@ int sigma_backward_impl(int replicate, T fill_e, T fill_d, const T* input, const
     mca::Geom g{};
     int rc = make_pair_geom(mca::EROSION, B, C, H, W, KH, KW, wbs, g);
     if (rc != MCA_OK) return rc;
-    if (!tapse || !tapsd) return fail("The fused sigma_layer backward needs both operations' saved taps");
+    if ((!tapse || !tapsd) && B * C * H * W > 0) return fail("The fused sigma_layer backward needs both operations' saved taps");
     T fill{};
     if ((rc = sigma_fill<T>(replicate, fill_e, fill_d, fill)) != MCA_OK) return rc;
     if ((rc = check_workspace(workspace_bytes, mca::morpho_sigma_backward_workspace<T>(g), workspace)) != MCA_OK) return rc;

@@ -175,6 +175,20 @@ hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n
 template <typename S, typename D>
 hipError_t convert_async(const S* src, D* dst, int64_t n, hipStream_t stream);
 
+// The output of a merge over no input channel (Cin == 0, a merge other than IDENTITY): the merge's
+// start value, finalised, as the reference's merge over no channel (morpho_merge_policy.hpp:10-86):
+// lowest() for MAX, max() for MIN, 0 for ADD and 0 / 0 (NaN) for AVERAGE. The kernels, which read the
+// input channels, are not launched for it; every saved winner is then (channel 0, tap 0).
+template <typename T>
+inline T empty_merge_value(int merge)
+{
+    using C = compute_t<T>;
+    if (merge == MERGE_MAX) return (T)std::numeric_limits<C>::lowest();
+    if (merge == MERGE_MIN) return (T)std::numeric_limits<C>::max();
+    if (merge == MERGE_AVERAGE) return (T)std::numeric_limits<C>::quiet_NaN();
+    return T(0);
+}
+
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);

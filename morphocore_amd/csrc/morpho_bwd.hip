@@ -674,7 +674,7 @@ static PackedPlan plan_packed(const Geom& g)
     const int64_t gin_n = (int64_t)g.B * g.Cin * g.plane();
     s.gather = gin_n > 0 && gin_n * g.Cout * g.taps() <= PACKED_GATHER_READS;
     s.gblocks = s.gather ? (int)((gin_n + BLOCK / GATHER_SLOTS - 1) / (BLOCK / GATHER_SLOTS)) : 0;
-    int64_t nchunks = (4096 + g.Cout - 1) / g.Cout;
+    int64_t nchunks = (4096 + g.Cout - 1) / std::max(g.Cout, 1);  // (no output channel: an empty launch)
     const int64_t max_chunks = (total + BLOCK - 1) / BLOCK;
     if (nchunks > max_chunks) nchunks = max_chunks;
     if (s.gather && nchunks > REDUCE_GROUP) nchunks = REDUCE_GROUP;  // one reduction launch
@@ -745,7 +745,7 @@ static TapsPlan plan_taps(int merge, const Geom& g, bool band_ok = true)
         // Up to 8 consecutive channels per workgroup, the next channel's loads in flight behind
         // each channel's gather.
         s.gather = true;
-        s.ig = g.Cin < 8 ? g.Cin : 8;
+        s.ig = std::max(1, std::min(g.Cin, 8));
         s.nig = (g.Cin + s.ig - 1) / s.ig;
         s.oc = 1;
         s.ncopy = 32;
@@ -1048,6 +1048,7 @@ hipError_t morpho_backward(int op, int merge, bool replicate, compute_t<T> fill,
                            hipStream_t stream)
 {
     if (workspace_bytes < morpho_backward_workspace<T>(merge, indices != nullptr, g)) return hipErrorInvalidValue;
+    if (g.Cin == 0) return hipSuccess;  // grad_input and grad_weight are empty
     unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
     return op == DILATION ? backward_op<T, DILATION>(merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, ws, stream)
                           : backward_op<T, EROSION>(merge, replicate, fill, x, w, indices, grad_out, grad_in, grad_w, g, ws, stream);
@@ -1154,6 +1155,7 @@ hipError_t half_backward(int op, int merge, bool replicate, float fill, const ST
                          ST* grad_in, ST* grad_w, const Geom& g, void* workspace, size_t workspace_bytes, hipStream_t stream)
 {
     if (workspace_bytes < half_backward_workspace<ST>(merge, indices != nullptr, g)) return hipErrorInvalidValue;
+    if (g.Cin == 0) return hipSuccess;  // grad_input and grad_weight are empty
     size_t inner, gout_b, gin_b, gw_b;
     const size_t base = half_parts<ST>(merge, g, inner, gout_b, gin_b, gw_b);
     unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
@@ -1170,7 +1172,12 @@ hipError_t half_backward(int op, int merge, bool replicate, float fill, const ST
     }
     const int64_t gout_n = (int64_t)g.B * g.Cout * g.plane(), gin_n = (int64_t)g.B * g.Cin * g.plane();
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
-    if (gout_n == 0) return morpho_backward<float>(op, merge, replicate, fill, nullptr, nullptr, indices, gout, gin, gw, g, ws, inner, stream);
+    if (gout_n == 0)
+    {
+        // No output gradient: both gradients are zero.
+        if ((err = fill_async<ST>(grad_in, gin_n, ST(0), stream)) != hipSuccess) return err;
+        return fill_async<ST>(grad_w, wnumel, ST(0), stream);
+    }
     if (packed_winners(merge) || plan_taps<float>(merge, g).gather)
         return op == DILATION ? half_direct<ST, DILATION>(merge, indices, grad_out, grad_in, grad_w, g, ws, gw, stream)
                               : half_direct<ST, EROSION>(merge, indices, grad_out, grad_in, grad_w, g, ws, gw, stream);

@@ -697,6 +697,13 @@ hipError_t morpho_pair_backward(int first_op, const uint8_t* taps1, const uint8_
 {
     if (!morpho_pair_supported(g)) return hipErrorInvalidValue;
     if (workspace_bytes < morpho_pair_backward_workspace<T>(g)) return hipErrorInvalidValue;
+    if ((int64_t)g.B * g.Cout * g.plane() == 0)
+    {
+        // No output (and no input) pixel: both elements' gradients are zero.
+        const int64_t nw = (int64_t)g.Cout * g.taps();
+        const hipError_t e = fill_async<T>(grad_w1, nw, T(0), stream);
+        return e != hipSuccess ? e : fill_async<T>(grad_w2, nw, T(0), stream);
+    }
     const Geom s = pair_stage_geom(g);
     const int second_op = first_op == DILATION ? EROSION : DILATION;
     unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -925,6 +925,13 @@ hipError_t morpho_forward(int op, int merge, bool replicate, compute_t<ST> fill,
                           const Geom& g, hipStream_t stream)
 {
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return hipSuccess;
+    if (g.Cin == 0 && merge != MERGE_IDENTITY)
+    {
+        const int64_t n = (int64_t)g.B * g.Cout * g.plane();
+        hipError_t err = fill_async<ST>(out, n, empty_merge_value<ST>(merge), stream);
+        if (err == hipSuccess && indices && packed_winners(merge)) err = fill_async<int32_t>(static_cast<int32_t*>(indices), n, 0, stream);
+        return err;
+    }
     FwdParams<ST> p{};
     p.x = x;
     p.w = w;

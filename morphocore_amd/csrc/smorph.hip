@@ -24,6 +24,8 @@
 // to an LDS copy of the tile's grad_input, to lane-striped LDS bins of grad_weight and to the
 // pair's grad_alpha (sum of p_k (v_k - ref)(v_k - out) g); the bins become this workgroup's partial
 // slot, summed over slots in a fixed order afterwards.
+#include <algorithm>
+
 #include "smorph_common.hpp"
 
 namespace mca
@@ -506,14 +508,14 @@ static SmorphBwdPlan plan_smorph_bwd(int merge, const Geom& g, bool saved = fals
     }
     s.t = make_tiling(g, rh);
     s.npairs = merge == MERGE_IDENTITY ? g.Cout : g.Cout * g.Cin;
-    const int64_t units = (int64_t)g.B * g.Cin;
+    const int64_t units = std::max<int64_t>(1, (int64_t)g.B * g.Cin);  // (an empty problem: one strip)
     const int ntiles = s.t.ntiles();
     int64_t nstrips = ((stat ? 8192 : 2048) + units - 1) / units;
     if (nstrips > ntiles) nstrips = ntiles;
     if (nstrips < 1) nstrips = 1;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     while (nstrips > 1 && (size_t)g.B * nstrips * (wnumel + s.npairs) * sizeof(T) > ((size_t)256 << 20)) nstrips = (nstrips + 1) / 2;
-    s.tps = (int)((ntiles + nstrips - 1) / nstrips);
+    s.tps = std::max(1, (int)((ntiles + nstrips - 1) / nstrips));
     s.nstrips = (int)((ntiles + s.tps - 1) / s.tps);
     const size_t nslots = (size_t)g.B * s.nstrips;
     s.part_w_bytes = nslots * wnumel * sizeof(T);
@@ -628,6 +630,8 @@ hipError_t smorph_forward(int merge, const T* x, const T* w, const T* alpha, T* 
 {
     if (stats && !smorph_static_supported<T>(g)) return hipErrorInvalidValue;
     if ((int64_t)g.B * g.Cout * g.plane() == 0) return hipSuccess;
+    if (g.Cin == 0)
+        return fill_async<T>(out, (int64_t)g.B * g.Cout * g.plane(), empty_merge_value<T>(merge), stream);  // no channel pairs
     SmorphFwdParams<T> p{};
     p.x = x;
     p.w = w;
@@ -664,7 +668,7 @@ hipError_t smorph_backward(int merge, const T* x, const T* w, const T* alpha, co
     if (workspace_bytes < smorph_plan_workspace<T>(s, g)) return hipErrorInvalidValue;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
-    if ((int64_t)g.B * g.Cout * g.plane() == 0)
+    if ((int64_t)g.B * g.Cout * g.plane() == 0 || g.Cin == 0)
     {
         if ((err = fill_async<T>(grad_w, wnumel, T(0), stream)) != hipSuccess) return err;
         return fill_async<T>(grad_alpha, s.npairs, T(0), stream);
@@ -851,7 +855,7 @@ hipError_t smorph_scm_backward(const T* x, const T* w, const T* alpha, const T* 
     if (workspace_bytes < smorph_plan_workspace<T>(s, g)) return hipErrorInvalidValue;
     const int64_t wnumel = (int64_t)g.Cout * g.Cw * g.taps();
     if ((err = fill_async<T>(grad_in, (int64_t)g.B * g.Cin * g.plane(), T(0), stream)) != hipSuccess) return err;
-    if ((int64_t)g.B * g.Cout * g.plane() == 0)
+    if ((int64_t)g.B * g.Cout * g.plane() == 0 || g.Cin == 0)
     {
         if ((err = fill_async<T>(grad_w, wnumel, T(0), stream)) != hipSuccess) return err;
         if ((err = fill_async<T>(grad_alpha, s.npairs, T(0), stream)) != hipSuccess) return err;

@@ -755,7 +755,8 @@ public:
         const Tensor w = w4.contiguous();
         const Geom g = geom_of(x, w);
         const Tensor ap = pair_alphas(alpha, merge, g.Cin, g.Cout);
-        if (needs_grad && g.B * g.Cout * g.H * g.W > 0)
+        // (No channel pair or no output: nothing for the kernels to do, and no workspace.)
+        if (needs_grad && g.B * g.Cout * g.Cin * g.H * g.W > 0)
         {
             const size_t ws = x.scalar_type() == c10::kFloat
                                   ? mca_smorph_backward_workspace_size_f32((int)merge, g.B, g.Cin, g.Cout, g.Cw, g.H, g.W, g.KH, g.KW)

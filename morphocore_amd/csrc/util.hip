@@ -173,6 +173,9 @@ template hipError_t round_async<_Float16>(const double*, _Float16*, int64_t, hip
 template hipError_t round_async<__bf16>(const double*, __bf16*, int64_t, hipStream_t);
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);
 template hipError_t fill_async<double>(double*, int64_t, double, hipStream_t);
+template hipError_t fill_async<_Float16>(_Float16*, int64_t, _Float16, hipStream_t);
+template hipError_t fill_async<__bf16>(__bf16*, int64_t, __bf16, hipStream_t);
+template hipError_t fill_async<int32_t>(int32_t*, int64_t, int32_t, hipStream_t);
 template size_t reduce_slots_scratch<float>(int, int64_t);
 template size_t reduce_slots_scratch<double>(int, int64_t);
 template hipError_t reduce_slots_async<float>(const float*, int, int64_t, float*, float*, hipStream_t);

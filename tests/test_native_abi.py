@@ -261,3 +261,36 @@ def test_smorph_backward_takes_large_elements(merge):
     assert lib.mca_smorph_backward_workspace_size_f64(merge, B, C, C, cw, H, W, K, K) > 0
     assert lib.mca_smorph_scm_backward_workspace_size_f32(B, C, C, C, H, W, K, K) > 0
     assert lib.mca_smorph_scm_backward_workspace_size_f64(B, C, C, C, H, W, K, K) > 0
+
+
+def test_size_queries_with_empty_dimensions():
+    """Every workspace and buffer size query answers for an empty batch, image height or width and for
+    no input or output channel (none divides by an empty dimension: an empty smorph batch once stopped
+    the process with a division by zero), and the byte counts of empty results are 0."""
+    lib = _native.lib()
+    base = dict(B=2, Cin=3, Cout=4, H=16, W=16)
+    cases = [(), ("B",), ("Cin",), ("Cout",), ("H",), ("W",), ("B", "Cin"), ("H", "W"), ("Cin", "Cout")]
+    for zero in cases:
+        d = dict(base, **{z: 0 for z in zero})
+        for K in (3, 7, 11, 31):
+            for merge in (0, 1, 2, 3, 5):
+                cin = d["Cin"]
+                cout = cin if merge == 5 else d["Cout"]
+                cw = 1 if merge == 5 else cin
+                g = (d["B"], cin, cout, cw, d["H"], d["W"], K, K)
+                lib.mca_morpho_indices_bytes(merge, *g)
+                for sfx in ("f32", "f64", "f16", "bf16"):
+                    for has_idx in (0, 1):
+                        getattr(lib, f"mca_morpho_backward_workspace_size_{sfx}")(merge, has_idx, *g)
+                for sfx in ("f32", "f64"):
+                    getattr(lib, f"mca_smorph_backward_workspace_size_{sfx}")(merge, *g)
+                stats = lib.mca_smorph_stats_bytes_f32(merge, *g)
+                if d["B"] * cout * cin * d["H"] * d["W"] == 0:
+                    assert stats == 0
+            g = (d["B"], d["Cin"], d["Cout"], d["Cin"], d["H"], d["W"], K, K)
+            for sfx in ("f32", "f64"):
+                getattr(lib, f"mca_smorph_scm_forward_workspace_size_{sfx}")(*g)
+                getattr(lib, f"mca_smorph_scm_backward_workspace_size_{sfx}")(*g)
+                getattr(lib, f"mca_morpho_pair_backward_workspace_size_{sfx}")(d["B"], d["Cin"], d["H"], d["W"], K, K)
+                getattr(lib, f"mca_morpho_sigma_backward_workspace_size_{sfx}")(d["B"], d["Cin"], d["H"], d["W"], K, K)
+            lib.mca_smorph_scm_stats_bytes_f32(*g)
