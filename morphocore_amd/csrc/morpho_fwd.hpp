@@ -103,8 +103,9 @@ __device__ __forceinline__ void merge_pair(T bv, int i, T& acc, int& win)
 
 // Finalises and stores one output pixel; for MAX / MIN / IDENTITY rescans the winning channel when
 // its tap is needed (PACKED) or when the result is zero (sign of the first zero tap). The merged
-// value is the winning channel's extremum (or the merge's clamp, lowest() / max(), which only a
-// channel 0 of all -inf / +inf taps leaves, whose tap is 0), so it is the value to look for.
+// value is the winning channel's extremum, so it is the value to look for, unless it is the merge's
+// clamp (lowest() / max()): then channel 0 won without a strictly better channel after it, and its
+// extremum may lie beyond the clamp (an infinite tap), so that extremum is recomputed and looked for.
 template <typename ST, int OP, int MK, int MODE>
 __device__ __forceinline__ void store_output(const FwdParams<ST>& p, int b, int o, int h, int wc, int i_count, compute_t<ST> acc, int win)
 {
@@ -126,7 +127,23 @@ __device__ __forceinline__ void store_output(const FwdParams<ST>& p, int b, int 
             const ST* __restrict__ wp = p.w + (int64_t)b * g.wbs + ((int64_t)o * g.Cw + (MK == MK_IDENT ? 0 : c)) * K;
             const ST* __restrict__ xp = p.x + ((int64_t)b * g.Cin + c) * g.plane();
             int karg = 0;
-            if (acc != Tr::init())
+            T target = acc;
+            if constexpr (MK == MK_MAX || MK == MK_MIN)
+            {
+                if (acc == merge_init<T, MK>())
+                {
+                    target = Tr::init();
+                    for (int kh = 0; kh < g.KH; ++kh)
+                        for (int kw = 0; kw < g.KW; ++kw)
+                        {
+                            const int y = h + ph - kh, x = wc + pw - kw;
+                            const T raw = (T)xp[(int64_t)clampi(y, 0, g.H - 1) * g.W + clampi(x, 0, g.W - 1)];
+                            const bool inb = y >= 0 && y < g.H && x >= 0 && x < g.W;
+                            target = Tr::pick(target, Tr::combine(inb || p.replicate ? raw : p.fill, (T)wp[kh * g.KW + kw]));
+                        }
+                }
+            }
+            if (target != Tr::init())
             {
                 // Taps in chunks of 4 whose loads are all in flight together (the rescan is a chain of
                 // dependent global loads otherwise); the first equal tap of the first chunk holding
@@ -158,7 +175,7 @@ __device__ __forceinline__ void store_output(const FwdParams<ST>& p, int b, int 
 #pragma unroll
                     for (int j = CH - 1; j >= 0; --j)
                     {
-                        const bool hit = k0 + j < K && val[j] == acc;
+                        const bool hit = k0 + j < K && val[j] == target;
                         found = hit ? k0 + j : found;
                         fval = hit ? val[j] : fval;
                     }
@@ -729,7 +746,9 @@ morpho_fwd_static(const FwdParams<ST> p)
                             kcol = eq ? kw : kcol;
                             fval = eq ? v : fval;
                         }
-                        rbucket[e] = (uint16_t)((krow * KW + kcol) | (fval == T(0) && signbit(fval) ? 0x8000 : 0));
+                        // A pair that never improves on the start value keeps tap 0.
+                        const int tap = best == Tr::init() ? 0 : krow * KW + kcol;
+                        rbucket[e] = (uint16_t)(tap | (fval == T(0) && signbit(fval) ? 0x8000 : 0));
                     }
                     if (cn < g.Cin) store(buf ^ 1);
                     __syncthreads();

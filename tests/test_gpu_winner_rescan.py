@@ -111,3 +111,21 @@ def test_rescan_channel_limit(Cin, merge):
     print(f"rescan Cin {Cin} {merge}", flush=True)
     x, w = _inputs("quant", 1, Cin, 4, 512, 2048, 5, 4000 + Cin)
     _check(O.DILATION, merge, "geodesic", 0.0, x, w, torch.float32, region=(40, 100))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", ["dilation min +inf", "erosion max -inf", "dilation max -inf", "erosion min +inf"])
+def test_rescan_infinite_border(case, dtype):
+    """An infinite constant border at the full launch shape. Beyond the merge's clamp (a 'min' of
+    dilations reading +inf, a 'max' of erosions reading -inf), every channel's extremum is that infinity,
+    the merge stays at max() / lowest() and channel 0 wins with its first tap reading the border. At the
+    op's start value (the inputs all -inf / +inf with NaN among them), no tap improves on it and the
+    winner is channel 0, tap 0, whatever the NaN taps."""
+    name, merge, pv = case.split()
+    op = O.DILATION if name == "dilation" else O.EROSION
+    print(f"rescan infinite border {case} {dtype}", flush=True)
+    x, w = _inputs("special", 4, 3, 6, 250, 600, 5, 5000)
+    if (name, merge) in (("dilation", "max"), ("erosion", "min")):
+        g = torch.Generator().manual_seed(5001)
+        x = torch.where(torch.rand(x.shape, generator=g) < 0.3, float("nan"), float(pv))
+    _check(op, merge, "constant", float(pv), x, w, dtype)
