@@ -24,7 +24,8 @@ and VALU instruction counts come from the committed rocprofv3 counter summaries.
 (the reference's own CPU extension, or the C oracle, on a bounded sample on the host cores, in a child
 process).
 
---config 1..5 are BASELINE.json's configs[0..4]. --config 6 and 7 are workloads of the fused
+--config 1..5 are BASELINE.json's configs[0..4]; --config 10 is configs[4]'s step with its three layers as
+one morpho_stack operator (the default run also times it, under "stack_fused_step"). --config 6 and 7 are workloads of the fused
 compositions at configs[3]'s float64 shape, per-channel merges and one 3x3 element: the opening
 (nn.Opening's default form) and sigma_layer, each as one fused operator; their lines also carry the
 same step run as the reference's composition of operators ("composition_step"). --config 8 is
@@ -81,6 +82,9 @@ CONFIGS = {
             w=(64, 64, 7, 7), x_dist=("randn", 0.0, 1.0), w_std=0.1, bound="valu", sample=dict(x=(1, 64, 64, 64)),
             key="smorph_scm_f32"),
 }
+# configs[4]'s stack as one operator (functional.morpho_stack: the layers run batch chunk by batch
+# chunk by the native stack executor); its kernels are configs[4]'s.
+CONFIGS[10] = dict(CONFIGS[5], name=CONFIGS[5]["name"] + ", as one morpho_stack operator", fused=True, key="configs[4]")
 
 # Bench dtypes: torch dtype and bytes per element.
 DTYPES = {"f64": ("float64", 8), "f32": ("float32", 4), "f16": ("float16", 2), "bf16": ("bfloat16", 2)}
@@ -123,7 +127,8 @@ def parse():
 # Default timed and warmup steps per config: about a tenth of a second to two seconds of timed work,
 # after enough warmup (~20 ms or one step of GPU work) for the clocks to settle; a 10-step run of a
 # millisecond-scale config reads ~8% high (configs[1]: 1.00 against 0.93 ms per step).
-DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20), 8: (200, 20), 9: (2, 1)}
+DEFAULT_STEPS = {1: (500, 50), 2: (100, 20), 3: (3, 1), 4: (200, 20), 5: (2, 1), 6: (200, 20), 7: (200, 20), 8: (200, 20), 9: (2, 1),
+                 10: (2, 1)}
 
 
 def taps(cfg, x_shape=None):
@@ -171,10 +176,15 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
     elif cfg["kind"] == "stack":
         alpha = torch.full((Cout, Cin), 5.0, dtype=dtype, device=dev, requires_grad=True)
 
-        def fwd():
-            y = F.dilation(xr, wr[0], "max", "replicate")
-            y = F.smorph(y, wr[1], alpha, channel_merge_mode="sum")
-            return [F.erosion(y, wr[2], "min", "replicate")]
+        if cfg.get("fused"):
+            def fwd():
+                return [F.morpho_stack(xr, [("dilation", wr[0], "max", "replicate"), ("smorph", wr[1], alpha, "sum"),
+                                            ("erosion", wr[2], "min", "replicate")])]
+        else:
+            def fwd():
+                y = F.dilation(xr, wr[0], "max", "replicate")
+                y = F.smorph(y, wr[1], alpha, channel_merge_mode="sum")
+                return [F.erosion(y, wr[2], "min", "replicate")]
 
         phases = [(fwd, lambda outs: torch.autograd.backward(outs, [grad]))]
         n_out = 3 * B * Cout * H * W
@@ -736,6 +746,14 @@ def main():
             s, w = DEFAULT_STEPS[c]
             line[f"configs{c - 1}_step"] = measure(c, torch, mca, _native, dev, s, w)
         line["target"] = target_summary(line)
+        # The same step with the three layers as one morpho_stack operator.
+        torch.cuda.empty_cache()
+        rs = run_steps(CONFIGS[10], torch, mca, dev, args.steps, args.warmup)
+        line["stack_fused_step"] = {"workload": CONFIGS[10]["name"], "steps": args.steps, "warmup": args.warmup,
+                                    "ms_per_step": rs["ms_per_step"], "fwd_ms": rs["fwd_ms"], "bwd_ms": rs["bwd_ms"],
+                                    "value": rs["n_out"] / (rs["ms_per_step"] * 1e-3), "unit": "output-elements/s"}
+        del rs
+        torch.cuda.empty_cache()
     if cfg["kind"] in ("pair", "sigma") and not args.no_extra:
         # The same step as the reference writes it: separate operator calls, intermediates in HBM.
         torch.cuda.empty_cache()

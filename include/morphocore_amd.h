@@ -319,6 +319,68 @@ int mca_morpho_sigma_backward_f64(int replicate, double fill_erosion, double fil
                                   double* grad_w_dilation, double* grad_terms, int64_t B, int64_t C, int64_t H, int64_t W, int64_t KH,
                                   int64_t KW, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Layer stacks: a chain of dilation / erosion / smorph layers (configs such as dilation -> smorph ->
+ * erosion) run forward and backward by one call each, batch chunk by batch chunk. Replaces the
+ * reference's layer-by-layer composition of operator calls (morphocore/functional/dilation.py:89-91,
+ * smorph.py:72-75, erosion.py:89-91, each a separate MorphoOperation / Smorph autograd node,
+ * morpho_op_wrap.hxx:24-211, smorph.cpp:13-104). Each chunk of `chunk` batch elements goes through every
+ * layer before the next chunk starts, and the backward keeps only one chunk of each intermediate
+ * gradient (two chunk-sized buffers for the whole chain) instead of whole-batch tensors. Values and winners are
+ * those of the separate entry points for the same layers; weight and alpha gradients are the chunks'
+ * partial gradients summed in chunk order (in double, rounded once), within the tolerance of the
+ * separate backward's.
+ *
+ * Layer l reads C_l channels (C_0 = the input's C) and writes out_channels = C_{l+1}; weight is
+ * [out_channels, weight_channels, kh, kw] as the single-layer entry points take it (an erosion's
+ * element already flipped, as functional/erosion.py passes it; a smorph's the blended w~), alpha one
+ * value per pair (index o * C_l + i; [C_l] for IDENTITY). merge: MAX, MIN, ADD, AVERAGE, IDENTITY.
+ * replicate / fill: the dilation's / erosion's border, as in mca_morpho_forward. save: keep what the
+ * backward can reuse — a dilation's / erosion's winners (packed for MAX / MIN, per pair otherwise;
+ * not kept when mca_morpho_forward could not save them), a float32 smorph's pair statistics (when
+ * mca_smorph_stats_bytes_f32 has them for the layer); otherwise the backward recomputes. grad_weight
+ * and grad_alpha are the backward's outputs for the layer (NULL: not wanted). */
+#define MCA_STACK_DILATION 0
+#define MCA_STACK_EROSION 1
+#define MCA_STACK_SMORPH 2
+
+typedef struct mca_stack_layer
+{
+    int kind;  /* MCA_STACK_DILATION, MCA_STACK_EROSION or MCA_STACK_SMORPH */
+    int merge;
+    int replicate;
+    int save;
+    double fill;
+    int64_t out_channels, weight_channels, kh, kw;
+    const void* weight;
+    const void* alpha; /* smorph only */
+    void* grad_weight;
+    void* grad_alpha; /* smorph only */
+} mca_stack_layer;
+
+/* Validates the chain and sizes its buffers: *saved_bytes for what the forward keeps for the
+ * backward (the activations between layers, the saved winners and statistics), *backward_bytes for the
+ * backward's own workspace. chunk: batch elements per chunk, 0 = the whole batch (the fastest for
+ * instruction-bound layers; smaller chunks bound the backward's intermediate gradient memory). The same
+ * (layers, n, shape, chunk) must be passed to the forward and the backward. */
+int mca_stack_plan_f32(const mca_stack_layer* layers, int n, int64_t B, int64_t C, int64_t H, int64_t W, int64_t chunk, size_t* saved_bytes,
+                       size_t* backward_bytes);
+int mca_stack_plan_f64(const mca_stack_layer* layers, int n, int64_t B, int64_t C, int64_t H, int64_t W, int64_t chunk, size_t* saved_bytes,
+                       size_t* backward_bytes);
+/* Forward of the chain: input [B, C, H, W] to output [B, C_n, H, W]; `saved` (saved_bytes) receives
+ * the state the backward reads. */
+int mca_stack_forward_f32(const mca_stack_layer* layers, int n, const float* input, float* output, int64_t B, int64_t C, int64_t H,
+                          int64_t W, int64_t chunk, void* saved, size_t saved_bytes, void* stream);
+int mca_stack_forward_f64(const mca_stack_layer* layers, int n, const double* input, double* output, int64_t B, int64_t C, int64_t H,
+                          int64_t W, int64_t chunk, void* saved, size_t saved_bytes, void* stream);
+/* Backward of the chain from the forward's input, output and saved state: grad_input [B, C, H, W]
+ * (NULL: not wanted) and every layer's grad_weight / grad_alpha, all overwritten. */
+int mca_stack_backward_f32(const mca_stack_layer* layers, int n, const float* input, const float* output, const float* grad_output,
+                           float* grad_input, int64_t B, int64_t C, int64_t H, int64_t W, int64_t chunk, const void* saved,
+                           size_t saved_bytes, void* workspace, size_t workspace_bytes, void* stream);
+int mca_stack_backward_f64(const mca_stack_layer* layers, int n, const double* input, const double* output, const double* grad_output,
+                           double* grad_input, int64_t B, int64_t C, int64_t H, int64_t W, int64_t chunk, const void* saved,
+                           size_t saved_bytes, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Test probe, no reference counterpart: y[j] = the exponential every smorph kernel evaluates, applied
  * to x[j] (n values, device pointers). It restates the reference's vector exponential
  * (morphocore/functional/csrc/cpp/morpho_cpu_simd.hpp:127-169) for the arguments the kernels pass,

@@ -67,11 +67,25 @@ EXPORTS = (
     "mca_morpho_sigma_backward_workspace_size_f64",
     "mca_morpho_sigma_backward_f32",
     "mca_morpho_sigma_backward_f64",
+    "mca_stack_plan_f32",
+    "mca_stack_plan_f64",
+    "mca_stack_forward_f32",
+    "mca_stack_forward_f64",
+    "mca_stack_backward_f32",
+    "mca_stack_backward_f64",
     "mca_probe_smorph_exp_f32",
     "mca_probe_smorph_exp_f64",
 )
 
 _lib = None
+
+
+class StackLayer(ctypes.Structure):
+    """mca_stack_layer: one layer of a stack (kind 0 dilation, 1 erosion, 2 smorph)."""
+    _fields_ = [("kind", ctypes.c_int), ("merge", ctypes.c_int), ("replicate", ctypes.c_int), ("save", ctypes.c_int),
+                ("fill", ctypes.c_double), ("out_channels", ctypes.c_int64), ("weight_channels", ctypes.c_int64),
+                ("kh", ctypes.c_int64), ("kw", ctypes.c_int64), ("weight", ctypes.c_void_p), ("alpha", ctypes.c_void_p),
+                ("grad_weight", ctypes.c_void_p), ("grad_alpha", ctypes.c_void_p)]
 
 _I, _I64, _P, _SZ = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
 _GEOM = [_I64] * 8
@@ -176,6 +190,17 @@ def lib() -> ctypes.CDLL:
     so.mca_smorph_scm_forward_stats_f32.restype = _I
     so.mca_smorph_scm_backward_stats_f32.argtypes = [_P] * 12 + _GEOM + [_P, _SZ, _P]
     so.mca_smorph_scm_backward_stats_f32.restype = _I
+    _SHAPE = [_I64] * 5  # B, C, H, W, chunk
+    for sfx in ("f32", "f64"):
+        f = getattr(so, f"mca_stack_plan_{sfx}")
+        f.argtypes = [_P, _I] + _SHAPE + [_P, _P]
+        f.restype = _I
+        f = getattr(so, f"mca_stack_forward_{sfx}")
+        f.argtypes = [_P, _I, _P, _P] + _SHAPE + [_P, _SZ, _P]
+        f.restype = _I
+        f = getattr(so, f"mca_stack_backward_{sfx}")
+        f.argtypes = [_P, _I, _P, _P, _P, _P] + _SHAPE + [_P, _SZ, _P, _SZ, _P]
+        f.restype = _I
     _lib = so
     return so
 
@@ -378,3 +403,37 @@ def morpho_sigma_backward(replicate, fill_erosion, fill_dilation, x, w_erosion, 
 def probe_smorph_exp(x, y):
     """y = the smorph kernels' exponential of x, elementwise (C ABI mca_probe_smorph_exp_*; tests)."""
     _check(getattr(lib(), f"mca_probe_smorph_exp_{_sfx(x)}")(_ptr(x), _ptr(y), x.numel(), _stream(x)))
+
+
+def stack_layers(specs):
+    """A ctypes array of mca_stack_layer from dicts with the fields of StackLayer (tensors for weight,
+    alpha, grad_weight, grad_alpha; missing fields 0 / NULL)."""
+    arr = (StackLayer * len(specs))()
+    for a, spec in zip(arr, specs):
+        for k, v in spec.items():
+            setattr(a, k, v.data_ptr() if isinstance(v, torch.Tensor) else v)
+        w = spec["weight"]
+        a.out_channels, a.weight_channels, a.kh, a.kw = w.shape
+    return arr
+
+
+def stack_plan(layers, dtype, shape, chunk=0):
+    """(saved bytes, backward workspace bytes) of a stack (C ABI mca_stack_plan_*); shape = (B, C, H, W)."""
+    saved, backward = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    f = getattr(lib(), "mca_stack_plan_f64" if dtype == torch.float64 else "mca_stack_plan_f32")
+    _check(f(ctypes.cast(layers, _P), len(layers), *shape, chunk, ctypes.byref(saved), ctypes.byref(backward)))
+    return saved.value, backward.value
+
+
+def stack_forward(layers, x, out, saved, chunk=0):
+    """Enqueue a stack's forward (C ABI mca_stack_forward_*) into `out`, its saved state into `saved`."""
+    f = getattr(lib(), f"mca_stack_forward_{_sfx(x)}")
+    _check(f(ctypes.cast(layers, _P), len(layers), _ptr(x), _ptr(out), *x.shape, chunk, _ptr(saved), saved.numel(), _stream(x)))
+
+
+def stack_backward(layers, x, out, grad_out, grad_in, saved, workspace, chunk=0):
+    """Enqueue a stack's backward (C ABI mca_stack_backward_*): grad_in (or None) and the layers'
+    grad_weight / grad_alpha buffers."""
+    f = getattr(lib(), f"mca_stack_backward_{_sfx(x)}")
+    _check(f(ctypes.cast(layers, _P), len(layers), _ptr(x), _ptr(out), _ptr(grad_out), _ptr(grad_in), *x.shape, chunk, _ptr(saved),
+             saved.numel(), _ptr(workspace), workspace.numel(), _stream(x)))

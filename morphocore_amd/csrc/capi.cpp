@@ -362,6 +362,13 @@ int noalloc_scratch(int device, void** out)
 
 }  // namespace
 
+namespace mca
+{
+// Error reporting of the entry points, for the other translation units of the C ABI (stack.cpp).
+int api_fail(const char* msg) { return fail(msg); }
+int api_hip_status(hipError_t err) { return hip_status(err); }
+}  // namespace mca
+
 extern "C" {
 
 const char* mca_version(void) { return "0.13.1-mi355x"; }

@@ -189,11 +189,20 @@ inline T empty_merge_value(int merge)
     return T(0);
 }
 
+// Records `msg` as the calling thread's last error (mca_last_error) and returns MCA_ERR_INVALID
+// (capi.cpp).
+int api_fail(const char* msg);
+// MCA_OK for hipSuccess; otherwise records the HIP error's text and returns MCA_ERR_HIP (capi.cpp).
+int api_hip_status(hipError_t err);
+
 // Shared helpers (util.hip).
 template <typename T>
 hipError_t fill_async(T* p, int64_t n, T v, hipStream_t stream);
 template <typename T>
 hipError_t round_async(const double* src, T* dst, int64_t n, hipStream_t stream);
+// acc[j] = (first ? 0 : acc[j]) + part[j], in double.
+template <typename T>
+hipError_t accumulate_async(double* acc, const T* part, int64_t n, bool first, hipStream_t stream);
 
 // Slots summed per group by the first stage of a long reduction.
 constexpr int REDUCE_GROUP = 32;

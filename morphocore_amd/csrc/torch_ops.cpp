@@ -987,6 +987,256 @@ Tensor smorph_scm(const Tensor& input, const Tensor& weight, const Tensor& alpha
     return output_to_original(SmorphScmFunction::apply(x4, w4, alpha, beta, needs_grad), input_dims);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Layer stacks: a chain of dilation / erosion / smorph layers as one operator and one autograd node,
+// run by the C ABI's stack executor batch chunk by batch chunk (mca_stack_*). No reference counterpart:
+// the reference chains one operator call and one autograd node per layer in Python
+// (functional/dilation.py:89-91, functional/smorph.py:72-75, functional/erosion.py:89-91).
+// ------------------------------------------------------------------------------------------------
+
+constexpr int64_t STACK_SMORPH = MCA_STACK_SMORPH;
+
+// The C ABI's layer descriptors: weights as each operator receives them, per-pair alphas (one tensor
+// per smorph layer, in order), the save flag of each layer.
+std::vector<mca_stack_layer> stack_layers(const std::vector<int64_t>& kinds, const std::vector<int64_t>& merges,
+                                          const std::vector<int64_t>& paddings, const std::vector<double>& values,
+                                          const std::vector<int64_t>& save, const std::vector<Tensor>& weights, const std::vector<Tensor>& aps)
+{
+    std::vector<mca_stack_layer> layers(kinds.size());
+    size_t a = 0;
+    for (size_t l = 0; l < kinds.size(); ++l)
+    {
+        mca_stack_layer& L = layers[l];
+        const Tensor& w = weights[l];
+        L.kind = (int)kinds[l];
+        L.merge = (int)merges[l];
+        L.replicate = kinds[l] != STACK_SMORPH && paddings[l] == REPLICATE;
+        L.save = (int)save[l];
+        L.fill = kinds[l] != STACK_SMORPH ? fill_value(kinds[l], paddings[l], values[l]) : 0.0;
+        L.out_channels = w.size(0);
+        L.weight_channels = w.size(1);
+        L.kh = w.size(2);
+        L.kw = w.size(3);
+        L.weight = w.data_ptr();
+        L.alpha = kinds[l] == STACK_SMORPH ? aps[a++].data_ptr() : nullptr;
+        L.grad_weight = nullptr;
+        L.grad_alpha = nullptr;
+    }
+    return layers;
+}
+
+int stack_plan(bool f32, const std::vector<mca_stack_layer>& layers, const Tensor& x, int64_t chunk, size_t* saved, size_t* backward)
+{
+    return (f32 ? mca_stack_plan_f32 : mca_stack_plan_f64)(layers.data(), (int)layers.size(), x.size(0), x.size(1), x.size(2), x.size(3), chunk,
+                                                          saved, backward);
+}
+
+class StackFunction : public torch::autograd::Function<StackFunction>
+{
+public:
+    // params: the n layers' weights, then the smorph layers' alphas.
+    static Tensor forward(AutogradContext* ctx, const Tensor& x4, at::TensorList params, std::vector<int64_t> kinds, std::vector<int64_t> merges,
+                          std::vector<int64_t> paddings, std::vector<double> values, bool save_indices, int64_t chunk, bool needs_grad,
+                          bool input_grad)
+    {
+        const c10::DeviceGuard guard(x4.device());
+        const Tensor x = x4.contiguous();
+        const size_t n = kinds.size();
+        const bool f32 = x.scalar_type() == c10::kFloat;
+        std::vector<Tensor> weights, alphas, aps;
+        int64_t cin = x.size(1);
+        for (size_t l = 0, a = n; l < n; ++l)
+        {
+            weights.push_back(params[l].contiguous());
+            if (kinds[l] == STACK_SMORPH)
+            {
+                alphas.push_back(params[a++]);
+                aps.push_back(pair_alphas(alphas.back(), merges[l], cin, weights[l].size(0)));
+            }
+            cin = weights[l].size(0);
+        }
+        // What the backward may reuse: winners (per-pair taps within MORPHOCORE_AMD_SAVED_TAPS_LIMIT), and
+        // float32 smorph statistics when the saved-statistics budget admits the whole saved state.
+        std::vector<int64_t> save(n, 0);
+        bool any_stats = false;
+        cin = x.size(1);
+        for (size_t l = 0; l < n; ++l)
+        {
+            const Tensor& w = weights[l];
+            if (save_indices && needs_grad)
+            {
+                if (kinds[l] == STACK_SMORPH)
+                {
+                    save[l] = f32;
+                    any_stats = any_stats || f32;
+                }
+                else
+                {
+                    const int64_t nbytes =
+                        (int64_t)mca_morpho_indices_bytes((int)merges[l], x.size(0), cin, w.size(0), w.size(1), x.size(2), x.size(3), w.size(2), w.size(3));
+                    save[l] = (merges[l] == MAX || merges[l] == MIN) || nbytes <= env_bytes("MORPHOCORE_AMD_SAVED_TAPS_LIMIT", int64_t(8) << 30);
+                }
+            }
+            cin = w.size(0);
+        }
+        std::vector<mca_stack_layer> layers = stack_layers(kinds, merges, paddings, values, save, weights, aps);
+        size_t saved_bytes = 0, backward_bytes = 0;
+        check_rc(stack_plan(f32, layers, x, chunk, &saved_bytes, &backward_bytes));
+        if (needs_grad && backward_bytes == 0 && x.numel() > 0)
+            TORCH_CHECK(false, "Structuring element too large for the smorph backward kernels' shared memory; run the stack without gradients");
+        Tensor saved;
+        if (any_stats) saved = SavedStats::get().allocate((int64_t)saved_bytes, x.options());
+        if (!saved.defined())
+        {
+            if (any_stats)
+            {
+                for (size_t l = 0; l < n; ++l)
+                    if (kinds[l] == STACK_SMORPH) save[l] = 0;
+                layers = stack_layers(kinds, merges, paddings, values, save, weights, aps);
+                check_rc(stack_plan(f32, layers, x, chunk, &saved_bytes, &backward_bytes));
+            }
+            saved = byte_buffer((int64_t)saved_bytes, x);
+        }
+        Tensor out = torch::empty({x.size(0), weights.back().size(0), x.size(2), x.size(3)}, x.options());
+        if (f32)
+            check_rc(mca_stack_forward_f32(layers.data(), (int)n, x.data_ptr<float>(), out.data_ptr<float>(), x.size(0), x.size(1), x.size(2),
+                                           x.size(3), chunk, saved.data_ptr(), (size_t)saved.nbytes(), stream_of(x)));
+        else
+            check_rc(mca_stack_forward_f64(layers.data(), (int)n, x.data_ptr<double>(), out.data_ptr<double>(), x.size(0), x.size(1), x.size(2),
+                                           x.size(3), chunk, saved.data_ptr(), (size_t)saved.nbytes(), stream_of(x)));
+        std::vector<Tensor> keep = {x, out, saved};
+        keep.insert(keep.end(), weights.begin(), weights.end());
+        keep.insert(keep.end(), alphas.begin(), alphas.end());
+        keep.insert(keep.end(), aps.begin(), aps.end());
+        ctx->save_for_backward(keep);
+        ctx->saved_data["kinds"] = kinds;
+        ctx->saved_data["merges"] = merges;
+        ctx->saved_data["paddings"] = paddings;
+        ctx->saved_data["values"] = values;
+        ctx->saved_data["save"] = save;
+        ctx->saved_data["chunk"] = chunk;
+        ctx->saved_data["input_grad"] = input_grad;
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grad_outputs)
+    {
+        const auto saved = ctx->get_saved_variables();
+        const std::vector<int64_t> kinds = ctx->saved_data["kinds"].toIntVector();
+        const std::vector<int64_t> merges = ctx->saved_data["merges"].toIntVector();
+        const std::vector<int64_t> paddings = ctx->saved_data["paddings"].toIntVector();
+        const std::vector<double> values = ctx->saved_data["values"].toDoubleVector();
+        const std::vector<int64_t> save = ctx->saved_data["save"].toIntVector();
+        const int64_t chunk = ctx->saved_data["chunk"].toInt();
+        const bool input_grad = ctx->saved_data["input_grad"].toBool();
+        const size_t n = kinds.size();
+        const size_t m = (saved.size() - 3 - n) / 2;
+        const Tensor& x = saved[0];
+        const Tensor& out = saved[1];
+        const Tensor& state = saved[2];
+        const std::vector<Tensor> weights(saved.begin() + 3, saved.begin() + 3 + n);
+        const std::vector<Tensor> alphas(saved.begin() + 3 + n, saved.begin() + 3 + n + m);
+        const std::vector<Tensor> aps(saved.begin() + 3 + n + m, saved.end());
+        const Tensor grad_output = grad_outputs[0].contiguous();
+        TORCH_CHECK(grad_output.sizes() == out.sizes(), "grad_output shape mismatch: expected [", out.sizes(), "] but got [", grad_output.sizes(),
+                    "]");
+        TORCH_CHECK(grad_output.device() == x.device(), "grad_output must be on the same device as input");
+        TORCH_CHECK(grad_output.scalar_type() == x.scalar_type(), "grad_output must have the same dtype as input");
+        const c10::DeviceGuard guard(x.device());
+        const bool f32 = x.scalar_type() == c10::kFloat;
+        std::vector<mca_stack_layer> layers = stack_layers(kinds, merges, paddings, values, save, weights, aps);
+        std::vector<Tensor> grad_w, grad_pairs;
+        for (size_t l = 0, a = 0; l < n; ++l)
+        {
+            grad_w.push_back(torch::empty_like(weights[l]));
+            layers[l].grad_weight = grad_w.back().data_ptr();
+            if (kinds[l] == STACK_SMORPH)
+            {
+                grad_pairs.push_back(torch::empty_like(aps[a++]));
+                layers[l].grad_alpha = grad_pairs.back().data_ptr();
+            }
+        }
+        size_t saved_bytes = 0, backward_bytes = 0;
+        check_rc(stack_plan(f32, layers, x, chunk, &saved_bytes, &backward_bytes));
+        Tensor ws = byte_buffer((int64_t)backward_bytes, x);
+        Tensor grad_input = input_grad ? torch::empty_like(x) : Tensor();
+        if (f32)
+            check_rc(mca_stack_backward_f32(layers.data(), (int)n, x.data_ptr<float>(), out.data_ptr<float>(), grad_output.data_ptr<float>(),
+                                            input_grad ? grad_input.data_ptr<float>() : nullptr, x.size(0), x.size(1), x.size(2), x.size(3),
+                                            chunk, state.data_ptr(), (size_t)state.nbytes(), ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        else
+            check_rc(mca_stack_backward_f64(layers.data(), (int)n, x.data_ptr<double>(), out.data_ptr<double>(), grad_output.data_ptr<double>(),
+                                            input_grad ? grad_input.data_ptr<double>() : nullptr, x.size(0), x.size(1), x.size(2), x.size(3),
+                                            chunk, state.data_ptr(), (size_t)state.nbytes(), ws.data_ptr(), (size_t)ws.numel(), stream_of(x)));
+        tensor_list grads = {grad_input};
+        grads.insert(grads.end(), grad_w.begin(), grad_w.end());
+        for (size_t a = 0; a < m; ++a) grads.push_back(alpha_grad(alphas[a], grad_pairs[a]));
+        for (int k = 0; k < 8; ++k) grads.push_back(Tensor());  // kinds .. input_grad
+        return grads;
+    }
+};
+
+// morpho_stack(input, weights, alphas, kinds, merges, paddings, padding_values, save_indices, chunk):
+// layer l is kinds[l] (0 dilation, 1 erosion, 2 smorph) with weights[l] as that operator receives it
+// (an erosion's element flipped, a smorph's blended w~), merges[l], and for dilation / erosion the
+// padding paddings[l] / padding_values[l]; alphas holds one alpha per smorph layer, in order (any shape
+// the smorph operator takes). Each layer's checks are the single operator's.
+Tensor morpho_stack(const Tensor& input, at::TensorList weights, at::TensorList alphas, at::IntArrayRef kinds, at::IntArrayRef merges,
+                    at::IntArrayRef paddings, at::ArrayRef<double> padding_values, bool save_indices, int64_t chunk)
+{
+    const size_t n = kinds.size();
+    TORCH_CHECK(n >= 1, "morpho_stack needs at least one layer");
+    TORCH_CHECK(weights.size() == n && merges.size() == n && paddings.size() == n && padding_values.size() == n,
+                "morpho_stack: weights, kinds, merges, paddings and padding_values must have one entry per layer");
+    TORCH_CHECK(chunk >= 0, "chunk must be non negative");
+    const int64_t input_dims = input.dim();
+    const Tensor x4 = input_to_4d(input);
+    TORCH_CHECK(x4.dim() == 4, "Input must be a 4d tensor (batch_size, in_channels, height, width)");
+    std::vector<Tensor> params;
+    std::vector<int64_t> kv(kinds.begin(), kinds.end()), mv, pv(n, 0);
+    bool needs_grad = input.requires_grad();
+    size_t a = 0;
+    int64_t cin = x4.size(1);
+    for (size_t l = 0; l < n; ++l)
+    {
+        TORCH_CHECK(kinds[l] == DILATION || kinds[l] == EROSION || kinds[l] == STACK_SMORPH, "Unknown layer kind ", kinds[l], " at layer ", l);
+        const int64_t merge = to_merge(merges[l]);
+        TORCH_CHECK(merge != SMOOTH, "Unsupported merge operation");
+        mv.push_back(merge);
+        if (kinds[l] != STACK_SMORPH) pv[l] = to_padding(paddings[l]);
+        const Tensor w4 = weight_to_4d(weights[l]);
+        TORCH_CHECK(w4.dim() == 4, "Weight must be a 4d tensor (out_channels, in_channels, kernel_height, kernel_width)");
+        if (merge == IDENTITY)
+        {
+            TORCH_CHECK(w4.size(0) == cin, "Identity mode requires weight.shape[0] == input.shape[1]");
+            TORCH_CHECK(w4.size(1) == 1, "Identity mode requires weight.shape[1] == 1");
+        }
+        else
+        {
+            TORCH_CHECK(w4.size(1) == cin, "Input channels must match weight input channels");
+        }
+        check_device("morpho_stack_forward_hip", x4, {w4});
+        params.push_back(w4);
+        needs_grad = needs_grad || weights[l].requires_grad();
+        if (kinds[l] == STACK_SMORPH)
+        {
+            TORCH_CHECK(a < alphas.size(), "morpho_stack: one alpha per smorph layer");
+            pair_alphas(alphas[a], merge, cin, w4.size(0));
+            check_device("morpho_stack_forward_hip", x4, {alphas[a]});
+            needs_grad = needs_grad || alphas[a].requires_grad();
+            ++a;
+        }
+        cin = w4.size(0);
+    }
+    TORCH_CHECK(a == alphas.size(), "morpho_stack: one alpha per smorph layer");
+    params.insert(params.end(), alphas.begin(), alphas.end());
+    needs_grad = needs_grad && torch::GradMode::is_enabled();
+    std::vector<double> vv(padding_values.begin(), padding_values.end());
+    const Tensor out = StackFunction::apply(x4, at::TensorList(params), kv, mv, pv, vv, save_indices, chunk, needs_grad,
+                                            needs_grad && input.requires_grad());
+    return output_to_original(out, input_dims);
+}
+
 // Module-level helpers for tests and the benchmark (no reference counterpart).
 PyObject* py_saved_stats_live_bytes(PyObject*, PyObject* args)
 {
@@ -1047,6 +1297,9 @@ TORCH_LIBRARY(morphocore, m)
     // No reference counterpart: the fused form of the reference's Python sigma_layer, 'identity' merge.
     m.def("sigma_identity(Tensor input, Tensor w_erosion, Tensor w_dilation, Tensor soft, int padding, float padding_value=0., "
           "bool save_indices=True, float noise_scale=0.) -> Tensor");
+    // No reference counterpart: a chain of dilation / erosion / smorph layers as one operator.
+    m.def("morpho_stack(Tensor input, Tensor[] weights, Tensor[] alphas, int[] kinds, int[] merges, int[] paddings, "
+          "float[] padding_values, bool save_indices=True, int chunk=0) -> Tensor");
 }
 
 // CompositeImplicitAutograd, as the reference (bindings.cpp:142-148): the kernels run above autograd
@@ -1059,6 +1312,7 @@ TORCH_LIBRARY_IMPL(morphocore, CompositeImplicitAutograd, m)
     m.impl("smorph_scm", &smorph_scm);
     m.impl("opening_closing", &opening_closing);
     m.impl("sigma_identity", &sigma_identity);
+    m.impl("morpho_stack", &morpho_stack);
 }
 
 // Importing morphocore_amd._C loads this library, which runs the registrations above.

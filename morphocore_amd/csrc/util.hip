@@ -60,6 +60,15 @@ __global__ __launch_bounds__(BLOCK) void round_kernel(const double* __restrict__
     for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK) dst[j] = (T)src[j];
 }
 
+// acc[j] = (first ? 0 : acc[j]) + part[j] in double: partial sums added in call order, rounded once by
+// round_async (or read as double) at the end.
+template <typename T>
+__global__ __launch_bounds__(BLOCK) void accumulate_kernel(double* __restrict__ acc, const T* __restrict__ part, int64_t n, int first)
+{
+    for (int64_t j = (int64_t)blockIdx.x * BLOCK + threadIdx.x; j < n; j += (int64_t)gridDim.x * BLOCK)
+        acc[j] = (first ? 0.0 : acc[j]) + (double)part[j];
+}
+
 // Per-sample structuring elements of weight noise: out[b][j] = w[j] + (u[b][j] * 2 - 1) * scale, with
 // the roundings of the four elementwise operations torch evaluates it with (morpho_op_wrap.hxx:55-64),
 // in their order, so that the elements are bit for bit the ones the composed expression gives.
@@ -146,6 +155,14 @@ hipError_t round_async(const double* src, T* dst, int64_t n, hipStream_t stream)
 }
 
 template <typename T>
+hipError_t accumulate_async(double* acc, const T* part, int64_t n, bool first, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    accumulate_kernel<T><<<grid_for(n), BLOCK, 0, stream>>>(acc, part, n, first ? 1 : 0);
+    return hipGetLastError();
+}
+
+template <typename T>
 hipError_t noise_sample_async(const T* w, const T* u, T scale, T* out, int64_t n, int64_t batch, hipStream_t stream)
 {
     const int64_t total = n * batch;
@@ -169,6 +186,9 @@ template hipError_t convert_async<float, __bf16>(const float*, __bf16*, int64_t,
 template hipError_t noise_sample_async<float>(const float*, const float*, float, float*, int64_t, int64_t, hipStream_t);
 template hipError_t noise_sample_async<double>(const double*, const double*, double, double*, int64_t, int64_t, hipStream_t);
 template hipError_t round_async<float>(const double*, float*, int64_t, hipStream_t);
+template hipError_t round_async<double>(const double*, double*, int64_t, hipStream_t);
+template hipError_t accumulate_async<float>(double*, const float*, int64_t, bool, hipStream_t);
+template hipError_t accumulate_async<double>(double*, const double*, int64_t, bool, hipStream_t);
 template hipError_t round_async<_Float16>(const double*, _Float16*, int64_t, hipStream_t);
 template hipError_t round_async<__bf16>(const double*, __bf16*, int64_t, hipStream_t);
 template hipError_t fill_async<float>(float*, int64_t, float, hipStream_t);

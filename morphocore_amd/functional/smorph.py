@@ -4,6 +4,20 @@ from ._ops import ops
 from .merge_enum import str_to_merge
 
 
+def w_tilde(w: torch.Tensor, alpha: torch.Tensor, channel_merge_mode: str = "sum") -> torch.Tensor:
+    """The element the smorph operator receives: w blended with its flip by tanh(alpha), per pair,
+    w~ = tanh(a) * ((1 - tanh(a)) / 2 * flip(w) + (1 + tanh(a)) / 2 * w), in torch operations so that
+    autograd carries w~'s gradient back to w and alpha (morphocore/functional/smorph.py:56-70)."""
+    if channel_merge_mode == 'identity' or alpha.dim() == 1:
+        tanh_alpha = torch.tanh(alpha).view(-1, 1, 1, 1)
+    else:
+        tanh_alpha = torch.tanh(alpha).unsqueeze(-1).unsqueeze(-1)
+
+    term1 = (1 + tanh_alpha) / 2
+    term2 = (1 - tanh_alpha) / 2
+    return tanh_alpha * (term2 * w.flip(dims=(-2, -1)) + term1 * w)
+
+
 def smorph(x: torch.Tensor, w: torch.Tensor, alpha: torch.Tensor, beta: torch.Tensor = None,
            channel_merge_mode: str = "sum") -> torch.Tensor:
     """Smooth morphology: an alpha-softmax over each window, dilation-like for alpha -> +inf and
@@ -26,15 +40,7 @@ def smorph(x: torch.Tensor, w: torch.Tensor, alpha: torch.Tensor, beta: torch.Te
         min-like for beta < 0, their mean at 0); ``channel_merge_mode`` is then ignored.
     channel_merge_mode : 'sum', 'mean', 'max', 'min' or 'identity'.
     """
-    if channel_merge_mode == 'identity' or alpha.dim() == 1:
-        tanh_alpha = torch.tanh(alpha).view(-1, 1, 1, 1)
-    else:
-        tanh_alpha = torch.tanh(alpha).unsqueeze(-1).unsqueeze(-1)
-
-    term1 = (1 + tanh_alpha) / 2
-    term2 = (1 - tanh_alpha) / 2
-    w_tilde_alpha = tanh_alpha * (term2 * w.flip(dims=(-2, -1)) + term1 * w)
-
+    w_tilde_alpha = w_tilde(w, alpha, channel_merge_mode)
     if beta is not None:
         return ops.smorph_scm(x, w_tilde_alpha, alpha, beta)
     return ops.smorph(x, w_tilde_alpha, alpha, str_to_merge(channel_merge_mode))

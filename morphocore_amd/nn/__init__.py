@@ -5,7 +5,8 @@ from .opening import Opening
 from .closing import Closing
 from .sigma_layer import SigmaLayer
 from .smorph import SMorph
+from .stack import MorphoStack
 from .morpho_module import MorphoModule
 from .alpha_module import AlphaModule
 
-__all__ = ['Dilation', 'Erosion', 'Opening', 'Closing', 'SigmaLayer', 'SMorph', 'MorphoModule', 'AlphaModule']
+__all__ = ['Dilation', 'Erosion', 'Opening', 'Closing', 'SigmaLayer', 'SMorph', 'MorphoStack', 'MorphoModule', 'AlphaModule']

@@ -30,7 +30,7 @@ OBJDIR = os.path.join(CSRC, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ROCM_INCLUDE = "/opt/rocm/include"
 
-KERNEL_SOURCES = ["morpho_fwd.hip", "morpho_fwd_half.hip", "morpho_bwd.hip", "morpho_ident.hip", "morpho_fused.hip", "smorph.hip", "smorph_static.hip", "util.hip", "capi.cpp"]
+KERNEL_SOURCES = ["morpho_fwd.hip", "morpho_fwd_half.hip", "morpho_bwd.hip", "morpho_ident.hip", "morpho_fused.hip", "smorph.hip", "smorph_static.hip", "util.hip", "capi.cpp", "stack.cpp"]
 KERNEL_HEADERS = ["common.hpp", "launch.hpp", "morpho_fwd.hpp", "smorph_common.hpp", os.path.join("..", "..", "include", "morphocore_amd.h")]
 # Packed FP32 instructions stay disabled: only scalar fp32 VALU forms are emitted.
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
