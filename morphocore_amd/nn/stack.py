@@ -2,6 +2,7 @@ import torch
 import torch.nn as nn
 
 from ..functional import morpho_stack
+from ._plain import calls_forward_plainly
 from .dilation import Dilation
 from .erosion import Erosion
 from .smorph import SMorph
@@ -15,8 +16,9 @@ class MorphoStack(nn.Module):
     ``MorphoStack(*layers, chunk=0)``: the layers are ordinary ``Dilation``, ``Erosion`` and ``SMorph``
     modules (registered as ``layers``, so their parameters and state_dict entries are the layers' own).
     The forward pass gives the values of calling the layers in turn. A layer that a stack does not take
-    (weight dropout or weight noise in training, SMorph's SMOOTH merge with ``beta``) makes the forward
-    call the layers one by one instead.
+    (weight dropout or weight noise in training, SMorph's SMOOTH merge with ``beta``), or one whose call
+    would run more than its class's forward (a hook, a subclass or an instance override of ``forward``),
+    makes the forward call the layers one by one instead.
     """
 
     def __init__(self, *layers: nn.Module, chunk: int = 0):
@@ -31,6 +33,8 @@ class MorphoStack(nn.Module):
 
     def _stackable(self) -> bool:
         for layer in self.layers:
+            if not any(calls_forward_plainly(layer, cls) for cls in (Dilation, Erosion, SMorph)):
+                return False
             if isinstance(layer, SMorph):
                 if layer.beta is not None:
                     return False

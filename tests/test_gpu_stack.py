@@ -254,6 +254,18 @@ def test_nn_morpho_stack_runs_layers_for_dropout():
     assert torch.equal(a, b)
 
 
+def test_nn_morpho_stack_calls_layers_with_hooks():
+    """A forward hook on a layer runs: the stack then calls the layers in turn (same values)."""
+    mods = _modules(torch.float32)
+    seen = []
+    handle = mods[1].register_forward_hook(lambda m, i, o: seen.append(o.shape))
+    x = seeded(903, 2, 3, 16, 30, kind="randn").to(DEV)
+    out = mca.nn.MorphoStack(*mods)(x)
+    handle.remove()
+    assert seen == [torch.Size([2, 4, 16, 30])]
+    assert torch.equal(out, torch.nn.Sequential(*mods)(x))
+
+
 def test_stack_rejects_bad_chains():
     x = torch.randn(2, 3, 8, 8, device=DEV)
     w = torch.randn(4, 2, 3, 3, device=DEV)

@@ -100,3 +100,26 @@ def test_element_too_large_for_the_smorph_backward():
     """The forward still plans; the backward workspace is 0 (no backward for this element)."""
     saved, backward = _plan([_layer(2, 2, 2, 2, 101)], (1, 2, 128, 128))
     assert saved == 0 and backward == 0
+
+
+def test_stack_layer_specs_and_module_checks():
+    """The Python layers of the stack check their arguments before any device work."""
+    import morphocore_amd as mca
+
+    w = torch.zeros(2, 2, 3, 3)
+    with pytest.raises(ValueError, match="Unknown layer kind"):
+        mca.functional.morpho_stack(torch.zeros(1, 2, 4, 4), [("opening", w)])
+    with pytest.raises(ValueError, match="A smorph layer is"):
+        mca.functional.morpho_stack(torch.zeros(1, 2, 4, 4), [("smorph", w)])
+    with pytest.raises(ValueError, match="A dilation layer is"):
+        mca.functional.morpho_stack(torch.zeros(1, 2, 4, 4), [("dilation", w, "max", "zero", 0.0, 1)])
+    with pytest.raises(ValueError, match="Unknown merge mode"):
+        mca.functional.morpho_stack(torch.zeros(1, 2, 4, 4), [("erosion", w, "median")])
+    with pytest.raises(ValueError, match="at least one layer"):
+        mca.functional.morpho_stack(torch.zeros(1, 2, 4, 4), [])
+    with pytest.raises(TypeError, match="takes Dilation, Erosion and SMorph layers"):
+        mca.nn.MorphoStack(torch.nn.ReLU())
+    with pytest.raises(ValueError, match="at least one layer"):
+        mca.nn.MorphoStack()
+    stack = mca.nn.MorphoStack(mca.nn.Dilation(2, 3, 3), mca.nn.SMorph(3, 3, 3), chunk=2)
+    assert [n for n, _ in stack.named_parameters()] == ["layers.0.weight", "layers.1.weight", "layers.1.alpha"]
