@@ -31,6 +31,12 @@ def _warm(fn):
     torch.cuda.synchronize()
 
 
+def _STACK(x, w):
+    """dilation(max) -> smorph(sum, alpha 2) -> erosion(min), one element for the three layers."""
+    alpha = torch.full((w.shape[0], x.shape[1]), 2.0, dtype=x.dtype, device=DEV)
+    return [("dilation", w, "max", "replicate"), ("smorph", w, alpha, "sum"), ("erosion", w, "min", "replicate")]
+
+
 CASES = [
     ("dilation max 3x3", lambda x, w: F.dilation(x, w, "max", "replicate"), (4, 3, 64, 64), (16, 3, 3, 3)),
     ("erosion sum 5x5", lambda x, w: F.erosion(x, w, "sum", "geodesic"), (2, 8, 40, 96), (8, 8, 5, 5)),
@@ -38,6 +44,8 @@ CASES = [
     ("erosion min 11x11", lambda x, w: F.erosion(x, w, "min", "zero"), (2, 4, 256, 512), (8, 4, 11, 11)),
     ("smorph mean 7x7", lambda x, w: F.smorph(x, w, torch.full((w.shape[0], x.shape[1]), 1.5, device=DEV), channel_merge_mode="mean"),
      (2, 4, 40, 80), (4, 4, 7, 7)),
+    ("stack 5x5", lambda x, w: F.morpho_stack(x, _STACK(x, w)), (2, 4, 40, 80), (4, 4, 5, 5)),
+    ("stack 5x5 chunks of one", lambda x, w: F.morpho_stack(x, _STACK(x, w), chunk=1), (3, 4, 40, 80), (4, 4, 5, 5)),
 ]
 
 

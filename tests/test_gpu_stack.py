@@ -211,6 +211,28 @@ def test_stack_empty_batch_and_no_gradient_graph():
     assert out.grad_fn is None
 
 
+@pytest.mark.parametrize("shape,couts", [((2, 3, 0, 9), (4, 4)), ((2, 3, 6, 0), (4, 4)), ((2, 3, 6, 9), (0, 4)), ((2, 0, 6, 9), (4, 2))])
+@pytest.mark.parametrize("merge", ["max", "sum", "mean"])
+def test_stack_empty_planes_and_channels(shape, couts, merge):
+    """Empty planes and a layer without channels: the values of the single operators (the merge's start
+    value where a layer has no input channel) and their gradients (zero or empty)."""
+    print(f"stack empty {shape} {couts} {merge}", flush=True)
+    B, C, H, W = shape
+    x = torch.randn(shape, dtype=torch.float64)
+    ws = [torch.randn(couts[0], C, 3, 3, dtype=torch.float64), torch.randn(couts[1], couts[0], 3, 3, dtype=torch.float64)]
+    layers = [("dilation", merge, ws[0], None, O.REPLICATE, 0.0), ("erosion", merge, ws[1], None, O.GEODESIC, 0.0)]
+    out, xd, wd, _ = _stack_op(x, layers, 1)
+    ref, rx, rws, _ = _single_ops(x, layers)
+    assert out.shape == ref.shape
+    assert torch.equal(out.isnan(), ref.isnan()) and torch.equal(out.nan_to_num(), ref.nan_to_num())
+    g = torch.randn(out.shape, dtype=torch.float64, device=DEV)
+    out.backward(g)
+    ref.backward(g)
+    for a, b in [(xd, rx)] + list(zip(wd, rws)):
+        assert a.grad.shape == b.grad.shape
+        torch.testing.assert_close(a.grad, b.grad, rtol=1e-12, atol=0)
+
+
 def _modules(dtype):
     torch.manual_seed(5)
     d = mca.nn.Dilation(3, 4, 5, "max", "replicate", dtype=dtype)
