@@ -108,6 +108,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="do not also time the other configs after the default configs[4]")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--stack-chunk", type=int, default=0,
+                   help="batch elements per chunk of the morpho_stack step (--config 10 and stack_fused_step; 0: the whole batch)")
     p.add_argument("--kernel-only", nargs="?", const="forward", choices=("forward", "backward"), default=None,
                    help="launch only the step's forward (default) or backward kernel --steps times after one launch (for rocprofv3 counter runs)")
     p.add_argument("--steps-only", action="store_true", help="time the steps only, no kernel or CPU measurement (for rocprofv3 kernel traces)")
@@ -179,7 +181,7 @@ def build_step(cfg, torch, mca, x, ws, dtype, dev):
         if cfg.get("fused"):
             def fwd():
                 return [F.morpho_stack(xr, [("dilation", wr[0], "max", "replicate"), ("smorph", wr[1], alpha, "sum"),
-                                            ("erosion", wr[2], "min", "replicate")])]
+                                            ("erosion", wr[2], "min", "replicate")], chunk=cfg.get("chunk", 0))]
         else:
             def fwd():
                 y = F.dilation(xr, wr[0], "max", "replicate")
@@ -688,6 +690,7 @@ def main():
     from morphocore_amd import _native
 
     _native.lib()
+    CONFIGS[10]["chunk"] = args.stack_chunk
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -749,7 +752,7 @@ def main():
         # The same step with the three layers as one morpho_stack operator.
         torch.cuda.empty_cache()
         rs = run_steps(CONFIGS[10], torch, mca, dev, args.steps, args.warmup)
-        line["stack_fused_step"] = {"workload": CONFIGS[10]["name"], "steps": args.steps, "warmup": args.warmup,
+        line["stack_fused_step"] = {"workload": CONFIGS[10]["name"], "chunk": args.stack_chunk, "steps": args.steps, "warmup": args.warmup,
                                     "ms_per_step": rs["ms_per_step"], "fwd_ms": rs["fwd_ms"], "bwd_ms": rs["bwd_ms"],
                                     "value": rs["n_out"] / (rs["ms_per_step"] * 1e-3), "unit": "output-elements/s"}
         del rs
