@@ -123,3 +123,19 @@ def test_stack_layer_specs_and_module_checks():
         mca.nn.MorphoStack()
     stack = mca.nn.MorphoStack(mca.nn.Dilation(2, 3, 3), mca.nn.SMorph(3, 3, 3), chunk=2)
     assert [n for n, _ in stack.named_parameters()] == ["layers.0.weight", "layers.1.weight", "layers.1.alpha"]
+
+
+def test_forward_and_backward_check_their_buffers_first():
+    """Buffer sizes are checked before any launch (so these run without a GPU)."""
+    arr = _layers(C5)
+    shape = (2, 64, 32, 32)
+    saved, backward = _native.stack_plan(arr, torch.float32, shape)
+    lib = _native.lib()
+    P = ctypes.c_void_p
+    assert lib.mca_stack_forward_f32(ctypes.cast(arr, P), 3, 16, 16, *shape, 0, 16, saved - 1, None) == 1
+    assert "Saved-state buffer too small" in lib.mca_last_error().decode()
+    assert lib.mca_stack_backward_f32(ctypes.cast(arr, P), 3, 16, 16, 16, None, *shape, 0, 16, saved, 16, backward - 1, None) == 1
+    assert "Workspace too small" in lib.mca_last_error().decode()
+    big = _layers([_layer(2, 2, 2, 2, 101)])
+    assert lib.mca_stack_backward_f32(ctypes.cast(big, P), 1, 16, 16, 16, None, 1, 2, 128, 128, 0, 16, 0, 16, 1 << 20, None) == 1
+    assert "too large for the smorph backward" in lib.mca_last_error().decode()
