@@ -328,11 +328,7 @@ def test_stack_full_size_c5(chunk):
         assert err <= TOL[torch.float32], f"{name}: {err}"
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_stack_random_chains_float64(seed):
-    """Seeded random chains: 1-4 layers of random kind, merge, padding, element shape (square, rectangular
-    and even) and channel counts, random chunking, in float64 against the oracle chain: forward bit for
-    bit, gradients within 1e-12."""
+def _random_chain(seed, dtype):
     rng = np.random.default_rng(1000 + seed)
     B, C = int(rng.integers(1, 4)), int(rng.integers(1, 5))
     H, W = int(rng.integers(3, 30)), int(rng.integers(3, 50))
@@ -344,19 +340,27 @@ def test_stack_random_chains_float64(seed):
         cout = cin if merge == "identity" else int(rng.integers(1, 5))
         KH, KW = int(rng.choice([1, 2, 3, 4, 5, 7])), int(rng.choice([1, 2, 3, 5, 6]))
         cw = 1 if merge == "identity" else cin
-        w = seeded(2000 + 10 * seed + j, cout, cw, KH, KW, dtype=torch.float64, kind="randn", scale=0.3)
+        w = seeded(2000 + 10 * seed + j, cout, cw, KH, KW, dtype=dtype, kind="randn", scale=0.3)
         if kind == "smorph":
             pairs = (cout,) if merge == "identity" else (cout, cin)
-            alpha = seeded(3000 + 10 * seed + j, *pairs, dtype=torch.float64, kind="randn", scale=3.0)
+            alpha = seeded(3000 + 10 * seed + j, *pairs, dtype=dtype, kind="randn", scale=3.0)
             layers.append((kind, merge, w, alpha, 0, 0.0))
         else:
             pad = int(rng.choice([O.ZERO, O.GEODESIC, O.CONSTANT, O.REPLICATE]))
             layers.append((kind, merge, w, None, pad, float(rng.normal())))
         cin = cout
     chunk = int(rng.integers(0, B + 2))
-    print(f"stack random chain {seed}: {(B, C, H, W)} chunk {chunk} "
+    print(f"stack random chain {seed} {dtype}: {(B, C, H, W)} chunk {chunk} "
           f"{[(k, m, tuple(w.shape), p) for k, m, w, _, p, _ in layers]}", flush=True)
-    x = seeded(4000 + seed, B, C, H, W, dtype=torch.float64, kind="randn")
+    return seeded(4000 + seed, B, C, H, W, dtype=dtype, kind="randn"), layers, chunk
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_stack_random_chains_float64(seed):
+    """Seeded random chains: 1-4 layers of random kind, merge, padding, element shape (square, rectangular
+    and even) and channel counts, random chunking, in float64 against the oracle chain: forward bit for
+    bit, gradients within 1e-12."""
+    x, layers, chunk = _random_chain(seed, torch.float64)
     npl = [(k, m, w.numpy(), None if a is None else a.numpy(), p, v) for k, m, w, a, p, v in layers]
     out, xd, ws, alphas = _stack_op(x, layers, chunk)
     g = seeded(5000 + seed, *out.shape, dtype=torch.float64, kind="randn")
@@ -368,3 +372,18 @@ def test_stack_random_chains_float64(seed):
         assert normwise_error(w.grad.cpu().numpy(), gw[j]) <= TOL[torch.float64], f"layer {j} weight"
     for a, want in zip(alphas, ga):
         assert normwise_error(a.grad.cpu().numpy(), want) <= TOL[torch.float64]
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_stack_random_chains_float32(seed):
+    """The same random chains in float32 against the chain of single operators: forward bit for bit,
+    gradients within 1e-6."""
+    x, layers, chunk = _random_chain(seed, torch.float32)
+    out, xd, ws, alphas = _stack_op(x, layers, chunk)
+    ref, rx, rws, ralphas = _single_ops(x, layers)
+    _assert_bits(out.detach().cpu().numpy(), ref.detach().cpu().numpy())
+    g = seeded(6000 + seed, *out.shape, kind="randn").to(DEV)
+    out.backward(g)
+    ref.backward(g)
+    for got, want in [(xd, rx)] + list(zip(ws, rws)) + list(zip(alphas, ralphas)):
+        assert normwise_error(got.grad.cpu().numpy(), want.grad.cpu().numpy()) <= TOL[torch.float32]
